@@ -1,0 +1,199 @@
+/*
+ * mlops_mi355x.h -- C ABI of the MI355X (gfx950) block-FP8 MoE expert path.
+ *
+ * One shared library, libmlops_mi355x.so. Every entry point takes raw device
+ * pointers, sizes and a hipStream_t (passed as void* so this header needs no
+ * HIP include), enqueues its kernels on that stream and returns 0, or a
+ * negative code with a message in mi355x_last_error(). No entry point
+ * allocates device memory, synchronizes the stream or reads device memory on
+ * the host; scratch space, where needed, is a caller-provided workspace whose
+ * size the matching *_workspace_size() function returns.
+ *
+ * Layout conventions (all row-major, contiguous):
+ *   bf16      : uint16 storage of bfloat16
+ *   e4m3      : uint8 storage of OCP float8_e4m3fn
+ *   A         : routed rows = tokens * top_k, in expert-sorted order
+ *   offsets   : int32 [E+1], rows of expert e are [offsets[e], offsets[e+1])
+ *   1x128 activation scales are stored K-block major: scale[kb][row]
+ *   128x128 weight scales: scale[e][out/128][in/128] (DeepSeek layout)
+ *
+ * The reference (als244/mlops) is pure Python; each entry point below names
+ * the reference function whose behaviour it reproduces.
+ */
+#ifndef MLOPS_MI355X_H
+#define MLOPS_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI355X_OK 0
+#define MI355X_EINVAL (-1)
+#define MI355X_ELAUNCH (-2)
+
+/* Routing modes (reference: src/mlops/kernels/moe_router.py:19, :290). */
+#define MI355X_ROUTE_TOPK_THEN_SOFTMAX 0
+#define MI355X_ROUTE_SOFTMAX_THEN_TOPK 1
+#define MI355X_ROUTE_SIGMOID_NOAUX_TC 2
+
+const char* mi355x_last_error(void);
+int mi355x_abi_version(void);
+
+/* ------------------------------------------------------------ router ---- */
+
+/* Top-k selection and route weights from fp32 logits [T,E].
+ * Replaces route() / _topk_kernel / route_torch
+ * (src/mlops/kernels/moe_router.py:235-344, :106-171, :347-400).
+ * Selection is a stable descending sort: ties go to the lower expert id.
+ * bias may be NULL (sigmoid mode only). forced_ids (NULL or int32 [T,k])
+ * replaces the selection, as routing_override does (moe_router.py:272-289).
+ * weights: fp32 [T,k]; ids: int32 [T,k]. */
+int mi355x_router_topk(const float* logits, int tokens, int experts, int top_k, int mode,
+                       const float* bias, int n_group, int topk_group, float routed_scaling,
+                       const int32_t* forced_ids, float* weights, int32_t* ids, void* stream);
+
+/* Routing statistics: aux loss, probability column sums and per-segment
+ * counts. Replaces routing_statistics (src/mlops/providers/moe_common.py:32-71).
+ * segments == 1 with seg_offsets/chunk_table NULL covers all tokens;
+ * otherwise seg_offsets int32 [S+1] and chunk_table int32 [nchunks][2] =
+ * (first token, segment) of each chunk of at most 64 tokens of one segment.
+ * aux: fp32 [1]; prob_sum: fp32 [E]; seg_counts: int32 [S,E]. */
+size_t mi355x_router_stats_workspace_size(int nchunks, int experts);
+int mi355x_router_stats(const float* logits, const int32_t* ids, int tokens, int experts,
+                        int top_k, int mode, int segments, const int32_t* seg_offsets,
+                        const int32_t* chunk_table, int nchunks, float* aux, float* prob_sum,
+                        int32_t* seg_counts, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* Logit gradient from the per-sorted-row score gradient dscore [A] (gathered
+ * to [T,k] through slots), grad_aux [1] and grad_prob_sum [E] (either may be
+ * NULL = zero); expert counts are read from offsets [E+1] (permute plan).
+ * Replaces routing_gradient + route_backward +
+ * add_aux_gradient_ + add_sequence_aux_gradient_
+ * (moe_common.py:74-124, moe_router.py:403-502). grad_logits: fp32 [T,E]. */
+int mi355x_router_topk_bwd(const float* logits, const float* weights, const int32_t* ids,
+                           const float* dscore, const int32_t* slots, int tokens, int experts,
+                           int top_k, int mode, const float* grad_aux,
+                           const float* grad_prob_sum, const int32_t* offsets, int segments,
+                           const int32_t* seg_offsets, const int32_t* seg_counts,
+                           float* grad_logits, void* stream);
+
+/* ----------------------------------------------------------- permute ---- */
+
+/* Stable counting sort of the flat expert ids [A] into expert order.
+ * Replaces sort_assignments (src/mlops/kernels/moe_dispatch.py:106-119):
+ * order = argsort(ids, stable), offsets = [0, cumsum(bincount)],
+ * slots[order[i]] = i. counts: int64 [E]. */
+size_t mi355x_permute_plan_workspace_size(int assignments, int experts);
+int mi355x_permute_plan(const int32_t* ids, int assignments, int experts, int64_t* counts,
+                        int32_t* offsets, int32_t* order, int32_t* slots, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* Dispatch + quantize: token rows x bf16 [T,H] read once, written as e4m3 to
+ * each of their k routed rows slots[t,j] with one fp32 descale per 1x128
+ * block: s = max(amax * (1/448), 1e-12), q = e4m3(clip(x / s, +-448)).
+ * Replaces dispatch + quantize_rows_fp8(gather=...)
+ * (moe_dispatch.py:122-124; kernels/quack_moe/quantize_rows.py:34-60,140-207)
+ * with 1x128 instead of per-row scales. q: [A,H]; scales: [H/128][A]. */
+int mi355x_permute_quantize_fp8(const void* x, int tokens, int width, int top_k,
+                                const int32_t* slots, uint8_t* q, float* scales, void* stream);
+
+/* Row quantizer with 1x128 scales for rows already in routed order; with
+ * gate_up != 0 an interleaved [gate_0, up_0, ...] row is stored gate columns
+ * first (quantize_rows.py:63-111 gate_up=True). q: [rows,width];
+ * scales: [width/128][rows]. */
+int mi355x_quantize_rows_fp8(const void* x, int rows, int width, int64_t pitch, int gate_up,
+                             uint8_t* q, float* scales, void* stream);
+
+/* SwiGLU of the interleaved pre-activation h [rows, 2I], clamped at limit
+ * when limit > 0, quantized to e4m3 with 1x128 scales.
+ * Replaces swiglu_quantize_rows_fp8 (kernels/quack_moe/swiglu_rows.py:246-258,
+ * _swiglu_rows :50-76). q: [rows,I]; scales: [I/128][rows]. */
+int mi355x_swiglu_quantize_fp8(const void* h, int rows, int width, float limit, uint8_t* q,
+                               float* scales, void* stream);
+
+/* 128x128 block quantizer of expert weights [E,out,in] (bf16, or fp32 when
+ * is_fp32): s = max(amax / 448, 1e-12) (true division), zero-padded partial
+ * blocks. q_t (NULL or [E,in,out]) also receives the transposed e4m3 copy.
+ * Replaces quantize_blocks (src/mlops/kernels/block_fp8.py:47-93). */
+int mi355x_quantize_weight_blocks(const void* w, int is_fp32, int experts, int out, int in,
+                                  uint8_t* q, float* scale, uint8_t* q_t, void* stream);
+
+/* e4m3 [E,rows,cols] -> [E,cols,rows]: the MN-major weight operand of the
+ * input-gradient GEMMs. Stands in for the in-shared-memory tile transposer of
+ * block_fp8_transposed_gemm (kernels/quack_moe/block_fp8_gemm.py:154-195). */
+int mi355x_transpose_fp8(const uint8_t* q, int experts, int rows, int cols, uint8_t* q_t,
+                         void* stream);
+
+/* Feature-major e4m3 operand of the weight-gradient GEMM: routed rows of x
+ * (bf16, row pitch `pitch`; with gather != NULL sorted row r reads source row
+ * gather[r] / gather_div) are written transposed, [width][padded], each
+ * expert's rows starting at its 128-aligned padded offset, zero filled, with
+ * one descale per (feature, 128-row block). gate_up de-interleaves columns as
+ * in mi355x_quantize_rows_fp8. Replaces quantize_transpose_fp8
+ * (kernels/quack_moe/quantize_transpose.py:126-313) with per-128-token
+ * instead of per-expert scales. scales: [width][padded/128]. */
+size_t mi355x_wgrad_padded_rows(int assignments, int experts);
+int mi355x_quantize_transpose_fp8(const void* x, int64_t pitch, int width, const int32_t* gather,
+                                  int gather_div, int gate_up, const int32_t* offsets,
+                                  int experts, int assignments, int padded, uint8_t* qt,
+                                  float* scales, void* stream);
+
+/* out[t] = bf16(residual[t] + sum_j weights[t,j] * y[slots[t,j]]), fp32 sum in
+ * j order. Replaces combine (moe_dispatch.py:21-72, :168-196). */
+int mi355x_unpermute_combine(const void* y, const int32_t* slots, const float* weights,
+                             const void* residual, int tokens, int top_k, int width, void* out,
+                             void* stream);
+
+/* out[t] = bf16(sum_j dx[slots[t,j]]). Replaces dispatch_backward
+ * (moe_dispatch.py:136-165). */
+int mi355x_unpermute_sum(const void* dx, const int32_t* slots, int tokens, int top_k,
+                         int width, void* out, void* stream);
+
+/* Routed SwiGLU backward over sorted rows: from r = dy @ W2 [A,I] (bf16),
+ * h [A,2I] interleaved and the route score of each sorted row
+ * (weights[order[row]]): dscore = <r, act> (fp32), dh = dSwiGLU(score * r)
+ * interleaved (bf16), a' = score * act (bf16). Replaces
+ * routed_swiglu_rows_backward (kernels/quack_moe/swiglu_rows.py:101-146,
+ * :278-318). */
+int mi355x_routed_swiglu_bwd(const void* r, const void* h, const float* weights,
+                             const int32_t* order, int rows, int width, float limit, void* dh,
+                             void* a_prime, float* dscore, void* stream);
+
+/* ------------------------------------------------------------- GEMMs ---- */
+
+/* Ragged grouped block-FP8 GEMM, fp8 MFMA with fp32 accumulation:
+ *   out[r, n] = sum_kb (sum_{k in kb} a[r,k] * W[e][n,k]) * a_scale[kb][r] * ws
+ * for rows r of expert e, ws the weight block's scale, plus addend when
+ * given. w is e4m3 [E,N,K]. w_scale_t == 0: w_scale is [E,N/128,K/128] (a
+ * projection, y = x @ W^T); w_scale_t == 1: w is the transposed copy of a
+ * weight [E,K,N] and w_scale is that weight's [E,K/128,N/128] (an input
+ * gradient, dx = dy @ W). interleave != 0 writes output column n < N/2 to 2n
+ * and n >= N/2 to 2(n-N/2)+1 (gate/up interleaved h). out, addend: bf16 [M,N].
+ * Replaces grouped_block_gemm / block_fp8_gemm / block_fp8_transposed_gemm
+ * (src/mlops/kernels/block_fp8.py:120-336; kernels/quack_moe/block_fp8_gemm.py
+ * :1424-1482). */
+int mi355x_gemm_fp8_block(const uint8_t* a, const float* a_scale, int rows, const uint8_t* w,
+                          const float* w_scale, int w_scale_t, int experts, int n, int k,
+                          const int32_t* offsets, int interleave, const void* addend, void* out,
+                          void* stream);
+
+/* Grouped weight-gradient GEMM over feature-major e4m3 operands of the same
+ * padded layout (see mi355x_quantize_transpose_fp8):
+ *   out[e][m][n] = sum_{rows of e} p[m][row] q[n][row], block-scaled,
+ * fp32 accumulation, written as bf16 (out_fp32 == 0) or fp32. Experts with no
+ * rows get zeros. Replaces the varlen-K wgrad GEMMs
+ * (providers/sonicmoe/moe.py:351-365, :404-419; quack_moe/wgrad.py:30). */
+int mi355x_gemm_fp8_block_wgrad(const uint8_t* p, const float* p_scale, int m_features,
+                                const uint8_t* q, const float* q_scale, int n_features,
+                                int padded, const int32_t* offsets, int experts, void* out,
+                                int out_fp32, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLOPS_MI355X_H */

@@ -1,0 +1,125 @@
+// Shared device helpers and C-ABI error plumbing for the MI355X (gfx950) MoE
+// kernels. Everything here is written for CDNA4: 64-lane wavefronts, the OCP
+// e4m3 conversion instructions of gfx950 and its fp8 MFMA.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mlops_mi355x.h"
+
+#define MI355X_WAVE 64
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- errors
+// Host-side: a thread-local message for the last failing entry point.
+void mi355x_set_error(const char* fmt, ...);
+
+#define MI355X_REQUIRE(cond, ...)                 \
+  do {                                            \
+    if (!(cond)) {                                \
+      mi355x_set_error(__VA_ARGS__);              \
+      return MI355X_EINVAL;                       \
+    }                                             \
+  } while (0)
+
+#define MI355X_LAUNCH_CHECK()                                              \
+  do {                                                                     \
+    hipError_t _e = hipGetLastError();                                     \
+    if (_e != hipSuccess) {                                                \
+      mi355x_set_error("kernel launch failed: %s", hipGetErrorString(_e)); \
+      return MI355X_ELAUNCH;                                               \
+    }                                                                      \
+  } while (0)
+
+// ---------------------------------------------------------------- numbers
+static constexpr float kE4M3Max = 448.0f;
+// The row quantizer's descale is amax times the fp32-rounded reciprocal of
+// 448 (a multiply, not a division); the weight-block quantizer divides.
+static constexpr float kInv448 = 1.0f / 448.0f;
+static constexpr float kMinScale = 1e-12f;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) {
+  return __uint_as_float(((uint32_t)v) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (what torch's .to(bfloat16) does).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// OCP e4m3 (float8_e4m3fn) encode of two values with gfx950's converter:
+// round-to-nearest-even, matching torch's cast for finite inputs in range.
+// Returns the two bytes in the low 16 bits (lo first).
+__device__ __forceinline__ uint32_t f32x2_to_e4m3(float lo, float hi) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(lo, hi, 0, false) & 0xffffu;
+}
+
+__device__ __forceinline__ uint32_t f32x4_to_e4m3(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+__device__ __forceinline__ float e4m3_to_f32(uint32_t byte) {
+  return __builtin_amdgcn_cvt_f32_fp8((int)byte, 0);
+}
+
+// Quantize one value given its descale: IEEE division, clip to +-448.
+__device__ __forceinline__ float quant_div(float x, float scale) {
+  float q = x / scale;
+  return fminf(fmaxf(q, -kE4M3Max), kE4M3Max);
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+__device__ __forceinline__ float sigmoid_f(float g) { return 1.0f / (1.0f + __expf(-g)); }
+
+// ---------------------------------------------------------------- waves
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+// Max over aligned groups of `width` lanes (width a power of two <= 64).
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+__device__ __forceinline__ uint64_t lanes_below() {
+  int l = lane_id();
+  return l == 0 ? 0ull : (~0ull >> (64 - l));
+}
+
+// Blocks are assigned to the 8 XCDs round-robin; this renumbering gives each
+// XCD a contiguous run of logical tiles so neighbours share its L2.
+__device__ __forceinline__ int xcd_swizzle(int bid, int nblocks) {
+  const int xcds = 8;
+  if (nblocks % xcds) return bid;
+  int per = nblocks / xcds;
+  return (bid % xcds) * per + bid / xcds;
+}

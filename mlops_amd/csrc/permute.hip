@@ -1,0 +1,275 @@
+// Token permutation: the stable counting sort that groups routed rows by
+// expert, the dispatch that quantizes each token once and writes its k routed
+// copies, and the token-parallel combine / token-sum of the way back.
+#include "common.h"
+
+namespace {
+
+constexpr int kPlanChunk = 4096;  // assignments per plan block
+constexpr int kPlanThreads = 256;
+constexpr int kMaxExperts = 1024;
+
+// Pass 1: per-chunk expert histogram.
+__global__ void __launch_bounds__(kPlanThreads) plan_hist_kernel(
+    const int32_t* __restrict__ ids, int n, int experts, int32_t* __restrict__ hist) {
+  __shared__ int h[kMaxExperts];
+  for (int e = threadIdx.x; e < experts; e += blockDim.x) h[e] = 0;
+  __syncthreads();
+  const int start = blockIdx.x * kPlanChunk;
+  const int end = min(n, start + kPlanChunk);
+  for (int i = start + threadIdx.x; i < end; i += blockDim.x) atomicAdd(&h[ids[i]], 1);
+  __syncthreads();
+  for (int e = threadIdx.x; e < experts; e += blockDim.x)
+    hist[(size_t)blockIdx.x * experts + e] = h[e];
+}
+
+// Pass 2 (one block): expert totals, their exclusive scan (offsets), and each
+// chunk's starting position per expert (written over the histogram).
+__global__ void __launch_bounds__(kMaxExperts) plan_scan_kernel(
+    int32_t* __restrict__ hist, int chunks, int experts, int n, int64_t* __restrict__ counts,
+    int32_t* __restrict__ offsets) {
+  __shared__ int scan[kMaxExperts];
+  const int e = threadIdx.x;
+  int total = 0;
+  if (e < experts) {
+    for (int c = 0; c < chunks; ++c) {
+      int v = hist[(size_t)c * experts + e];
+      hist[(size_t)c * experts + e] = total;
+      total += v;
+    }
+  }
+  scan[e] = total;
+  __syncthreads();
+  for (int o = 1; o < kMaxExperts; o <<= 1) {
+    int v = e >= o ? scan[e - o] : 0;
+    __syncthreads();
+    scan[e] += v;
+    __syncthreads();
+  }
+  const int base = scan[e] - total;  // exclusive prefix
+  if (e < experts) {
+    counts[e] = total;
+    offsets[e] = base;
+    for (int c = 0; c < chunks; ++c) hist[(size_t)c * experts + e] += base;
+  }
+  if (e == 0) offsets[experts] = n;
+}
+
+// Pass 3: stable scatter. A chunk is walked in 256-element tiles in index
+// order; inside a tile, equal ids are ranked by wave (ballot match on the
+// id's bits) and by lane, so order is the stable argsort.
+__global__ void __launch_bounds__(kPlanThreads) plan_scatter_kernel(
+    const int32_t* __restrict__ ids, int n, int experts, const int32_t* __restrict__ base,
+    int32_t* __restrict__ order, int32_t* __restrict__ slots) {
+  __shared__ int running[kMaxExperts];
+  __shared__ int wave_count[kPlanThreads / 64][kMaxExperts];
+  for (int e = threadIdx.x; e < experts; e += blockDim.x) {
+    running[e] = base[(size_t)blockIdx.x * experts + e];
+#pragma unroll
+    for (int w = 0; w < kPlanThreads / 64; ++w) wave_count[w][e] = 0;
+  }
+  __syncthreads();
+  const int wave = threadIdx.x >> 6;
+  int bits = 1;
+  while ((1 << bits) < experts + 1) ++bits;
+  const int start = blockIdx.x * kPlanChunk;
+  const int end = min(n, start + kPlanChunk);
+  for (int tile = start; tile < end; tile += kPlanThreads) {
+    const int i = tile + threadIdx.x;
+    const bool valid = i < end;
+    const int e = valid ? ids[i] : experts;  // invalid lanes share a sentinel id
+    uint64_t peers = __ballot(1);
+    for (int b = 0; b < bits; ++b) {
+      uint64_t ones = __ballot((e >> b) & 1);
+      peers &= ((e >> b) & 1) ? ones : ~ones;
+    }
+    const int rank = __popcll(peers & lanes_below());
+    const bool leader = rank == 0;
+    const int cnt = __popcll(peers);
+    if (valid && leader) wave_count[wave][e] = cnt;
+    __syncthreads();
+    if (valid) {
+      int pos = running[e] + rank;
+      for (int w = 0; w < wave; ++w) pos += wave_count[w][e];
+      order[pos] = i;
+      slots[i] = pos;
+    }
+    __syncthreads();
+    if (valid && leader) {
+      atomicAdd(&running[e], cnt);
+      wave_count[wave][e] = 0;
+    }
+    __syncthreads();
+  }
+}
+
+// Dispatch + 1x128 quantization: one wave per token; lane handles 8
+// consecutive columns per 512-column step, 16 lanes make one 128 block.
+__global__ void __launch_bounds__(256) permute_quantize_kernel(
+    const uint16_t* __restrict__ x, int tokens, int width, int top_k,
+    const int32_t* __restrict__ slots, uint8_t* __restrict__ q, float* __restrict__ scales,
+    int rows) {
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= tokens) return;
+  int dest[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j)
+    if (j < top_k) dest[j] = slots[(size_t)t * top_k + j];
+  const uint16_t* src = x + (size_t)t * width;
+  for (int base = 0; base < width; base += 512) {
+    const int col = base + lane * 8;
+    const bool ok = col < width;
+    float v[8];
+    if (ok) {
+      uint4 raw = *(const uint4*)(src + col);
+      uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = bf16_to_f32(w4[i] & 0xffff);
+        v[2 * i + 1] = bf16_to_f32(w4[i] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = group_max<16>(amax);
+    const float s = fmaxf(amax * kInv448, kMinScale);
+    uint32_t lo = f32x4_to_e4m3(quant_div(v[0], s), quant_div(v[1], s), quant_div(v[2], s),
+                                quant_div(v[3], s));
+    uint32_t hi = f32x4_to_e4m3(quant_div(v[4], s), quant_div(v[5], s), quant_div(v[6], s),
+                                quant_div(v[7], s));
+    if (ok) {
+      const int kb = col >> 7;
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        if (j < top_k) {
+          *(uint2*)(q + (size_t)dest[j] * width + col) = make_uint2(lo, hi);
+          if ((lane & 15) == 0) scales[(size_t)kb * rows + dest[j]] = s;
+        }
+      }
+    }
+  }
+}
+
+// out[t] = residual[t] + sum_j w[t,j] * y[slot[t,j]] (fp32, j order), one
+// block per token, 8 columns per thread.
+__global__ void __launch_bounds__(256) combine_kernel(
+    const uint16_t* __restrict__ y, const int32_t* __restrict__ slots,
+    const float* __restrict__ weights, const uint16_t* __restrict__ residual, int top_k,
+    int width, uint16_t* __restrict__ out) {
+  const int t = blockIdx.x;
+  for (int col = threadIdx.x * 8; col < width; col += blockDim.x * 8) {
+    float acc[8];
+    if (residual != nullptr) {
+      uint4 r = *(const uint4*)(residual + (size_t)t * width + col);
+      uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] = bf16_to_f32(w4[i] & 0xffff);
+        acc[2 * i + 1] = bf16_to_f32(w4[i] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    }
+    for (int j = 0; j < top_k; ++j) {
+      const size_t flat = (size_t)t * top_k + j;
+      const int slot = slots[flat];
+      const float w = weights != nullptr ? weights[flat] : 1.0f;
+      uint4 r = *(const uint4*)(y + (size_t)slot * width + col);
+      uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (weights != nullptr) {
+          acc[2 * i] += bf16_to_f32(w4[i] & 0xffff) * w;
+          acc[2 * i + 1] += bf16_to_f32(w4[i] >> 16) * w;
+        } else {
+          acc[2 * i] += bf16_to_f32(w4[i] & 0xffff);
+          acc[2 * i + 1] += bf16_to_f32(w4[i] >> 16);
+        }
+      }
+    }
+    uint4 o;
+    o.x = pack_bf16x2(acc[0], acc[1]);
+    o.y = pack_bf16x2(acc[2], acc[3]);
+    o.z = pack_bf16x2(acc[4], acc[5]);
+    o.w = pack_bf16x2(acc[6], acc[7]);
+    *(uint4*)(out + (size_t)t * width + col) = o;
+  }
+}
+
+}  // namespace
+
+extern "C" size_t mi355x_permute_plan_workspace_size(int assignments, int experts) {
+  size_t chunks = ((size_t)assignments + kPlanChunk - 1) / kPlanChunk;
+  return (chunks ? chunks : 1) * (size_t)experts * sizeof(int32_t) + 256;
+}
+
+extern "C" int mi355x_permute_plan(const int32_t* ids, int assignments, int experts,
+                                   int64_t* counts, int32_t* offsets, int32_t* order,
+                                   int32_t* slots, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= kMaxExperts, "permute_plan: experts must be in [1, %d]",
+                 kMaxExperts);
+  MI355X_REQUIRE(assignments >= 0, "permute_plan: negative assignments");
+  MI355X_REQUIRE(workspace_bytes >= mi355x_permute_plan_workspace_size(assignments, experts),
+                 "permute_plan: workspace too small");
+  hipStream_t s = (hipStream_t)stream;
+  const int chunks = (assignments + kPlanChunk - 1) / kPlanChunk;
+  int32_t* hist = (int32_t*)workspace;
+  if (chunks > 0) {
+    hipLaunchKernelGGL(plan_hist_kernel, dim3(chunks), dim3(kPlanThreads), 0, s, ids,
+                       assignments, experts, hist);
+    MI355X_LAUNCH_CHECK();
+  }
+  hipLaunchKernelGGL(plan_scan_kernel, dim3(1), dim3(kMaxExperts), 0, s, hist, chunks, experts,
+                     assignments, counts, offsets);
+  MI355X_LAUNCH_CHECK();
+  if (chunks > 0) {
+    hipLaunchKernelGGL(plan_scatter_kernel, dim3(chunks), dim3(kPlanThreads), 0, s, ids,
+                       assignments, experts, hist, order, slots);
+    MI355X_LAUNCH_CHECK();
+  }
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_permute_quantize_fp8(const void* x, int tokens, int width, int top_k,
+                                           const int32_t* slots, uint8_t* q, float* scales,
+                                           void* stream) {
+  MI355X_REQUIRE(width > 0 && width % 128 == 0, "permute_quantize: width must be a multiple of 128");
+  MI355X_REQUIRE(top_k > 0 && top_k <= 32, "permute_quantize: top_k must be in [1, 32]");
+  if (tokens == 0) return MI355X_OK;
+  hipLaunchKernelGGL(permute_quantize_kernel, dim3((tokens + 3) / 4), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)x, tokens, width, top_k, slots, q,
+                     scales, tokens * top_k);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_unpermute_combine(const void* y, const int32_t* slots, const float* weights,
+                                        const void* residual, int tokens, int top_k, int width,
+                                        void* out, void* stream) {
+  MI355X_REQUIRE(width > 0 && width % 8 == 0, "combine: width must be a multiple of 8");
+  MI355X_REQUIRE(weights != nullptr, "combine: route weights are required");
+  if (tokens == 0) return MI355X_OK;
+  hipLaunchKernelGGL(combine_kernel, dim3(tokens), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)y, slots, weights, (const uint16_t*)residual, top_k, width,
+                     (uint16_t*)out);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_unpermute_sum(const void* dx, const int32_t* slots, int tokens, int top_k,
+                                    int width, void* out, void* stream) {
+  MI355X_REQUIRE(width > 0 && width % 8 == 0, "unpermute_sum: width must be a multiple of 8");
+  if (tokens == 0) return MI355X_OK;
+  hipLaunchKernelGGL(combine_kernel, dim3(tokens), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)dx, slots, (const float*)nullptr, (const uint16_t*)nullptr,
+                     top_k, width, (uint16_t*)out);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}

@@ -1,0 +1,476 @@
+// FP8 (OCP e4m3) quantizers of the block-FP8 MoE path and the routed SwiGLU
+// backward row pass. All of them are HBM-bound byte/element work: each reads
+// its source once with 16-byte vector loads and writes e4m3 with 8- or
+// 16-byte stores; 128-element scale groups are formed by 16-lane shuffles.
+#include "common.h"
+
+namespace {
+
+__device__ __forceinline__ void load_bf16x8(const uint16_t* p, float* v) {
+  uint4 r = *(const uint4*)p;
+  uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16_to_f32(w4[i] & 0xffff);
+    v[2 * i + 1] = bf16_to_f32(w4[i] >> 16);
+  }
+}
+
+__device__ __forceinline__ uint2 quant8(const float* v, float s) {
+  uint32_t lo = f32x4_to_e4m3(quant_div(v[0], s), quant_div(v[1], s), quant_div(v[2], s),
+                              quant_div(v[3], s));
+  uint32_t hi = f32x4_to_e4m3(quant_div(v[4], s), quant_div(v[5], s), quant_div(v[6], s),
+                              quant_div(v[7], s));
+  return make_uint2(lo, hi);
+}
+
+// ---------------------------------------------------------------------------
+// 128x128 weight blocks. One block per (expert, block row, block column); a
+// 16-lane group reads one 256-byte row slice, 16 rows per pass, 8 passes.
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float* v);
+template <>
+__device__ __forceinline__ void load8<uint16_t>(const uint16_t* p, float* v) { load_bf16x8(p, v); }
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float* v) {
+  float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) weight_blocks_kernel(
+    const T* __restrict__ w, int out, int in, int bo_count, int bi_count,
+    uint8_t* __restrict__ q, float* __restrict__ scale, uint8_t* __restrict__ q_t) {
+  __shared__ float red[4];
+  __shared__ uint8_t tile[128][128 + 8];
+  const int e = blockIdx.z, bo = blockIdx.y, bi = blockIdx.x;
+  const int lane16 = threadIdx.x & 15, rsub = threadIdx.x >> 4;
+  const int col = bi * 128 + lane16 * 8;
+  const size_t ebase = (size_t)e * out * in;
+  float v[8][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int row = bo * 128 + p * 16 + rsub;
+    if (row < out && col < in) {
+      load8<T>(w + ebase + (size_t)row * in + col, v[p]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[p][i] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[p][i]));
+  }
+  amax = wave_max(amax);
+  if (lane_id() == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = fmaxf(amax / kE4M3Max, kMinScale);
+  if (threadIdx.x == 0) scale[((size_t)e * bo_count + bo) * bi_count + bi] = s;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int row = bo * 128 + p * 16 + rsub;
+    uint2 packed = quant8(v[p], s);
+    if (row < out && col < in) *(uint2*)(q + ebase + (size_t)row * in + col) = packed;
+    if (q_t != nullptr) *(uint2*)&tile[p * 16 + rsub][lane16 * 8] = packed;
+  }
+  if (q_t == nullptr) return;
+  __syncthreads();
+  // Transposed copy: thread writes 8 consecutive source rows of one column.
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int idx = p * 256 + threadIdx.x;  // 2048 = 128 columns x 16 row groups
+    const int c = idx >> 4, rg = idx & 15;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo |= (uint32_t)tile[rg * 8 + i][c] << (8 * i);
+      hi |= (uint32_t)tile[rg * 8 + 4 + i][c] << (8 * i);
+    }
+    const int tcol = bi * 128 + c, trow = bo * 128 + rg * 8;
+    if (tcol < in && trow < out)
+      *(uint2*)(q_t + ebase + (size_t)tcol * out + trow) = make_uint2(lo, hi);
+  }
+}
+
+// e4m3 [E,R,C] -> [E,C,R] through a 128x128 LDS tile.
+__global__ void __launch_bounds__(256) transpose_fp8_kernel(const uint8_t* __restrict__ src,
+                                                            int rows, int cols,
+                                                            uint8_t* __restrict__ dst) {
+  __shared__ uint8_t tile[128][128 + 8];
+  const int e = blockIdx.z, br = blockIdx.y, bc = blockIdx.x;
+  const size_t ebase = (size_t)e * rows * cols;
+  const int lane8 = threadIdx.x & 7, rsub = threadIdx.x >> 3;  // 8 x 16B per 128B row
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int r = br * 128 + p * 32 + rsub, c = bc * 128 + lane8 * 16;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (r < rows && c < cols) val = *(const uint4*)(src + ebase + (size_t)r * cols + c);
+    *(uint2*)&tile[p * 32 + rsub][lane8 * 16] = make_uint2(val.x, val.y);
+    *(uint2*)&tile[p * 32 + rsub][lane8 * 16 + 8] = make_uint2(val.z, val.w);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int idx = p * 256 + threadIdx.x;
+    const int c = idx >> 4, rg = idx & 15;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo |= (uint32_t)tile[rg * 8 + i][c] << (8 * i);
+      hi |= (uint32_t)tile[rg * 8 + 4 + i][c] << (8 * i);
+    }
+    const int tr = bc * 128 + c, tc = br * 128 + rg * 8;
+    if (tr < cols && tc < rows) *(uint2*)(dst + ebase + (size_t)tr * rows + tc) = make_uint2(lo, hi);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Rows already in routed order -> e4m3 with 1x128 scales [width/128][rows].
+// gate_up: the source row is [g0,u0,g1,u1,...]; store gates then ups.
+__global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __restrict__ x,
+                                                            int rows, int width, int64_t pitch,
+                                                            int gate_up, uint8_t* __restrict__ q,
+                                                            float* __restrict__ scales) {
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int r = blockIdx.x * 4 + wave;
+  if (r >= rows) return;
+  const uint16_t* src = x + (size_t)r * pitch;
+  if (!gate_up) {
+    for (int base = 0; base < width; base += 512) {
+      const int col = base + lane * 8;
+      const bool ok = col < width;
+      float v[8];
+      if (ok) load_bf16x8(src + col, v);
+      else
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+      amax = group_max<16>(amax);
+      const float s = fmaxf(amax * kInv448, kMinScale);
+      uint2 packed = quant8(v, s);
+      if (ok) {
+        *(uint2*)(q + (size_t)r * width + col) = packed;
+        if ((lane & 15) == 0) scales[(size_t)(col >> 7) * rows + r] = s;
+      }
+    }
+    return;
+  }
+  const int half = width / 2;
+  for (int base = 0; base < half; base += 512) {
+    const int j = base + lane * 8;  // gate/up pair index
+    const bool ok = j < half;
+    float g[8], u[8];
+    if (ok) {
+      float a[8], b[8];
+      load_bf16x8(src + 2 * j, a);
+      load_bf16x8(src + 2 * j + 8, b);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        g[i] = a[2 * i]; u[i] = a[2 * i + 1];
+        g[4 + i] = b[2 * i]; u[4 + i] = b[2 * i + 1];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) g[i] = u[i] = 0.0f;
+    }
+    float ga = 0.0f, ua = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ga = fmaxf(ga, fabsf(g[i]));
+      ua = fmaxf(ua, fabsf(u[i]));
+    }
+    ga = group_max<16>(ga);
+    ua = group_max<16>(ua);
+    const float sg = fmaxf(ga * kInv448, kMinScale), su = fmaxf(ua * kInv448, kMinScale);
+    uint2 pg = quant8(g, sg), pu = quant8(u, su);
+    if (ok) {
+      *(uint2*)(q + (size_t)r * width + j) = pg;
+      *(uint2*)(q + (size_t)r * width + half + j) = pu;
+      if ((lane & 15) == 0) {
+        scales[(size_t)(j >> 7) * rows + r] = sg;
+        scales[(size_t)((half + j) >> 7) * rows + r] = su;
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ void clamp_gate_up(float& g, float& u, float limit) {
+  if (limit > 0.0f) {
+    g = fminf(g, limit);
+    u = fminf(fmaxf(u, -limit), limit);
+  }
+}
+
+// SwiGLU of interleaved h [rows, 2I] -> e4m3 act [rows, I] + 1x128 scales.
+__global__ void __launch_bounds__(256) swiglu_quantize_kernel(const uint16_t* __restrict__ h,
+                                                              int rows, int width, float limit,
+                                                              uint8_t* __restrict__ q,
+                                                              float* __restrict__ scales) {
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int r = blockIdx.x * 4 + wave;
+  if (r >= rows) return;
+  const uint16_t* src = h + (size_t)r * 2 * width;
+  for (int base = 0; base < width; base += 512) {
+    const int j = base + lane * 8;
+    const bool ok = j < width;
+    float act[8];
+    if (ok) {
+      float a[8], b[8];
+      load_bf16x8(src + 2 * j, a);
+      load_bf16x8(src + 2 * j + 8, b);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float g0 = a[2 * i], u0 = a[2 * i + 1], g1 = b[2 * i], u1 = b[2 * i + 1];
+        clamp_gate_up(g0, u0, limit);
+        clamp_gate_up(g1, u1, limit);
+        act[i] = silu_f(g0) * u0;
+        act[4 + i] = silu_f(g1) * u1;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) act[i] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(act[i]));
+    amax = group_max<16>(amax);
+    const float s = fmaxf(amax * kInv448, kMinScale);
+    uint2 packed = quant8(act, s);
+    if (ok) {
+      *(uint2*)(q + (size_t)r * width + j) = packed;
+      if ((lane & 15) == 0) scales[(size_t)(j >> 7) * rows + r] = s;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Weight-gradient operand: routed rows (optionally gathered) transposed to
+// feature-major e4m3, each expert's rows at its 128-aligned padded offset.
+// Block = (padded 128-row block, 128 source columns).
+__global__ void __launch_bounds__(256) quantize_transpose_kernel(
+    const uint16_t* __restrict__ x, int64_t pitch, int width, const int32_t* __restrict__ gather,
+    int gather_div, int gate_up, const int32_t* __restrict__ offsets, int experts, int padded,
+    uint8_t* __restrict__ qt, float* __restrict__ scales) {
+  __shared__ int ptile[1025];
+  __shared__ uint16_t tile[128][128 + 8];
+  __shared__ float colmax[2][128];
+  const int pb = blockIdx.x, cb = blockIdx.y;
+  // Padded tile prefix per expert (exclusive), computed by thread 0's scan.
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int e = 0; e < experts; ++e) {
+      ptile[e] = acc;
+      acc += (offsets[e + 1] - offsets[e] + 127) >> 7;
+    }
+    ptile[experts] = acc;
+  }
+  __syncthreads();
+  if (pb >= ptile[experts]) return;
+  int lo = 0, hi = experts - 1;
+  while (lo < hi) {  // last e with ptile[e] <= pb
+    int mid = (lo + hi + 1) >> 1;
+    if (ptile[mid] <= pb) lo = mid; else hi = mid - 1;
+  }
+  const int e = lo;
+  const int r0 = offsets[e] + (pb - ptile[e]) * 128;
+  const int nvalid = min(128, offsets[e + 1] - r0);
+  // Load 128 rows x 128 source columns (bf16) into LDS.
+  const int lane16 = threadIdx.x & 15, rsub = threadIdx.x >> 4;
+  const int c0 = cb * 128;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int rr = p * 16 + rsub;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (rr < nvalid && c0 + lane16 * 8 < width) {
+      int src_row = r0 + rr;
+      if (gather != nullptr) src_row = gather[src_row] / gather_div;
+      val = *(const uint4*)(x + (size_t)src_row * pitch + c0 + lane16 * 8);
+    }
+    *(uint4*)&tile[rr][lane16 * 8] = val;
+  }
+  __syncthreads();
+  // Two threads per column, 64 rows each.
+  const int c = threadIdx.x >> 1, half = threadIdx.x & 1;
+  float v[64];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    v[i] = bf16_to_f32(tile[half * 64 + i][c]);
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  const float s = fmaxf(amax * kInv448, kMinScale);
+  const int src_col = c0 + c;
+  if (src_col >= width) return;
+  const int feat = gate_up ? ((src_col & 1) ? width / 2 + (src_col >> 1) : (src_col >> 1)) : src_col;
+  uint8_t* dst = qt + (size_t)feat * padded + (size_t)pb * 128 + half * 64;
+#pragma unroll
+  for (int i = 0; i < 64; i += 16) {
+    uint4 w;
+    w.x = f32x4_to_e4m3(quant_div(v[i], s), quant_div(v[i + 1], s), quant_div(v[i + 2], s),
+                        quant_div(v[i + 3], s));
+    w.y = f32x4_to_e4m3(quant_div(v[i + 4], s), quant_div(v[i + 5], s), quant_div(v[i + 6], s),
+                        quant_div(v[i + 7], s));
+    w.z = f32x4_to_e4m3(quant_div(v[i + 8], s), quant_div(v[i + 9], s), quant_div(v[i + 10], s),
+                        quant_div(v[i + 11], s));
+    w.w = f32x4_to_e4m3(quant_div(v[i + 12], s), quant_div(v[i + 13], s),
+                        quant_div(v[i + 14], s), quant_div(v[i + 15], s));
+    *(uint4*)(dst + i) = w;
+  }
+  if (half == 0) scales[(size_t)feat * (padded / 128) + pb] = s;
+  (void)colmax;
+}
+
+// ---------------------------------------------------------------------------
+// Routed SwiGLU backward, one wave per sorted row.
+__global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
+    const uint16_t* __restrict__ rmat, const uint16_t* __restrict__ h,
+    const float* __restrict__ weights, const int32_t* __restrict__ order, int rows, int width,
+    float limit, uint16_t* __restrict__ dh, uint16_t* __restrict__ a_prime,
+    float* __restrict__ dscore) {
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int row = blockIdx.x * 4 + wave;
+  if (row >= rows) return;
+  const float score = weights[order[row]];
+  const uint16_t* hr = h + (size_t)row * 2 * width;
+  const uint16_t* rr = rmat + (size_t)row * width;
+  float dot = 0.0f;
+  for (int base = 0; base < width; base += 512) {
+    const int j = base + lane * 8;
+    if (j >= width) continue;
+    float a[8], b[8], r[8];
+    load_bf16x8(hr + 2 * j, a);
+    load_bf16x8(hr + 2 * j + 8, b);
+    load_bf16x8(rr + j, r);
+    float dg[8], du[8], ap[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float rg = i < 4 ? a[2 * i] : b[2 * (i - 4)];
+      const float ru = i < 4 ? a[2 * i + 1] : b[2 * (i - 4) + 1];
+      float gv = rg, uv = ru;
+      clamp_gate_up(gv, uv, limit);
+      const float sig = sigmoid_f(gv);
+      const float silu = gv * sig;
+      const float act = silu * uv;
+      dot += r[i] * act;
+      const float gg = r[i] * score;
+      float dgate = gg * uv * (sig + silu * (1.0f - sig));
+      float dup = gg * silu;
+      if (limit > 0.0f) {
+        dgate = rg <= limit ? dgate : 0.0f;
+        dup = (ru >= -limit && ru <= limit) ? dup : 0.0f;
+      }
+      dg[i] = dgate;
+      du[i] = dup;
+      ap[i] = act * score;
+    }
+    uint4 o0, o1, o2;
+    o0.x = pack_bf16x2(dg[0], du[0]); o0.y = pack_bf16x2(dg[1], du[1]);
+    o0.z = pack_bf16x2(dg[2], du[2]); o0.w = pack_bf16x2(dg[3], du[3]);
+    o1.x = pack_bf16x2(dg[4], du[4]); o1.y = pack_bf16x2(dg[5], du[5]);
+    o1.z = pack_bf16x2(dg[6], du[6]); o1.w = pack_bf16x2(dg[7], du[7]);
+    o2.x = pack_bf16x2(ap[0], ap[1]); o2.y = pack_bf16x2(ap[2], ap[3]);
+    o2.z = pack_bf16x2(ap[4], ap[5]); o2.w = pack_bf16x2(ap[6], ap[7]);
+    *(uint4*)(dh + (size_t)row * 2 * width + 2 * j) = o0;
+    *(uint4*)(dh + (size_t)row * 2 * width + 2 * j + 8) = o1;
+    *(uint4*)(a_prime + (size_t)row * width + j) = o2;
+  }
+  dot = wave_sum(dot);
+  if (lane == 0) dscore[row] = dot;
+}
+
+}  // namespace
+
+extern "C" int mi355x_quantize_weight_blocks(const void* w, int is_fp32, int experts, int out,
+                                             int in, uint8_t* q, float* scale, uint8_t* q_t,
+                                             void* stream) {
+  MI355X_REQUIRE(experts >= 0 && out > 0 && in > 0, "quantize_weight_blocks: bad shape");
+  MI355X_REQUIRE(in % 16 == 0 && out % 16 == 0,
+                 "quantize_weight_blocks: out and in must be multiples of 16");
+  if (experts == 0) return MI355X_OK;
+  const int bo = (out + 127) / 128, bi = (in + 127) / 128;
+  dim3 grid(bi, bo, experts);
+  if (is_fp32)
+    hipLaunchKernelGGL(weight_blocks_kernel<float>, grid, dim3(256), 0, (hipStream_t)stream,
+                       (const float*)w, out, in, bo, bi, q, scale, q_t);
+  else
+    hipLaunchKernelGGL(weight_blocks_kernel<uint16_t>, grid, dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)w, out, in, bo, bi, q, scale, q_t);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_transpose_fp8(const uint8_t* q, int experts, int rows, int cols,
+                                    uint8_t* q_t, void* stream) {
+  MI355X_REQUIRE(rows % 16 == 0 && cols % 16 == 0, "transpose_fp8: rows/cols must be multiples of 16");
+  if (experts == 0 || rows == 0 || cols == 0) return MI355X_OK;
+  dim3 grid((cols + 127) / 128, (rows + 127) / 128, experts);
+  hipLaunchKernelGGL(transpose_fp8_kernel, grid, dim3(256), 0, (hipStream_t)stream, q, rows, cols,
+                     q_t);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_quantize_rows_fp8(const void* x, int rows, int width, int64_t pitch,
+                                        int gate_up, uint8_t* q, float* scales, void* stream) {
+  MI355X_REQUIRE(width > 0 && width % 128 == 0, "quantize_rows: width must be a multiple of 128");
+  MI355X_REQUIRE(!gate_up || width % 256 == 0,
+                 "quantize_rows: a gate/up row needs halves that are multiples of 128");
+  MI355X_REQUIRE(pitch >= width && pitch % 8 == 0, "quantize_rows: bad pitch");
+  if (rows == 0) return MI355X_OK;
+  hipLaunchKernelGGL(quantize_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, rows, width, pitch, gate_up, q, scales);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_swiglu_quantize_fp8(const void* h, int rows, int width, float limit,
+                                          uint8_t* q, float* scales, void* stream) {
+  MI355X_REQUIRE(width > 0 && width % 128 == 0, "swiglu_quantize: I must be a multiple of 128");
+  if (rows == 0) return MI355X_OK;
+  hipLaunchKernelGGL(swiglu_quantize_kernel, dim3((rows + 3) / 4), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)h, rows, width, limit, q, scales);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" size_t mi355x_wgrad_padded_rows(int assignments, int experts) {
+  size_t bound = (size_t)assignments + (size_t)experts * 127;
+  return (bound + 127) / 128 * 128;
+}
+
+extern "C" int mi355x_quantize_transpose_fp8(const void* x, int64_t pitch, int width,
+                                             const int32_t* gather, int gather_div, int gate_up,
+                                             const int32_t* offsets, int experts, int assignments,
+                                             int padded, uint8_t* qt, float* scales,
+                                             void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= 1024, "quantize_transpose: experts must be in [1, 1024]");
+  MI355X_REQUIRE(width > 0 && width % 128 == 0, "quantize_transpose: width must be a multiple of 128");
+  MI355X_REQUIRE(!gate_up || width % 2 == 0, "quantize_transpose: gate/up width must be even");
+  MI355X_REQUIRE(padded % 128 == 0 && (size_t)padded >= mi355x_wgrad_padded_rows(assignments, experts),
+                 "quantize_transpose: padded must be a multiple of 128 >= mi355x_wgrad_padded_rows");
+  MI355X_REQUIRE(gather == nullptr || gather_div > 0, "quantize_transpose: gather_div must be > 0");
+  if (assignments == 0) return MI355X_OK;
+  dim3 grid(padded / 128, width / 128);
+  hipLaunchKernelGGL(quantize_transpose_kernel, grid, dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, pitch, width, gather, gather_div, gate_up, offsets,
+                     experts, padded, qt, scales);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_routed_swiglu_bwd(const void* r, const void* h, const float* weights,
+                                        const int32_t* order, int rows, int width, float limit,
+                                        void* dh, void* a_prime, float* dscore, void* stream) {
+  MI355X_REQUIRE(width > 0 && width % 8 == 0, "routed_swiglu_bwd: width must be a multiple of 8");
+  if (rows == 0) return MI355X_OK;
+  hipLaunchKernelGGL(routed_swiglu_bwd_kernel, dim3((rows + 3) / 4), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)r, (const uint16_t*)h, weights, order,
+                     rows, width, limit, (uint16_t*)dh, (uint16_t*)a_prime, dscore);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}

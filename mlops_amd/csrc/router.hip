@@ -1,0 +1,538 @@
+// Router kernels: top-k selection with route weights, routing statistics and
+// the analytic logit gradient. One 64-lane wavefront owns one token; lane l
+// holds experts l, l+64, ... so a token's logits are read once, coalesced.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "common.h"
+
+namespace {
+
+constexpr int kMaxPerLane = 8;  // experts <= 512
+constexpr int kMaxTopK = 32;
+constexpr int kStatsChunk = 64;  // tokens per statistics chunk
+constexpr int kTokensPerBlock = 4;
+
+// Per-lane expert slots: unrolled so the arrays stay in registers.
+#define SLOTS(i) _Pragma("unroll") for (int i = 0; i < kMaxPerLane; ++i) if (i < per_lane)
+
+// Wave argmax with the stable-sort tie rule: larger value first, equal
+// values -> smaller expert id. Returns the winning expert id (or -1).
+__device__ __forceinline__ int wave_argmax(float v, int idx) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float ov = __shfl_xor(v, o, 64);
+    int oi = __shfl_xor(idx, o, 64);
+    bool take = (oi >= 0) && (idx < 0 || ov > v || (ov == v && oi < idx));
+    v = take ? ov : v;
+    idx = take ? oi : idx;
+  }
+  return idx;
+}
+
+// One selection round: the best remaining eligible candidate of the wave
+// (stable descending order). `taken` is the lane's bitmask of used slots.
+__device__ __forceinline__ int select_next(const float* val, const bool* eligible, int per_lane,
+                                           uint32_t& taken) {
+  const int lane = lane_id();
+  float best = 0.0f;
+  int best_idx = -1;
+  SLOTS(i) {
+    if (!eligible[i] || ((taken >> i) & 1u)) continue;
+    if (best_idx < 0 || val[i] > best) {  // ascending e: strict > keeps the lower id
+      best = val[i];
+      best_idx = lane + 64 * i;
+    }
+  }
+  int winner = wave_argmax(best, best_idx);
+  if (winner >= 0 && (winner & 63) == lane) taken |= 1u << (winner >> 6);
+  return winner;
+}
+
+__global__ void __launch_bounds__(256) router_topk_kernel(
+    const float* __restrict__ logits, int tokens, int experts, int top_k, int mode,
+    const float* __restrict__ bias, int n_group, int topk_group, float routed_scaling,
+    const int32_t* __restrict__ forced, float* __restrict__ weights, int32_t* __restrict__ ids) {
+  __shared__ float lds_sel[kTokensPerBlock][512];
+  const int wave = threadIdx.x >> 6;
+  const int lane = lane_id();
+  const int token = blockIdx.x * kTokensPerBlock + wave;
+  if (token >= tokens) return;
+  const int per_lane = (experts + 63) / 64;
+  const float* row = logits + (size_t)token * experts;
+
+  float l[kMaxPerLane], val[kMaxPerLane];
+  bool ok[kMaxPerLane];
+  _Pragma("unroll") for (int i = 0; i < kMaxPerLane; ++i) {
+    int e = lane + 64 * i;
+    l[i] = (i < per_lane && e < experts) ? row[e] : -INFINITY;
+    ok[i] = (i < per_lane && e < experts);
+  }
+
+  // Full softmax (mode 1) or sigmoid scores (mode 2) where needed.
+  float p[kMaxPerLane];
+  _Pragma("unroll") for (int i = 0; i < kMaxPerLane; ++i) p[i] = 0.0f;
+  if (mode == MI355X_ROUTE_SOFTMAX_THEN_TOPK) {
+    float m = -INFINITY;
+    SLOTS(i) m = fmaxf(m, l[i]);
+    m = wave_max(m);
+    float s = 0.0f;
+    SLOTS(i) {
+      p[i] = ok[i] ? __expf(l[i] - m) : 0.0f;
+      s += p[i];
+    }
+    s = wave_sum(s);
+    SLOTS(i) p[i] = p[i] / s;
+  } else if (mode == MI355X_ROUTE_SIGMOID_NOAUX_TC) {
+    SLOTS(i) p[i] = ok[i] ? sigmoid_f(l[i]) : 0.0f;
+  }
+
+  if (forced == nullptr) {
+    if (mode == MI355X_ROUTE_TOPK_THEN_SOFTMAX) {
+      SLOTS(i) val[i] = l[i];
+    } else if (mode == MI355X_ROUTE_SOFTMAX_THEN_TOPK) {
+      SLOTS(i) val[i] = p[i];
+    } else {
+      SLOTS(i) {
+        int e = lane + 64 * i;
+        val[i] = p[i] + (bias != nullptr && ok[i] ? bias[e] : 0.0f);
+      }
+      if (topk_group < n_group) {
+        // Group-limited selection: a group's score is the sum of its two
+        // largest selection values; keep the topk_group best groups.
+        float* sv = lds_sel[wave];
+        SLOTS(i) {
+          int e = lane + 64 * i;
+          if (e < experts) sv[e] = val[i];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int gsize = experts / n_group;
+        float gscore = -INFINITY;
+        if (lane < n_group) {
+          float b1 = -INFINITY, b2 = -INFINITY;
+          for (int t = 0; t < gsize; ++t) {
+            float v = sv[lane * gsize + t];
+            if (v > b1) { b2 = b1; b1 = v; } else if (v > b2) { b2 = v; }
+          }
+          gscore = gsize >= 2 ? b1 + b2 : b1;
+        }
+        uint64_t keep = 0;
+        bool gtaken = false;
+        for (int j = 0; j < topk_group; ++j) {
+          int cand = (lane < n_group && !gtaken) ? lane : -1;
+          int w = wave_argmax(gscore, cand);
+          if (w >= 0) keep |= 1ull << w;
+          if (w == lane) gtaken = true;
+        }
+        SLOTS(i) {
+          int e = lane + 64 * i;
+          if (e < experts && !((keep >> (e / gsize)) & 1ull)) val[i] = -INFINITY;
+        }
+      }
+    }
+  }
+
+  // k rounds: pick (or read the forced) expert j, and hand its logit /
+  // probability to lane j, which owns route weight j.
+  uint32_t taken = 0;
+  float mine = 0.0f;
+  int my_id = 0;
+  for (int j = 0; j < top_k; ++j) {
+    int e = forced != nullptr ? forced[(size_t)token * top_k + j]
+                              : select_next(val, ok, per_lane, taken);
+    int owner = e & 63, slot = e >> 6;
+    float lv = 0.0f, pv = 0.0f;
+    SLOTS(i) {
+      if (i == slot) {
+        lv = l[i];
+        pv = p[i];
+      }
+    }
+    lv = __shfl(lv, owner, 64);
+    pv = __shfl(pv, owner, 64);
+    if (lane == j) {
+      mine = (mode == MI355X_ROUTE_TOPK_THEN_SOFTMAX) ? lv : pv;
+      my_id = e;
+    }
+  }
+  float w = 0.0f;
+  const bool active = lane < top_k;
+  if (mode == MI355X_ROUTE_TOPK_THEN_SOFTMAX) {
+    float m = wave_max(active ? mine : -INFINITY);
+    float ex = active ? __expf(mine - m) : 0.0f;
+    float s = wave_sum(ex);
+    w = ex / s;
+  } else if (mode == MI355X_ROUTE_SOFTMAX_THEN_TOPK) {
+    w = mine;
+  } else {
+    float s = wave_sum(active ? mine : 0.0f);
+    w = mine / s * routed_scaling;
+  }
+  if (active) {
+    weights[(size_t)token * top_k + lane] = w;
+    ids[(size_t)token * top_k + lane] = my_id;
+  }
+}
+
+// Per-chunk partial column sums of the routing probabilities and per-chunk
+// expert counts. Wave w sums tokens start+w, start+w+4, ...; the four wave
+// partials are then added in wave order, so the result is deterministic.
+__global__ void __launch_bounds__(256) router_stats_partial_kernel(
+    const float* __restrict__ logits, const int32_t* __restrict__ ids, int tokens, int experts,
+    int top_k, int mode, const int32_t* __restrict__ seg_offsets,
+    const int32_t* __restrict__ chunk_table, float* __restrict__ part_p,
+    int32_t* __restrict__ part_c) {
+  __shared__ float wave_p[4][512];
+  __shared__ int counts[512];
+  const int c = blockIdx.x;
+  int start, end;
+  if (chunk_table == nullptr) {
+    start = c * kStatsChunk;
+    end = min(tokens, start + kStatsChunk);
+  } else {
+    start = chunk_table[2 * c];
+    int seg = chunk_table[2 * c + 1];
+    end = min(seg_offsets[seg + 1], start + kStatsChunk);
+  }
+  for (int e = threadIdx.x; e < experts; e += blockDim.x) counts[e] = 0;
+  __syncthreads();
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int per_lane = (experts + 63) / 64;
+  float acc[kMaxPerLane];
+  _Pragma("unroll") for (int i = 0; i < kMaxPerLane; ++i) acc[i] = 0.0f;
+  for (int t = start + wave; t < end; t += 4) {
+    const float* row = logits + (size_t)t * experts;
+    float l[kMaxPerLane];
+    SLOTS(i) {
+      int e = lane + 64 * i;
+      l[i] = e < experts ? row[e] : -INFINITY;
+    }
+    if (mode == MI355X_ROUTE_SIGMOID_NOAUX_TC) {
+      float s = 0.0f;
+      SLOTS(i) {
+        int e = lane + 64 * i;
+        l[i] = e < experts ? sigmoid_f(l[i]) : 0.0f;
+        s += l[i];
+      }
+      s = wave_sum(s);
+      SLOTS(i) acc[i] += l[i] / s;
+    } else {
+      float m = -INFINITY;
+      SLOTS(i) m = fmaxf(m, l[i]);
+      m = wave_max(m);
+      float s = 0.0f;
+      SLOTS(i) {
+        l[i] = (lane + 64 * i) < experts ? __expf(l[i] - m) : 0.0f;
+        s += l[i];
+      }
+      s = wave_sum(s);
+      SLOTS(i) acc[i] += l[i] / s;
+    }
+    if (lane < top_k) atomicAdd(&counts[ids[(size_t)t * top_k + lane]], 1);
+  }
+  SLOTS(i) {
+    int e = lane + 64 * i;
+    if (e < experts) wave_p[wave][e] = acc[i];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < experts; e += blockDim.x) {
+    float s = ((wave_p[0][e] + wave_p[1][e]) + wave_p[2][e]) + wave_p[3][e];
+    part_p[(size_t)c * experts + e] = s;
+    part_c[(size_t)c * experts + e] = counts[e];
+  }
+}
+
+// Reduce the chunk partials per segment (in chunk order), then the aux loss.
+__global__ void __launch_bounds__(256) router_stats_final_kernel(
+    const float* __restrict__ part_p, const int32_t* __restrict__ part_c, int nchunks,
+    int tokens, int experts, int top_k, int mode, int segments,
+    const int32_t* __restrict__ seg_offsets, const int32_t* __restrict__ chunk_table,
+    float* __restrict__ aux, float* __restrict__ prob_sum, int32_t* __restrict__ seg_counts) {
+  __shared__ float red[256];
+  float aux_part = 0.0f;
+  for (int e = threadIdx.x; e < experts; e += blockDim.x) {
+    float total_p = 0.0f;
+    int c = 0;
+    for (int s = 0; s < segments; ++s) {
+      float sp = 0.0f;
+      int sc = 0;
+      while (c < nchunks) {
+        int seg = chunk_table == nullptr ? 0 : chunk_table[2 * c + 1];
+        if (seg != s) break;
+        sp += part_p[(size_t)c * experts + e];
+        sc += part_c[(size_t)c * experts + e];
+        ++c;
+      }
+      seg_counts[(size_t)s * experts + e] = sc;
+      total_p += sp;
+      if (mode == MI355X_ROUTE_SIGMOID_NOAUX_TC) {
+        int len = seg_offsets == nullptr ? tokens : seg_offsets[s + 1] - seg_offsets[s];
+        float freq = (float)sc * (float)experts / (float)(top_k * len);
+        aux_part += freq * (sp / (float)len);
+      }
+    }
+    prob_sum[e] = total_p;
+    if (mode != MI355X_ROUTE_SIGMOID_NOAUX_TC) {
+      float freq = (float)seg_counts[e] / (float)(tokens * top_k);
+      aux_part += freq * (total_p / (float)tokens);
+    }
+  }
+  red[threadIdx.x] = aux_part;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0)
+    aux[0] = mode == MI355X_ROUTE_SIGMOID_NOAUX_TC ? red[0] : (float)experts * red[0];
+}
+
+__global__ void __launch_bounds__(256) router_bwd_kernel(
+    const float* __restrict__ logits, const float* __restrict__ weights,
+    const int32_t* __restrict__ ids, const float* __restrict__ dscore,
+    const int32_t* __restrict__ slots, int tokens, int experts, int top_k, int mode,
+    const float* __restrict__ grad_aux, const float* __restrict__ grad_ps,
+    const int32_t* __restrict__ offsets, int segments, const int32_t* __restrict__ seg_offsets,
+    const int32_t* __restrict__ seg_counts, float* __restrict__ grad_logits) {
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int token = blockIdx.x * kTokensPerBlock + wave;
+  if (token >= tokens) return;
+  const int per_lane = (experts + 63) / 64;
+  const float* row = logits + (size_t)token * experts;
+  float l[kMaxPerLane], g[kMaxPerLane];
+  _Pragma("unroll") for (int i = 0; i < kMaxPerLane; ++i) {
+    int e = lane + 64 * i;
+    l[i] = (i < per_lane && e < experts) ? row[e] : -INFINITY;
+    g[i] = 0.0f;
+  }
+  // Route-weight cotangent of this token's k choices (lane j owns choice j).
+  const bool active = lane < top_k;
+  float gw = 0.0f, wj = 0.0f;
+  int idj = 0;
+  if (active) {
+    size_t flat = (size_t)token * top_k + lane;
+    gw = dscore[slots[flat]];
+    wj = weights[flat];
+    idj = ids[flat];
+  }
+  // Probabilities of the token (softmax or normalized sigmoid).
+  float p[kMaxPerLane], s[kMaxPerLane];
+  if (mode == MI355X_ROUTE_SIGMOID_NOAUX_TC) {
+    float rs = 0.0f;
+    SLOTS(i) {
+      s[i] = (lane + 64 * i) < experts ? sigmoid_f(l[i]) : 0.0f;
+      rs += s[i];
+    }
+    rs = wave_sum(rs);
+    SLOTS(i) p[i] = s[i] / rs;
+    // route_backward, sigmoid branch (moe_router.py:406-421).
+    float sj = active ? sigmoid_f(row[idj]) : 0.0f;
+    float score_sum = wave_sum(sj);
+    float scaling = wave_sum(active ? wj : 0.0f);
+    float dot = wave_sum(active ? gw * wj : 0.0f);
+    float selg = active ? ((scaling * gw - dot) / score_sum) * sj * (1.0f - sj) : 0.0f;
+    for (int j = 0; j < top_k; ++j) {
+      float v = __shfl(selg, j, 64);
+      int e = __shfl(idj, j, 64);
+      SLOTS(i)
+        if (e == lane + 64 * i) g[i] += v;
+    }
+    // Per-sequence aux gradient (moe_router.py:476-502).
+    if (grad_aux != nullptr) {
+      int seg = 0;
+      if (seg_offsets != nullptr) {
+        int lo = 0, hi = segments - 1;
+        while (lo < hi) {
+          int mid = (lo + hi + 1) >> 1;
+          if (seg_offsets[mid] <= token) lo = mid; else hi = mid - 1;
+        }
+        seg = lo;
+      }
+      int len = seg_offsets == nullptr ? tokens : seg_offsets[seg + 1] - seg_offsets[seg];
+      float f[kMaxPerLane];
+      float qf = 0.0f;
+      SLOTS(i) {
+        int e = lane + 64 * i;
+        f[i] = e < experts ? (float)seg_counts[(size_t)seg * experts + e] * (float)experts /
+                                 (float)(top_k * len)
+                           : 0.0f;
+        qf += p[i] * f[i];
+      }
+      qf = wave_sum(qf);
+      float coef = grad_aux[0] / ((float)len * rs);
+      SLOTS(i) g[i] += coef * (f[i] - qf) * s[i] * (1.0f - s[i]);
+    }
+    if (grad_ps != nullptr) {
+      float pg = 0.0f;
+      SLOTS(i) {
+        int e = lane + 64 * i;
+        pg += e < experts ? p[i] * grad_ps[e] : 0.0f;
+      }
+      pg = wave_sum(pg);
+      SLOTS(i) {
+        int e = lane + 64 * i;
+        if (e < experts) g[i] += (1.0f - s[i]) * p[i] * (grad_ps[e] - pg);
+      }
+    }
+  } else {
+    float m = -INFINITY;
+    SLOTS(i) m = fmaxf(m, l[i]);
+    m = wave_max(m);
+    float z = 0.0f;
+    SLOTS(i) {
+      p[i] = (lane + 64 * i) < experts ? __expf(l[i] - m) : 0.0f;
+      z += p[i];
+    }
+    z = wave_sum(z);
+    SLOTS(i) p[i] = p[i] / z;
+    if (mode == MI355X_ROUTE_TOPK_THEN_SOFTMAX) {
+      // p_sel (g - <g, p_sel>) scattered to the chosen experts.
+      float dot = wave_sum(active ? gw * wj : 0.0f);
+      float v = active ? wj * (gw - dot) : 0.0f;
+      for (int j = 0; j < top_k; ++j) {
+        float vj = __shfl(v, j, 64);
+        int e = __shfl(idj, j, 64);
+        SLOTS(i)
+          if (e == lane + 64 * i) g[i] += vj;
+      }
+    } else {
+      // -p * <g, p_sel> + scatter(g * p_sel).
+      float psel = 0.0f;
+      for (int j = 0; j < top_k; ++j) {
+        int e = __shfl(idj, j, 64);
+        float pe = 0.0f;
+        SLOTS(i)
+          if (e == lane + 64 * i) pe = p[i];
+        pe = __shfl(pe, e & 63, 64);
+        if (lane == j) psel = pe;
+      }
+      float dot = wave_sum(active ? gw * psel : 0.0f);
+      SLOTS(i) g[i] = -p[i] * dot;
+      float v = active ? gw * psel : 0.0f;
+      for (int j = 0; j < top_k; ++j) {
+        float vj = __shfl(v, j, 64);
+        int e = __shfl(idj, j, 64);
+        SLOTS(i)
+          if (e == lane + 64 * i) g[i] += vj;
+      }
+    }
+    // Batch aux gradient (moe_router.py:455-473): c * p (f - <p, f>).
+    if (grad_aux != nullptr) {
+      float f[kMaxPerLane];
+      float pf = 0.0f;
+      SLOTS(i) {
+        int e = lane + 64 * i;
+        f[i] = e < experts ? (float)(offsets[e + 1] - offsets[e]) / (float)(tokens * top_k) : 0.0f;
+        pf += p[i] * f[i];
+      }
+      pf = wave_sum(pf);
+      float coef = grad_aux[0] * (float)experts / (float)tokens;
+      SLOTS(i) g[i] += coef * p[i] * (f[i] - pf);
+    }
+    if (grad_ps != nullptr) {
+      float pg = 0.0f;
+      SLOTS(i) {
+        int e = lane + 64 * i;
+        pg += e < experts ? p[i] * grad_ps[e] : 0.0f;
+      }
+      pg = wave_sum(pg);
+      SLOTS(i) {
+        int e = lane + 64 * i;
+        if (e < experts) g[i] += p[i] * (grad_ps[e] - pg);
+      }
+    }
+  }
+  float* out = grad_logits + (size_t)token * experts;
+  SLOTS(i) {
+    int e = lane + 64 * i;
+    if (e < experts) out[e] = g[i];
+  }
+}
+
+}  // namespace
+
+extern "C" int mi355x_router_topk(const float* logits, int tokens, int experts, int top_k,
+                                  int mode, const float* bias, int n_group, int topk_group,
+                                  float routed_scaling, const int32_t* forced_ids,
+                                  float* weights, int32_t* ids, void* stream) {
+  MI355X_REQUIRE(tokens >= 0 && experts > 0 && experts <= 64 * kMaxPerLane,
+                 "router: experts must be in [1, %d], got %d", 64 * kMaxPerLane, experts);
+  MI355X_REQUIRE(top_k > 0 && top_k <= experts && top_k <= kMaxTopK,
+                 "router: top_k must be in [1, min(E, %d)], got %d", kMaxTopK, top_k);
+  MI355X_REQUIRE(mode >= 0 && mode <= 2, "router: unknown mode %d", mode);
+  if (mode == MI355X_ROUTE_SIGMOID_NOAUX_TC) {
+    MI355X_REQUIRE(n_group > 0 && experts % n_group == 0 && n_group <= 64,
+                   "router: n_group must divide experts and be <= 64");
+    MI355X_REQUIRE(topk_group > 0, "router: topk_group must be positive");
+  }
+  if (tokens == 0) return MI355X_OK;
+  dim3 grid((tokens + kTokensPerBlock - 1) / kTokensPerBlock);
+  hipLaunchKernelGGL(router_topk_kernel, grid, dim3(256), 0, (hipStream_t)stream, logits, tokens,
+                     experts, top_k, mode, bias, n_group, topk_group, routed_scaling, forced_ids,
+                     weights, ids);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" size_t mi355x_router_stats_workspace_size(int nchunks, int experts) {
+  size_t n = (size_t)nchunks * experts;
+  return n * sizeof(float) + n * sizeof(int32_t) + 256;
+}
+
+extern "C" int mi355x_router_stats(const float* logits, const int32_t* ids, int tokens,
+                                   int experts, int top_k, int mode, int segments,
+                                   const int32_t* seg_offsets, const int32_t* chunk_table,
+                                   int nchunks, float* aux, float* prob_sum, int32_t* seg_counts,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= 64 * kMaxPerLane, "router_stats: bad experts %d",
+                 experts);
+  MI355X_REQUIRE(tokens > 0 && top_k > 0 && top_k <= 64, "router_stats: bad tokens/top_k");
+  MI355X_REQUIRE(segments >= 1, "router_stats: segments must be >= 1");
+  if (chunk_table == nullptr) {
+    MI355X_REQUIRE(segments == 1, "router_stats: several segments need a chunk table");
+    MI355X_REQUIRE(nchunks == (tokens + kStatsChunk - 1) / kStatsChunk,
+                   "router_stats: nchunks must be ceil(tokens / %d)", kStatsChunk);
+  } else {
+    MI355X_REQUIRE(seg_offsets != nullptr, "router_stats: chunk table needs seg_offsets");
+  }
+  MI355X_REQUIRE(workspace_bytes >= mi355x_router_stats_workspace_size(nchunks, experts),
+                 "router_stats: workspace too small");
+  float* part_p = (float*)workspace;
+  int32_t* part_c = (int32_t*)(part_p + (size_t)nchunks * experts);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(router_stats_partial_kernel, dim3(nchunks), dim3(256), 0, s, logits, ids,
+                     tokens, experts, top_k, mode, seg_offsets, chunk_table, part_p, part_c);
+  MI355X_LAUNCH_CHECK();
+  hipLaunchKernelGGL(router_stats_final_kernel, dim3(1), dim3(256), 0, s, part_p, part_c,
+                     nchunks, tokens, experts, top_k, mode, segments, seg_offsets, chunk_table,
+                     aux, prob_sum, seg_counts);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_router_topk_bwd(const float* logits, const float* weights,
+                                      const int32_t* ids, const float* dscore,
+                                      const int32_t* slots, int tokens, int experts, int top_k,
+                                      int mode, const float* grad_aux, const float* grad_prob_sum,
+                                      const int32_t* offsets, int segments,
+                                      const int32_t* seg_offsets, const int32_t* seg_counts,
+                                      float* grad_logits, void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= 64 * kMaxPerLane, "router_bwd: bad experts %d",
+                 experts);
+  MI355X_REQUIRE(top_k > 0 && top_k <= experts && top_k <= kMaxTopK, "router_bwd: bad top_k");
+  MI355X_REQUIRE(mode >= 0 && mode <= 2, "router_bwd: unknown mode %d", mode);
+  if (mode == MI355X_ROUTE_SIGMOID_NOAUX_TC && grad_aux != nullptr)
+    MI355X_REQUIRE(seg_counts != nullptr && (segments == 1 || seg_offsets != nullptr),
+                   "router_bwd: sequence aux gradient needs segment counts and offsets");
+  if (mode != MI355X_ROUTE_SIGMOID_NOAUX_TC && grad_aux != nullptr)
+    MI355X_REQUIRE(offsets != nullptr, "router_bwd: aux gradient needs expert offsets");
+  if (tokens == 0) return MI355X_OK;
+  dim3 grid((tokens + kTokensPerBlock - 1) / kTokensPerBlock);
+  hipLaunchKernelGGL(router_bwd_kernel, grid, dim3(256), 0, (hipStream_t)stream, logits, weights,
+                     ids, dscore, slots, tokens, experts, top_k, mode, grad_aux, grad_prob_sum,
+                     offsets, segments, seg_offsets, seg_counts, grad_logits);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}

@@ -1,0 +1,411 @@
+"""Typed wrappers over the C-ABI kernels of ``libmlops_mi355x.so``.
+
+Each wrapper validates shapes, dtypes and devices on the host, allocates its
+outputs with torch on the input's device, and enqueues the kernel on torch's
+current stream. None of them synchronizes or reads device memory.
+
+Layouts: routed rows ``A = tokens * top_k`` are in expert-sorted order;
+1x128 activation scales are stored K-block major (``scales[kb, row]``);
+128x128 weight scales are ``[E, ceil(out/128), ceil(in/128)]``.
+"""
+
+from __future__ import annotations
+
+from typing import Sequence
+
+import torch
+
+from . import _native
+
+FP8 = torch.float8_e4m3fn
+ROUTING_MODES = {"topk_then_softmax": 0, "softmax_then_topk": 1, "sigmoid_noaux_tc": 2}
+STATS_CHUNK = 64
+MAX_EXPERTS = 512
+MAX_TOP_K = 32
+
+
+class LaunchTimer:
+    """Records a pair of device events around each timed kernel launch, on the
+    stream the kernel is enqueued on, with the launch's algorithmic work.
+    Install with ``set_launch_timer``; read ``summary()`` after a sync."""
+
+    def __init__(self):
+        self.records = []  # (name, start, end, flops, bytes)
+
+    def start(self, device):
+        event = torch.cuda.Event(enable_timing=True)
+        event.record(torch.cuda.current_stream(device))
+        return event
+
+    def stop(self, name, device, start, flops=0, nbytes=0):
+        event = torch.cuda.Event(enable_timing=True)
+        event.record(torch.cuda.current_stream(device))
+        self.records.append((name, start, event, flops, nbytes))
+
+    def summary(self):
+        """``{name: dict(launches, ms_total, ms_avg, flops, bytes)}``."""
+        out = {}
+        for name, start, end, flops, nbytes in self.records:
+            entry = out.setdefault(name, dict(launches=0, ms_total=0.0, flops=0, bytes=0))
+            entry["launches"] += 1
+            entry["ms_total"] += start.elapsed_time(end)
+            entry["flops"] += flops
+            entry["bytes"] += nbytes
+        for entry in out.values():
+            entry["ms_avg"] = entry["ms_total"] / entry["launches"]
+        return out
+
+
+_TIMER: LaunchTimer | None = None
+
+
+def set_launch_timer(timer: LaunchTimer | None) -> None:
+    global _TIMER
+    _TIMER = timer
+
+
+def _timed(name, device, flops, nbytes, fn, *args):
+    if _TIMER is None:
+        _native.call(fn, *args)
+        return
+    start = _TIMER.start(device)
+    _native.call(fn, *args)
+    _TIMER.stop(name, device, start, flops, nbytes)
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _on_gpu(*tensors: torch.Tensor | None) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("the MI355X kernels take GPU tensors only")
+        if not t.is_contiguous():
+            raise ValueError("the MI355X kernels take contiguous tensors")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError("all tensors of one kernel call must be on one device")
+    return device
+
+
+def _check(t: torch.Tensor, shape, dtype, name: str) -> None:
+    if tuple(t.shape) != tuple(shape) or t.dtype != dtype:
+        raise ValueError(f"{name}: expected {dtype} {tuple(shape)}, got {t.dtype} {tuple(t.shape)}")
+
+
+def _limit(limit: float | None) -> float:
+    return 0.0 if limit is None else float(limit)
+
+
+# ------------------------------------------------------------------ router
+def router_topk(
+    logits: torch.Tensor,
+    top_k: int,
+    mode: str,
+    *,
+    bias: torch.Tensor | None = None,
+    n_group: int = 1,
+    topk_group: int = 1,
+    routed_scaling: float = 1.0,
+    forced_ids: torch.Tensor | None = None,
+):
+    """``(weights fp32 [T,k], ids int32 [T,k])`` of fp32 ``logits [T,E]``."""
+    if mode not in ROUTING_MODES:
+        raise ValueError(f"unsupported routing mode {mode!r}")
+    if logits.dtype != torch.float32 or logits.ndim != 2:
+        raise ValueError("router logits must be fp32 [tokens, experts]")
+    tokens, experts = logits.shape
+    if bias is not None:
+        bias = bias.float().contiguous()
+        if bias.shape != (experts,):
+            raise ValueError("router bias must be [experts]")
+    if forced_ids is not None:
+        forced_ids = forced_ids.to(device=logits.device, dtype=torch.int32).contiguous()
+        _check(forced_ids, (tokens, top_k), torch.int32, "forced_ids")
+    device = _on_gpu(logits, bias, forced_ids)
+    weights = torch.empty((tokens, top_k), dtype=torch.float32, device=device)
+    ids = torch.empty((tokens, top_k), dtype=torch.int32, device=device)
+    _native.call(
+        "mi355x_router_topk", _ptr(logits), tokens, experts, int(top_k), ROUTING_MODES[mode],
+        _ptr(bias), int(n_group), int(topk_group), float(routed_scaling), _ptr(forced_ids),
+        _ptr(weights), _ptr(ids), _stream(device),
+    )
+    return weights, ids
+
+
+def segment_tables(lengths: Sequence[int], tokens: int, device):
+    """``(seg_offsets, chunk_table, nchunks)`` for per-sequence statistics;
+    ``(None, None, ceil(T/64))`` for one segment."""
+    lengths = [int(x) for x in lengths]
+    if len(lengths) <= 1:
+        return None, None, (tokens + STATS_CHUNK - 1) // STATS_CHUNK
+    offsets = [0]
+    chunks = []
+    for segment, length in enumerate(lengths):
+        start = offsets[-1]
+        for first in range(start, start + length, STATS_CHUNK):
+            chunks.extend((first, segment))
+        offsets.append(start + length)
+    seg = torch.tensor(offsets, dtype=torch.int32).to(device, non_blocking=False)
+    table = torch.tensor(chunks, dtype=torch.int32).to(device, non_blocking=False)
+    return seg, table, len(chunks) // 2
+
+
+def router_stats(logits, ids, top_k: int, mode: str, lengths: Sequence[int]):
+    """``(aux fp32 [], prob_sum fp32 [E], seg_counts int32 [S,E], seg_offsets)``."""
+    tokens, experts = logits.shape
+    device = _on_gpu(logits, ids)
+    seg_offsets, table, nchunks = segment_tables(lengths, tokens, device)
+    segments = max(1, len(tuple(lengths)))
+    aux = torch.empty((), dtype=torch.float32, device=device)
+    prob_sum = torch.empty(experts, dtype=torch.float32, device=device)
+    seg_counts = torch.empty((segments, experts), dtype=torch.int32, device=device)
+    size = _native.query("mi355x_router_stats_workspace_size", nchunks, experts)
+    workspace = torch.empty(size, dtype=torch.uint8, device=device)
+    _native.call(
+        "mi355x_router_stats", _ptr(logits), _ptr(ids), tokens, experts, int(top_k),
+        ROUTING_MODES[mode], segments, _ptr(seg_offsets), _ptr(table), nchunks, _ptr(aux),
+        _ptr(prob_sum), _ptr(seg_counts), _ptr(workspace), size, _stream(device),
+    )
+    return aux, prob_sum, seg_counts, seg_offsets
+
+
+def router_backward(
+    logits, weights, ids, dscore, slots, mode: str, *, grad_aux=None, grad_prob_sum=None,
+    offsets=None, seg_offsets=None, seg_counts=None,
+):
+    """fp32 ``grad_logits [T,E]`` (route weights' cotangent = ``dscore[slots]``)."""
+    tokens, experts = logits.shape
+    top_k = ids.shape[1]
+    if grad_aux is not None:
+        grad_aux = grad_aux.float().reshape(1).contiguous()
+    if grad_prob_sum is not None:
+        grad_prob_sum = grad_prob_sum.float().contiguous()
+    device = _on_gpu(logits, weights, ids, dscore, slots, grad_aux, grad_prob_sum, offsets,
+                     seg_offsets, seg_counts)
+    segments = 1 if seg_counts is None else seg_counts.shape[0]
+    grad = torch.empty((tokens, experts), dtype=torch.float32, device=device)
+    _native.call(
+        "mi355x_router_topk_bwd", _ptr(logits), _ptr(weights), _ptr(ids), _ptr(dscore),
+        _ptr(slots), tokens, experts, top_k, ROUTING_MODES[mode], _ptr(grad_aux),
+        _ptr(grad_prob_sum), _ptr(offsets), segments, _ptr(seg_offsets), _ptr(seg_counts),
+        _ptr(grad), _stream(device),
+    )
+    return grad
+
+
+# ----------------------------------------------------------------- permute
+def permute_plan(ids: torch.Tensor, experts: int):
+    """``(counts int64 [E], offsets int32 [E+1], order int32 [A], slots int32 [T,k])``."""
+    if ids.dtype != torch.int32:
+        raise ValueError("route ids must be int32")
+    device = _on_gpu(ids)
+    n = ids.numel()
+    counts = torch.empty(experts, dtype=torch.int64, device=device)
+    offsets = torch.empty(experts + 1, dtype=torch.int32, device=device)
+    order = torch.empty(n, dtype=torch.int32, device=device)
+    slots = torch.empty(ids.shape, dtype=torch.int32, device=device)
+    size = _native.query("mi355x_permute_plan_workspace_size", n, experts)
+    workspace = torch.empty(size, dtype=torch.uint8, device=device)
+    _native.call(
+        "mi355x_permute_plan", _ptr(ids), n, int(experts), _ptr(counts), _ptr(offsets),
+        _ptr(order), _ptr(slots), _ptr(workspace), size, _stream(device),
+    )
+    return counts, offsets, order, slots
+
+
+def permute_quantize(x: torch.Tensor, slots: torch.Tensor):
+    """Each token of ``x bf16 [T,H]`` quantized once and written to its k
+    routed rows: ``(q e4m3 [A,H], scales fp32 [H/128, A])``."""
+    if x.dtype != torch.bfloat16 or x.ndim != 2:
+        raise ValueError("permute_quantize takes bf16 [tokens, width]")
+    tokens, width = x.shape
+    top_k = slots.shape[1]
+    _check(slots, (tokens, top_k), torch.int32, "slots")
+    device = _on_gpu(x, slots)
+    rows = tokens * top_k
+    q = torch.empty((rows, width), dtype=FP8, device=device)
+    scales = torch.empty((width // 128, rows), dtype=torch.float32, device=device)
+    nbytes = 2 * tokens * width + rows * width + 4 * rows * (width // 128) + 4 * rows
+    _timed("permute_quantize_fp8", device, 0, nbytes, "mi355x_permute_quantize_fp8", _ptr(x),
+           tokens, width, top_k, _ptr(slots), _ptr(q), _ptr(scales), _stream(device))
+    return q, scales
+
+
+def quantize_rows(x: torch.Tensor, *, gate_up: bool = False):
+    """Rows ``bf16 [R,W]`` -> ``(e4m3 [R,W], scales [W/128, R])``; ``gate_up``
+    stores an interleaved gate/up row as gate columns then up columns."""
+    if x.dtype != torch.bfloat16 or x.ndim != 2:
+        raise ValueError("quantize_rows takes bf16 [rows, width]")
+    rows, width = x.shape
+    device = _on_gpu(x)
+    q = torch.empty((rows, width), dtype=FP8, device=device)
+    scales = torch.empty((width // 128, rows), dtype=torch.float32, device=device)
+    _native.call("mi355x_quantize_rows_fp8", _ptr(x), rows, width, width, int(gate_up), _ptr(q),
+                 _ptr(scales), _stream(device))
+    return q, scales
+
+
+def swiglu_quantize(h: torch.Tensor, limit: float | None = None):
+    """``silu(gate) * up`` of interleaved ``h [R, 2I]`` as ``(e4m3 [R,I], scales [I/128, R])``."""
+    if h.dtype != torch.bfloat16 or h.ndim != 2 or h.shape[1] % 2:
+        raise ValueError("swiglu_quantize takes bf16 [rows, 2I]")
+    rows, width = h.shape[0], h.shape[1] // 2
+    device = _on_gpu(h)
+    q = torch.empty((rows, width), dtype=FP8, device=device)
+    scales = torch.empty((width // 128, rows), dtype=torch.float32, device=device)
+    nbytes = 4 * rows * width + rows * width + 4 * rows * (width // 128)
+    _timed("swiglu_quantize_fp8", device, 0, nbytes, "mi355x_swiglu_quantize_fp8", _ptr(h), rows,
+           width, _limit(limit), _ptr(q), _ptr(scales), _stream(device))
+    return q, scales
+
+
+def quantize_weight_blocks(w: torch.Tensor, *, transposed: bool = False):
+    """``(data e4m3 [E,out,in], scale fp32 [E,ceil(out/128),ceil(in/128)][, data_t])``."""
+    if w.ndim != 3 or w.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("quantize_weight_blocks takes bf16/fp32 [experts, out, in]")
+    w = w.contiguous()
+    device = _on_gpu(w)
+    experts, out, inner = w.shape
+    data = torch.empty(w.shape, dtype=FP8, device=device)
+    scale = torch.empty((experts, -(-out // 128), -(-inner // 128)), dtype=torch.float32,
+                        device=device)
+    data_t = torch.empty((experts, inner, out), dtype=FP8, device=device) if transposed else None
+    _native.call("mi355x_quantize_weight_blocks", _ptr(w), int(w.dtype == torch.float32),
+                 experts, out, inner, _ptr(data), _ptr(scale), _ptr(data_t), _stream(device))
+    return (data, scale, data_t) if transposed else (data, scale)
+
+
+def transpose_fp8(data: torch.Tensor) -> torch.Tensor:
+    """e4m3 ``[E,R,C]`` -> ``[E,C,R]``."""
+    if data.dtype != FP8 or data.ndim != 3:
+        raise ValueError("transpose_fp8 takes e4m3 [E, R, C]")
+    device = _on_gpu(data)
+    experts, rows, cols = data.shape
+    out = torch.empty((experts, cols, rows), dtype=FP8, device=device)
+    _native.call("mi355x_transpose_fp8", _ptr(data), experts, rows, cols, _ptr(out),
+                 _stream(device))
+    return out
+
+
+def wgrad_padded_rows(assignments: int, experts: int) -> int:
+    return _native.query("mi355x_wgrad_padded_rows", int(assignments), int(experts))
+
+
+def quantize_transpose(
+    x: torch.Tensor, offsets: torch.Tensor, assignments: int, *, gather=None,
+    gather_div: int = 1, gate_up: bool = False, padded: int | None = None,
+):
+    """Feature-major e4m3 wgrad operand of the routed rows of ``x``:
+    ``(qt [W, P], scales [W, P/128], P)``, each expert's rows at its
+    128-aligned padded offset (zeros between)."""
+    if x.dtype != torch.bfloat16 or x.ndim != 2:
+        raise ValueError("quantize_transpose takes bf16 [rows, width]")
+    width = x.shape[1]
+    experts = offsets.numel() - 1
+    device = _on_gpu(x, offsets, gather)
+    if padded is None:
+        padded = wgrad_padded_rows(assignments, experts)
+    qt = torch.empty((width, padded), dtype=FP8, device=device)
+    scales = torch.empty((width, padded // 128), dtype=torch.float32, device=device)
+    _native.call(
+        "mi355x_quantize_transpose_fp8", _ptr(x), x.stride(0), width, _ptr(gather),
+        int(gather_div), int(gate_up), _ptr(offsets), experts, int(assignments), int(padded),
+        _ptr(qt), _ptr(scales), _stream(device),
+    )
+    return qt, scales, padded
+
+
+def combine(y, slots, weights, residual):
+    """``residual[t] + sum_j weights[t,j] * y[slots[t,j]]`` in fp32, rounded once."""
+    tokens, top_k = slots.shape
+    width = y.shape[1]
+    _check(weights, (tokens, top_k), torch.float32, "route weights")
+    _check(residual, (tokens, width), torch.bfloat16, "residual")
+    device = _on_gpu(y, slots, weights, residual)
+    out = torch.empty_like(residual)
+    nbytes = 2 * tokens * top_k * width + 8 * tokens * top_k + 4 * tokens * width
+    _timed("unpermute_combine", device, 0, nbytes, "mi355x_unpermute_combine", _ptr(y), _ptr(slots),
+           _ptr(weights), _ptr(residual), tokens, top_k, width, _ptr(out), _stream(device))
+    return out
+
+
+def unpermute_sum(dx, slots):
+    """``sum_j dx[slots[t,j]]`` per token, bf16."""
+    tokens, top_k = slots.shape
+    width = dx.shape[1]
+    device = _on_gpu(dx, slots)
+    out = torch.empty((tokens, width), dtype=dx.dtype, device=device)
+    _native.call("mi355x_unpermute_sum", _ptr(dx), _ptr(slots), tokens, top_k, width, _ptr(out),
+                 _stream(device))
+    return out
+
+
+def routed_swiglu_backward(r, h, weights, order, limit=None):
+    """``(dh [A,2I] interleaved, a' [A,I], dscore fp32 [A])``."""
+    rows, width = r.shape
+    _check(h, (rows, 2 * width), torch.bfloat16, "h")
+    device = _on_gpu(r, h, weights, order)
+    dh = torch.empty_like(h)
+    a_prime = torch.empty_like(r)
+    dscore = torch.empty(rows, dtype=torch.float32, device=device)
+    _native.call("mi355x_routed_swiglu_bwd", _ptr(r), _ptr(h), _ptr(weights), _ptr(order), rows,
+                 width, _limit(limit), _ptr(dh), _ptr(a_prime), _ptr(dscore), _stream(device))
+    return dh, a_prime, dscore
+
+
+# ------------------------------------------------------------------- GEMMs
+def gemm(a, a_scale, w, w_scale, offsets, *, transposed_scale=False, interleave=False,
+         addend=None):
+    """Grouped block-FP8 GEMM: bf16 ``[A, N]`` (see the C header for the math)."""
+    rows, k = a.shape
+    experts, n, wk = w.shape
+    if a.dtype != FP8 or w.dtype != FP8 or wk != k:
+        raise ValueError("gemm takes e4m3 rows [A,K] and e4m3 weights [E,N,K]")
+    _check(a_scale, (k // 128, rows), torch.float32, "row scales")
+    expected = (experts, k // 128, n // 128) if transposed_scale else (experts, n // 128, k // 128)
+    _check(w_scale, expected, torch.float32, "weight scales")
+    _check(offsets, (experts + 1,), torch.int32, "offsets")
+    if addend is not None:
+        _check(addend, (rows, n), torch.bfloat16, "addend")
+    device = _on_gpu(a, a_scale, w, w_scale, offsets, addend)
+    out = torch.empty((rows, n), dtype=torch.bfloat16, device=device)
+    _timed(
+        "gemm_fp8_block", device, 2 * rows * n * k, rows * k + experts * n * k + 2 * rows * n,
+        "mi355x_gemm_fp8_block", _ptr(a), _ptr(a_scale), rows, _ptr(w), _ptr(w_scale),
+        int(transposed_scale), experts, n, k, _ptr(offsets), int(interleave), _ptr(addend),
+        _ptr(out), _stream(device),
+    )
+    return out
+
+
+def wgrad(p, p_scale, q, q_scale, offsets, *, out_dtype=torch.bfloat16, rows=None):
+    """``out[e] = sum over expert e's rows of p[:, row] q[:, row]^T`` -> ``[E, M, N]``.
+    ``rows`` (the routed row count, for the launch timer's FLOP count) is optional."""
+    m, padded = p.shape
+    n = q.shape[0]
+    experts = offsets.numel() - 1
+    _check(q, (n, padded), FP8, "q")
+    _check(p_scale, (m, padded // 128), torch.float32, "p scales")
+    _check(q_scale, (n, padded // 128), torch.float32, "q scales")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("wgrad writes bf16 or fp32")
+    device = _on_gpu(p, p_scale, q, q_scale, offsets)
+    out = torch.empty((experts, m, n), dtype=out_dtype, device=device)
+    flops = 2 * m * n * (padded if rows is None else int(rows))
+    _timed(
+        "gemm_fp8_block_wgrad", device, flops, (m + n) * padded + experts * m * n * out.element_size(),
+        "mi355x_gemm_fp8_block_wgrad", _ptr(p), _ptr(p_scale), m, _ptr(q), _ptr(q_scale), n,
+        padded, _ptr(offsets), experts, _ptr(out), int(out_dtype == torch.float32),
+        _stream(device),
+    )
+    return out

@@ -1,0 +1,68 @@
+"""The router GEMM and its gradients at the reference's precisions.
+
+Semantics of ``src/mlops/kernels/router.py:54-113`` on the GPU:
+
+* logits: bf16 operands (the router weight taken to the activation dtype),
+  fp32 sums, fp32 result (``aten.mm.dtype``);
+* input gradient: ``grad_logits`` taken to bf16, times the bf16 weight,
+  added in place into the bf16 hidden gradient;
+* weight gradient: the cotangent split ``hi = bf16(g)``, ``mid = bf16(g - hi)``,
+  each multiplied against the bf16 activation with fp32 sums (fp32-quality
+  gradient for an fp32 master), then written at the requested dtype.
+
+These small GEMMs ([T,H]x[H,E]) run on hipBLASLt through torch; the MoE
+provider's own kernels take over from the fp32 logits.
+"""
+
+from __future__ import annotations
+
+import torch
+
+OPERAND_DTYPES = (torch.bfloat16, torch.float16)
+
+
+def operand_dtype(hidden: torch.Tensor) -> torch.dtype:
+    return hidden.dtype if hidden.is_cuda and hidden.dtype in OPERAND_DTYPES else torch.float32
+
+
+def _product_fp32(left: torch.Tensor, right: torch.Tensor) -> torch.Tensor:
+    if left.is_cuda and left.dtype in OPERAND_DTYPES and left.dtype == right.dtype:
+        return torch.ops.aten.mm.dtype(left, right, torch.float32)
+    return left.float() @ right.float()
+
+
+def router_logits(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """fp32 ``[rows, E]`` logits of ``hidden [rows, D]`` through ``weight [E, D]``."""
+    dtype = operand_dtype(hidden)
+    return _product_fp32(hidden.to(dtype), weight.to(dtype).t())
+
+
+def add_router_input_gradient_(grad_hidden, grad_logits, weight):
+    """``grad_hidden += grad_logits @ weight`` in place, operands at its dtype."""
+    dtype = operand_dtype(grad_hidden)
+    if dtype == grad_hidden.dtype:
+        grad_hidden.addmm_(grad_logits.to(dtype), weight.to(dtype))
+    else:
+        grad_hidden.add_((grad_logits.float() @ weight.float()).to(grad_hidden.dtype))
+    return grad_hidden
+
+
+def router_weight_gradient(grad_logits, hidden, dtype) -> torch.Tensor:
+    """``grad_logits.T @ hidden`` with fp32 sums, the cotangent in two bf16 pieces."""
+    operands = operand_dtype(hidden)
+    if operands is torch.float32:
+        return (grad_logits.float().t() @ hidden.float()).to(dtype)
+    rows = hidden.to(operands)
+    high = grad_logits.to(operands)
+    gradient = _product_fp32(high.t().contiguous(), rows)
+    residue = (grad_logits.float() - high.float()).to(operands)
+    gradient.add_(_product_fp32(residue.t().contiguous(), rows))
+    return gradient.to(dtype)
+
+
+__all__ = [
+    "add_router_input_gradient_",
+    "operand_dtype",
+    "router_logits",
+    "router_weight_gradient",
+]

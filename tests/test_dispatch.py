@@ -1,0 +1,236 @@
+"""Registry, resolution and context contracts (CPU).
+
+Mirrors the reference's registry tests (tests/test_implementation_registry.py)
+and support-refusal tests (tests/test_sonicmoe_moe.py:226-259): duplicate IDs
+raise, the highest priority wins with ties by ID, forced choices must be
+supported, the explicit surface needs forward/backward, and the MI355X
+provider refuses anything it cannot serve -- with the reason."""
+
+import pytest
+import torch
+from torch.utils.flop_counter import FlopCounterMode
+
+import mlops_amd
+from mlops_amd.dispatch import (
+    Implementation,
+    SupportResult,
+    capture_dispatch,
+    dispatch_manifest,
+    explain_implementation,
+    implementation_registry,
+    resolve_implementation,
+    use_implementation,
+    weight_gradient_dtype,
+    weight_gradients_at,
+)
+from mlops_amd.dispatch import context, registry
+from mlops_amd.dispatch.logical_costs import moe_flops
+from mlops_amd.providers.mi355x import moe as provider
+
+
+def _args(tokens=4, hidden=256, experts=8, inter=128, device="cpu", dtype=torch.bfloat16):
+    x = torch.zeros(tokens, hidden, dtype=dtype, device=device)
+    return (x, x.clone(), torch.zeros(experts, hidden), torch.zeros(experts, 2 * inter, hidden),
+            torch.zeros(experts, hidden, inter))
+
+
+def test_catalog_contains_the_provider():
+    table = implementation_registry()["moe"]
+    assert list(table) == ["mi355x.moe.block_fp8"]
+    impl = table["mi355x.moe.block_fp8"]
+    assert impl.priority > 110 and impl.deterministic and impl.forward and impl.backward
+
+
+def test_duplicate_id_and_pairing_rules():
+    with pytest.raises(ValueError, match="duplicate"):
+        registry.register_implementation(provider.IMPLEMENTATION)
+    with pytest.raises(ValueError, match="together"):
+        Implementation("moe", "x", "p", 0, True, lambda *a, **k: True, lambda: None,
+                       forward=lambda: None)
+
+
+def test_priority_selection_and_forcing():
+    calls = []
+
+    def yes(*a, **k):
+        return SupportResult.yes()
+
+    registry._CATALOG["toy"] = {}
+    try:
+        for name, prio in (("b.low", 1), ("a.high", 5), ("c.high", 5)):
+            registry.register_implementation(
+                Implementation("toy", name, "t", prio, True, yes, lambda *a, **k: calls.append(name)))
+        assert resolve_implementation("toy").implementation_id == "a.high"
+        with use_implementation("toy", "b.low"):
+            assert resolve_implementation("toy").implementation_id == "b.low"
+        with pytest.raises(ValueError, match="unknown implementation"):
+            with use_implementation("toy", "missing"):
+                pass
+        explanation = explain_implementation("toy", surface="explicit")
+        assert explanation.selected is None
+        assert "explicit" in explanation.candidates["a.high"].reason
+    finally:
+        del registry._CATALOG["toy"]
+
+
+def test_resolution_error_lists_reasons():
+    with pytest.raises(RuntimeError, match="mi355x.moe.block_fp8: .*GPU"):
+        mlops_amd.moe(*_args(), top_k=2, routing_mode="topk_then_softmax",
+                      compute_precision="fp8_block")
+
+
+@pytest.mark.parametrize("kwargs,reason", [
+    (dict(compute_precision="bf16"), "not served"),
+    (dict(compute_precision="fp8_current"), "not served"),
+    (dict(compute_precision=None), "compute in bf16"),
+])
+def test_support_refusals_precision(kwargs, reason):
+    result = provider.supports(*_args(), surface="semantic", top_k=2,
+                               routing_mode="topk_then_softmax", **kwargs)
+    assert not result and reason in result.reason
+
+
+def test_support_refusals_with_a_gfx950_device(monkeypatch):
+    """Shape rules, checked past the device gate (monkeypatched, as the
+    reference's support tests monkeypatch capability)."""
+    monkeypatch.setattr(torch.version, "hip", "7.0", raising=False)
+    monkeypatch.setattr(provider, "_arch", lambda device: "gfx950:sramecc+:xnack-")
+
+    class FakeCuda(torch.Tensor):
+        pass
+
+    def gpu(t):
+        t = t.as_subclass(FakeCuda)
+        return t
+
+    monkeypatch.setattr(FakeCuda, "is_cuda", property(lambda self: True))
+    base = dict(surface="semantic", top_k=2, routing_mode="topk_then_softmax",
+                compute_precision="fp8_block")
+    ok = provider.supports(*map(gpu, _args()), **base)
+    assert ok, ok.reason
+    cases = [
+        (_args(hidden=200), {}, "multiples of 128"),
+        (_args(inter=96), {}, "multiples of 128"),
+        (_args(dtype=torch.float32), {}, "bf16"),
+        (_args(), dict(top_k=9), "top_k"),
+        (_args(), dict(routing_mode="nope"), "routing mode"),
+        (_args(), dict(routing_mode="sigmoid_noaux_tc", n_group=3), "n_group"),
+        (_args(), dict(lengths=(1, 2)), "lengths"),
+    ]
+    for args, extra, reason in cases:
+        result = provider.supports(*map(gpu, args), **{**base, **extra})
+        assert not result and reason in result.reason, (extra, result.reason)
+
+
+def test_facade_validation():
+    args = _args()
+    with pytest.raises(ValueError, match="compute precision"):
+        mlops_amd.moe(*args, top_k=2, routing_mode="topk_then_softmax", compute_precision="fp4")
+    with pytest.raises(ValueError, match="positive"):
+        mlops_amd.moe(*args, top_k=2, routing_mode="topk_then_softmax", swiglu_limit=0)
+    with pytest.raises(ValueError, match="together"):
+        mlops_amd.moe(*args, top_k=2, routing_mode="topk_then_softmax", shared_w13=args[2])
+    with pytest.raises(ValueError, match="shared_gate_weight"):
+        mlops_amd.moe(*args, top_k=2, routing_mode="topk_then_softmax", shared_mode="sigmoid")
+
+
+def test_environment_override(monkeypatch):
+    monkeypatch.setenv("MLOPS_IMPLEMENTATIONS", "moe=mi355x.moe.block_fp8")
+    token = context._FORCED.set(context._FORCED.get())
+    try:
+        applied = context.apply_environment_overrides()
+        assert dict(applied) == {"moe": "mi355x.moe.block_fp8"}
+        assert context.implementation_override("moe") == "mi355x.moe.block_fp8"
+    finally:
+        context._FORCED.reset(token)
+    monkeypatch.setenv("MLOPS_IMPLEMENTATIONS", "garbage")
+    with pytest.raises(ValueError):
+        context.apply_environment_overrides()
+
+
+def test_weight_gradient_dtype_context():
+    assert weight_gradient_dtype() is None
+    with weight_gradients_at(torch.float32):
+        assert weight_gradient_dtype() is torch.float32
+    with pytest.raises(ValueError):
+        with weight_gradients_at(torch.int32):
+            pass
+
+
+def test_dispatch_manifest():
+    assert dict(dispatch_manifest({"moe": {"a": 2}})) == {"moe": "a"}
+    with pytest.raises(ValueError):
+        dispatch_manifest({"moe": {"a": 1, "b": 1}})
+    with capture_dispatch() as trace:
+        context.record_dispatch("moe", "x")
+    assert trace == {"moe": {"x": 1}}
+
+
+def test_flop_formulas_on_fake_tensors():
+    """The op pair is priced by FlopCounterMode under fake tensors
+    (reference tests/test_flop_formulas.py:288,403)."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    tokens, hidden, inter, experts, k = 64, 256, 128, 4, 2
+    with FakeTensorMode():
+        x = torch.empty(tokens, hidden, dtype=torch.bfloat16)
+        wr = torch.empty(experts, hidden)
+        w13 = torch.empty(experts, 2 * inter, hidden, dtype=torch.float8_e4m3fn)
+        w2 = torch.empty(experts, hidden, inter, dtype=torch.float8_e4m3fn)
+        s13 = torch.empty(experts, 2, 2)
+        s2 = torch.empty(experts, 2, 1)
+        with FlopCounterMode(display=False) as counter:
+            torch.ops.mlops_mi355x.moe_mi355x_block_fp8_fwd(
+                x, x, wr, w13, w2, torch.empty(0), k, "topk_then_softmax", 1, 1, 1.0, [tokens],
+                "float32", None, None, [s13, s2])
+    expected = moe_flops(x, wr, w13, w2, k, forward=True)
+    assert counter.get_total_flops() == expected
+    a = tokens * k
+    assert expected == (2 * tokens * hidden * experts + 3 * tokens * experts
+                        + 2 * a * hidden * 2 * inter + 5 * a * inter + 2 * a * inter * hidden
+                        + 2 * a * hidden)
+
+
+def test_op_namespace_is_separate():
+    """New ops live in mlops_mi355x:: so the reference's exact torch.ops.mlops
+    manifest test (tests/test_custom_op_contracts.py:787) is unaffected."""
+    assert hasattr(torch.ops.mlops_mi355x, "moe_mi355x_block_fp8_fwd")
+    assert hasattr(torch.ops.mlops_mi355x, "moe_mi355x_block_fp8_bwd")
+
+
+def test_block_fp8_container_on_cpu():
+    from oracle import moe_oracle as O
+
+    w = torch.randn(2, 256, 128) * 0.02
+    data, scale = O.quantize_blocks(w)
+    c = mlops_amd.BlockFP8Weight(data, scale)
+    assert c.shape == (2, 256, 128) and c.dtype == torch.bfloat16
+    assert torch.equal(c.detach()._data.view(torch.uint8), data.view(torch.uint8))
+    d = c.dequantize(dtype=torch.float32)
+    assert torch.allclose(d, O.dequantize_blocks(data, scale))
+    cl = c.clone()
+    assert isinstance(cl, mlops_amd.BlockFP8Weight)
+    flat, meta = c.__tensor_flatten__()
+    assert flat == ["_data", "_scale"]
+    with pytest.raises(ValueError, match="MI355X"):
+        mlops_amd.BlockFP8Weight.quantize(w)
+    with pytest.raises(ValueError, match="E4M3"):
+        mlops_amd.BlockFP8Weight(w, scale)
+    with pytest.raises(NotImplementedError):
+        c + 1
+    assert c.to(torch.float32).dtype == torch.float32  # dequantizing copy
+
+
+def test_routing_override_validation():
+    from mlops_amd.routing import next_override, routing_override
+
+    ids = torch.tensor([[0, 1], [2, 3]])
+    with pytest.raises(RuntimeError, match="consumed 0"):
+        with routing_override([ids]):
+            pass
+    with routing_override([torch.tensor([[0, 0], [1, 2]])]):
+        with pytest.raises(ValueError, match="duplicate"):
+            next_override(2, 4, 2, "cpu")
+    with routing_override([ids]):
+        with pytest.raises(ValueError, match="shape"):
+            next_override(3, 4, 2, "cpu")
