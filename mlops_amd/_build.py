@@ -25,6 +25,9 @@ FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the block-scale fold reads every result with VALU
+    # FMAs, which would otherwise copy each one out of the AGPRs first.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-result",
 ]
 

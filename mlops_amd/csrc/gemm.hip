@@ -399,6 +399,11 @@ int persistent_grid(int tiles) {
 
 }  // namespace
 
+int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, const uint8_t* w,
+                          const float* w_scale, int w_scale_t, int experts, int n, int k,
+                          const int32_t* offsets, int interleave, const void* addend, void* out,
+                          void* stream);
+
 extern "C" int mi355x_gemm_fp8_block(const uint8_t* a, const float* a_scale, int rows,
                                      const uint8_t* w, const float* w_scale, int w_scale_t,
                                      int experts, int n, int k, const int32_t* offsets,
@@ -412,6 +417,9 @@ extern "C" int mi355x_gemm_fp8_block(const uint8_t* a, const float* a_scale, int
                  "gemm: a gate/up weight needs halves that are multiples of 64");
   MI355X_REQUIRE(rows >= 0, "gemm: negative rows");
   if (rows == 0) return MI355X_OK;
+  const int v2 = mi355x_gemm_v2_launch(a, a_scale, rows, w, w_scale, w_scale_t, experts, n, k,
+                                       offsets, interleave, addend, out, stream);
+  if (v2 <= 0) return v2;
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   hipLaunchKernelGGL(grouped_gemm_kernel, dim3(persistent_grid(upper)), dim3(kThreads), 0,
                      (hipStream_t)stream, a, a_scale, rows, w, w_scale, w_scale_t, experts, n, k,

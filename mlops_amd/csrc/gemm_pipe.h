@@ -1,0 +1,136 @@
+// Pipelined block-FP8 MFMA main loop for gfx950, shared by the grouped GEMMs.
+//
+// Workgroup tile 128 (M) x 256 (N) x 128 (K), 4 waves in a 2 x 2 grid, wave
+// tile 64 x 128 (4 x 8 blocks of v_mfma_f32_16x16x128_f8f6f4). Operands are
+// copied global -> LDS by the CDNA4 direct loads (global_load_lds_dwordx4:
+// no staging registers, no LDS store instructions) into a 3-stage ring,
+// waited with an explicit vmcnt and one s_barrier per K step.
+//
+// LDS rows are 128 bytes, unpadded; the 16-byte unit c of row r is stored at
+// unit c ^ ((r >> 1) & 7). With 64 four-byte banks, the 16 rows x one unit
+// that an MFMA fragment read touches then fall on 16 distinct bank groups.
+// A direct load writes 64 lanes x 16 B = 8 rows; lane L writes unit L % 8 of
+// row L / 8 and so loads the logical unit (L % 8) ^ swizzle(row).
+#pragma once
+
+#include "common.h"
+
+namespace pipe {
+
+constexpr int BM = 128, BN = 256, BK = 128;
+constexpr int kThreads = 256;
+constexpr int kStages = 3;
+constexpr int A_BYTES = BM * BK;          // 16 KB
+constexpr int B_BYTES = BN * BK;          // 32 KB
+constexpr int SA_BYTES = BM * 4;          // row scales of A
+constexpr int SB_BYTES = BN * 4;          // column scales of B (weight-gradient form)
+constexpr int STAGE_BYTES = A_BYTES + B_BYTES + SA_BYTES + SB_BYTES;
+constexpr int A_LOADS = A_BYTES / 1024 / 4;  // direct loads per wave per stage: 4
+constexpr int B_LOADS = B_BYTES / 1024 / 4;  // 8
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+
+// The direct loads are issued as inline assembly, invisible to the
+// compiler's wait-count bookkeeping: it would otherwise wait for every
+// in-flight load before any LDS read it cannot prove disjoint. The kernels
+// count their own loads and wait with wait_and_sync<N>.
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return (uint32_t)(size_t)(lds_ptr_t)p;
+}
+// Source address = wave-uniform 64-bit base (SGPRs) + per-lane 32-bit byte
+// offset (one VGPR), the saddr form of the global load.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, const uint8_t* lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds_addr(lds)), "v"(off), "s"(base) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, const uint8_t* lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
+               :: "s"(lds_addr(lds)), "v"(off), "s"(base) : "memory", "m0");
+}
+
+// Wait until at most N direct loads of this wave are in flight, then barrier.
+template <int N>
+__device__ __forceinline__ void wait_and_sync() {
+  static_assert(N >= 0 && N < 16, "vmcnt range");
+  // gfx9 s_waitcnt: vmcnt[3:0], expcnt[6:4]=7, lgkmcnt[11:8]=15, vmcnt[5:4]=0
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void sync_all() {
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// 32 fp8 K-values of one fragment row from a swizzled stage tile.
+__device__ __forceinline__ v8i frag(const uint8_t* tile, int row, int lane) {
+  const int g = lane >> 4;  // units 2g, 2g+1
+  const int s = swz(row);
+  const uint8_t* base = tile + row * 128;
+  uint4 x = *(const uint4*)(base + 16 * ((2 * g) ^ s));
+  uint4 y = *(const uint4*)(base + 16 * ((2 * g + 1) ^ s));
+  v8i r;
+  r[0] = x.x; r[1] = x.y; r[2] = x.z; r[3] = x.w;
+  r[4] = y.x; r[5] = y.y; r[6] = y.z; r[7] = y.w;
+  return r;
+}
+
+__device__ __forceinline__ v4f mfma(v8i a, v8i b) {
+  const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, zero, 0, 0, 0, 0, 0, 0);
+}
+
+// Exclusive prefix of ceil(rows_e / tile) over experts -> prefix[0..E].
+__device__ inline void tile_prefix(const int32_t* __restrict__ offsets, int experts, int tile,
+                                   int* prefix, int* tmp) {
+  const int t = threadIdx.x;
+  const int per = (experts + kThreads - 1) / kThreads;
+  int local = 0;
+  for (int i = 0; i < per; ++i) {
+    int e = t * per + i;
+    if (e < experts) local += (offsets[e + 1] - offsets[e] + tile - 1) / tile;
+  }
+  tmp[t] = local;
+  __syncthreads();
+  for (int o = 1; o < kThreads; o <<= 1) {
+    int v = t >= o ? tmp[t - o] : 0;
+    __syncthreads();
+    tmp[t] += v;
+    __syncthreads();
+  }
+  int run = tmp[t] - local;
+  for (int i = 0; i < per; ++i) {
+    int e = t * per + i;
+    if (e < experts) {
+      prefix[e] = run;
+      run += (offsets[e + 1] - offsets[e] + tile - 1) / tile;
+    }
+  }
+  if (t == kThreads - 1) prefix[experts] = tmp[t];
+  __syncthreads();
+}
+
+__device__ __forceinline__ int find_expert(const int* prefix, int experts, int tile) {
+  int lo = 0, hi = experts - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (prefix[mid] <= tile) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Persistent tile order: in each round of G tiles, XCD x (= block % 8) takes
+// the G/8 consecutive tiles starting at x * G/8, so the 32 CUs of one XCD
+// share A rows across N tiles and weights across M tiles in their L2.
+__device__ __forceinline__ int tile_of(int round, int block, int grid) {
+  if (grid % 8) return round * grid + block;
+  return round * grid + (block % 8) * (grid / 8) + block / 8;
+}
+
+}  // namespace pipe
