@@ -1,14 +1,22 @@
 // Pipelined block-FP8 MFMA main loop for gfx950, shared by the grouped GEMMs.
 //
-// Workgroup tile 128 (M) x 256 (N) x 128 (K), 4 waves in a 2 x 2 grid, wave
-// tile 64 x 128 (4 x 8 blocks of v_mfma_f32_16x16x128_f8f6f4). Operands are
-// copied global -> LDS by the CDNA4 direct loads (global_load_lds_dwordx4:
-// no staging registers, no LDS store instructions) into a 3-stage ring,
-// waited with an explicit vmcnt and one s_barrier per K step.
+// Workgroup tile 256 (M) x 256 (N) x 128 (K), 8 waves (two per SIMD) in a
+// 4 x 2 grid, wave tile 64 x 128 (4 x 8 blocks of
+// v_mfma_f32_16x16x128_f8f6f4). Operands are copied global -> LDS by the
+// CDNA4 direct loads (global_load_lds_dwordx4: no staging registers, no LDS
+// store instructions) into two stages, one s_barrier per K step.
+//
+// Why 256 x 256: the L2 -> LDS direct-load path sustains ~54 B/clk/CU on
+// MI355X (measured); a K step of this tile moves 64 KB for 16.8 MFLOP
+// (256 flop/B), so the copy takes ~60% of the MFMA time and hides under it,
+// where a 128 x 256 tile (171 flop/B) would make the GEMM copy-bound.
 //
 // LDS rows are 128 bytes, unpadded; the 16-byte unit c of row r is stored at
-// unit c ^ ((r >> 1) & 7). With 64 four-byte banks, the 16 rows x one unit
-// that an MFMA fragment read touches then fall on 16 distinct bank groups.
+// unit c ^ (r & 7). A fragment lane (row l % 16, group g = l / 16) takes the
+// units g and g + 4 of its row: A and B lanes agree on that K assignment, so
+// the MFMA sum is unchanged, and a wave's 16 rows x 4 units per read then
+// hit every bank once (measured on MI355X: full LDS read bandwidth, against
+// ~63% for adjacent unit pairs under any row swizzle).
 // A direct load writes 64 lanes x 16 B = 8 rows; lane L writes unit L % 8 of
 // row L / 8 and so loads the logical unit (L % 8) ^ swizzle(row).
 #pragma once
@@ -17,27 +25,29 @@
 
 namespace pipe {
 
-constexpr int BM = 128, BN = 256, BK = 128;
-constexpr int kThreads = 256;
-constexpr int kStages = 3;
-constexpr int A_BYTES = BM * BK;          // 16 KB
+constexpr int BM = 256, BN = 256, BK = 128;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kStages = 2;
+constexpr int A_BYTES = BM * BK;          // 32 KB
 constexpr int B_BYTES = BN * BK;          // 32 KB
 constexpr int SA_BYTES = BM * 4;          // row scales of A
 constexpr int SB_BYTES = BN * 4;          // column scales of B (weight-gradient form)
 constexpr int STAGE_BYTES = A_BYTES + B_BYTES + SA_BYTES + SB_BYTES;
-constexpr int A_LOADS = A_BYTES / 1024 / 4;  // direct loads per wave per stage: 4
-constexpr int B_LOADS = B_BYTES / 1024 / 4;  // 8
+constexpr int A_LOADS = A_BYTES / 1024 / kWaves;  // direct loads per wave per stage: 4
+constexpr int B_LOADS = B_BYTES / 1024 / kWaves;  // 4
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int swz(int row) { return row & 7; }
 
 // The direct loads are issued as inline assembly, invisible to the
 // compiler's wait-count bookkeeping: it would otherwise wait for every
 // in-flight load before any LDS read it cannot prove disjoint. The kernels
 // count their own loads and wait with wait_and_sync<N>.
+// LDS byte address of a (wave-uniform) LDS pointer, as a scalar for M0.
 __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
-  return (uint32_t)(size_t)(lds_ptr_t)p;
+  return __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_ptr_t)p);
 }
 // Source address = wave-uniform 64-bit base (SGPRs) + per-lane 32-bit byte
 // offset (one VGPR), the saddr form of the global load.
@@ -70,11 +80,11 @@ __device__ __forceinline__ void sync_all() {
 
 // 32 fp8 K-values of one fragment row from a swizzled stage tile.
 __device__ __forceinline__ v8i frag(const uint8_t* tile, int row, int lane) {
-  const int g = lane >> 4;  // units 2g, 2g+1
+  const int g = lane >> 4;  // units g and g + 4
   const int s = swz(row);
   const uint8_t* base = tile + row * 128;
-  uint4 x = *(const uint4*)(base + 16 * ((2 * g) ^ s));
-  uint4 y = *(const uint4*)(base + 16 * ((2 * g + 1) ^ s));
+  uint4 x = *(const uint4*)(base + 16 * (g ^ s));
+  uint4 y = *(const uint4*)(base + 16 * ((g + 4) ^ s));
   v8i r;
   r[0] = x.x; r[1] = x.y; r[2] = x.z; r[3] = x.w;
   r[4] = y.x; r[5] = y.y; r[6] = y.z; r[7] = y.w;
@@ -128,9 +138,11 @@ __device__ __forceinline__ int find_expert(const int* prefix, int experts, int t
 // Persistent tile order: in each round of G tiles, XCD x (= block % 8) takes
 // the G/8 consecutive tiles starting at x * G/8, so the 32 CUs of one XCD
 // share A rows across N tiles and weights across M tiles in their L2.
+// Round-robin tile assignment. Grouping consecutive tiles onto one XCD (block
+// b runs on XCD b % 8) raised the L2 hit rate from ~10% to ~64% but measured
+// 5-20% slower on the MoE and dense shapes, so tiles go out in plain order.
 __device__ __forceinline__ int tile_of(int round, int block, int grid) {
-  if (grid % 8) return round * grid + block;
-  return round * grid + (block % 8) * (grid / 8) + block / 8;
+  return round * grid + block;
 }
 
 }  // namespace pipe
