@@ -54,6 +54,10 @@ def make_inputs(cfg, device, seed=0):
 
 def gpu_step(moe, args, cfg):
     x, res, wr, w13, w2, dy = args
+    # A training step starts from cleared gradients (optimizer.zero_grad(set_to_none=True));
+    # without this, autograd would add each step's weight gradients into the last ones.
+    for t in (wr, w13, w2):
+        t.grad = None
     out, aux, counts, psum = moe(x, res, wr, w13, w2, top_k=cfg["top_k"],
                                  routing_mode="topk_then_softmax", compute_precision="fp8_block")
     torch.autograd.backward([out, aux], [dy, torch.full_like(aux, 0.01)])

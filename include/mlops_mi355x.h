@@ -132,10 +132,12 @@ int mi355x_transpose_fp8(const uint8_t* q, int experts, int rows, int cols, uint
  * (bf16, row pitch `pitch`; with gather != NULL sorted row r reads source row
  * gather[r] / gather_div) are written transposed, [width][padded], each
  * expert's rows starting at its 128-aligned padded offset, zero filled, with
- * one descale per (feature, 128-row block). gate_up de-interleaves columns as
- * in mi355x_quantize_rows_fp8. Replaces quantize_transpose_fp8
+ * one descale per (feature, 128-row block): max(amax / 448, 1e-12) rounded
+ * up to a power of two, so that the weight-gradient GEMM can apply it as an
+ * MFMA E8M0 block scale. gate_up de-interleaves columns as in
+ * mi355x_quantize_rows_fp8. Replaces quantize_transpose_fp8
  * (kernels/quack_moe/quantize_transpose.py:126-313) with per-128-token
- * instead of per-expert scales. scales: [width][padded/128]. */
+ * power-of-two instead of per-expert fp32 scales. scales: [padded/128][width]. */
 size_t mi355x_wgrad_padded_rows(int assignments, int experts);
 int mi355x_quantize_transpose_fp8(const void* x, int64_t pitch, int width, const int32_t* gather,
                                   int gather_div, int gate_up, const int32_t* offsets,
@@ -184,7 +186,11 @@ int mi355x_gemm_fp8_block(const uint8_t* a, const float* a_scale, int rows, cons
 /* Grouped weight-gradient GEMM over feature-major e4m3 operands of the same
  * padded layout (see mi355x_quantize_transpose_fp8):
  *   out[e][m][n] = sum_{rows of e} p[m][row] q[n][row], block-scaled,
- * fp32 accumulation, written as bf16 (out_fp32 == 0) or fp32. Experts with no
+ * fp32 accumulation, written as bf16 (out_fp32 == 0) or fp32. p_scale
+ * [padded/128][m_features], q_scale [padded/128][n_features]: powers of two
+ * (as written by mi355x_quantize_transpose_fp8; other values are truncated to
+ * their power-of-two exponent when both feature counts are multiples of 256,
+ * where the MFMA applies the scales in hardware). Experts with no
  * rows get zeros. Replaces the varlen-K wgrad GEMMs
  * (providers/sonicmoe/moe.py:351-365, :404-419; quack_moe/wgrad.py:30). */
 int mi355x_gemm_fp8_block_wgrad(const uint8_t* p, const float* p_scale, int m_features,

@@ -75,6 +75,14 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t byte) {
 }
 
 // Quantize one value given its descale: IEEE division, clip to +-448.
+// Smallest power of two >= x (x positive, normal): the descale of an operand
+// the MFMA scales in hardware (E8M0 = the fp32 biased exponent byte).
+__device__ __forceinline__ float pow2_ceil(float x) {
+  uint32_t b = __float_as_uint(x);
+  if (b & 0x7fffffu) b = (b & 0x7f800000u) + 0x800000u;
+  return __uint_as_float(b);
+}
+
 __device__ __forceinline__ float quant_div(float x, float scale) {
   float q = x / scale;
   return fminf(fmaxf(q, -kE4M3Max), kE4M3Max);

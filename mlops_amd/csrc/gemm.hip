@@ -266,7 +266,6 @@ __global__ void __launch_bounds__(kThreads, 2) wgrad_gemm_kernel(
   const int m_tiles = Mf / BM, n_tiles = Nf / BN;
   const int per_e = m_tiles * n_tiles;
   const int total = experts * per_e;
-  const int pblocks = padded / 128;
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
@@ -299,8 +298,8 @@ __global__ void __launch_bounds__(kThreads, 2) wgrad_gemm_kernel(
         ra[s] = *(const uint4*)(gp[s] + koff);
         rb[s] = *(const uint4*)(gq[s] + koff);
       }
-      if (tid < BM) rs = p_scale[(size_t)(mt * BM + tid) * pblocks + kb0 + kb];
-      else rs = q_scale[(size_t)(nt * BN + tid - BM) * pblocks + kb0 + kb];
+      if (tid < BM) rs = p_scale[(size_t)(kb0 + kb) * Mf + mt * BM + tid];
+      else rs = q_scale[(size_t)(kb0 + kb) * Nf + nt * BN + tid - BM];
     };
     auto stash = [&](int buf) {
 #pragma unroll
@@ -404,6 +403,11 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
                           const int32_t* offsets, int interleave, const void* addend, void* out,
                           void* stream);
 
+int mi355x_wgrad_v2_launch(const uint8_t* p, const float* p_scale, int m_features,
+                           const uint8_t* q, const float* q_scale, int n_features, int padded,
+                           const int32_t* offsets, int experts, void* out, int out_fp32,
+                           void* stream);
+
 extern "C" int mi355x_gemm_fp8_block(const uint8_t* a, const float* a_scale, int rows,
                                      const uint8_t* w, const float* w_scale, int w_scale_t,
                                      int experts, int n, int k, const int32_t* offsets,
@@ -438,6 +442,9 @@ extern "C" int mi355x_gemm_fp8_block_wgrad(const uint8_t* p, const float* p_scal
   MI355X_REQUIRE(m_features > 0 && m_features % BM == 0 && n_features > 0 && n_features % BN == 0,
                  "wgrad: feature counts must be multiples of 128");
   MI355X_REQUIRE(padded % 128 == 0, "wgrad: padded rows must be a multiple of 128");
+  const int v2 = mi355x_wgrad_v2_launch(p, p_scale, m_features, q, q_scale, n_features, padded,
+                                        offsets, experts, out, out_fp32, stream);
+  if (v2 <= 0) return v2;
   const int tiles = experts * (m_features / BM) * (n_features / BN);
   hipLaunchKernelGGL(wgrad_gemm_kernel, dim3(persistent_grid(tiles)), dim3(kThreads), 0,
                      (hipStream_t)stream, p, p_scale, m_features, q, q_scale, n_features, padded,

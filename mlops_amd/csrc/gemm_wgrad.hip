@@ -1,0 +1,218 @@
+// Grouped weight-gradient GEMM, pipelined form (both feature counts
+// multiples of 256):
+//   out[e][m][n] = sum over expert e's padded rows k of P[m][k] * Q[n][k]
+// with P, Q the feature-major e4m3 operands written by the transposing
+// quantizer and one power-of-two descale per (feature, 128-row block).
+//
+// Same main loop as the grouped GEMM (gemm_pipe.h: 256 x 256 tile, 8 waves,
+// direct-to-LDS loads, two stages) with one difference: both operands carry
+// per-row scales that are powers of two, so the MFMA applies them itself
+// (v_mfma_scale_f32_16x16x128_f8f6f4 with E8M0 scales = the fp32 exponent
+// byte) and accumulates across K blocks in place: no VALU work in the loop.
+// Hardware operand layout (measured on MI355X): lane l of a 16x16x128
+// fragment holds K bytes [16g, 16g+16) and [64+16g, 64+16g+16), g = l / 16,
+// and the scale of (row m, 32-wide K block b) is taken from lane 16b + m; a
+// scale constant over the 128 K values means each lane passes its own row's.
+#include "gemm_pipe.h"
+
+using namespace pipe;
+
+namespace {
+
+constexpr int kMaxExperts = 512;
+
+// q feature behind B-tile row tr: MFMA column c of block jb feeds output
+// column c * 8 + jb of the wave's 128, so a lane's eight accumulator blocks
+// are eight consecutive output columns.
+__device__ __forceinline__ int feature_col(int tr, int nt) {
+  const int part = tr >> 7, local = tr & 127;
+  return nt * BN + part * 128 + (local & 15) * 8 + (local >> 4);
+}
+
+__device__ __forceinline__ int e8m0(float pow2_scale) { return __float_as_int(pow2_scale) >> 23; }
+
+__device__ __forceinline__ v4f mfma_e8(v8i a, v8i b, v4f c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
+}
+
+struct WTile {
+  int e, mt, nt, k0, nk;  // expert, tile coordinates, first padded block, blocks
+};
+
+__device__ __forceinline__ WTile wdescribe(const int* prefix, int per_e, int n_tiles, int tile) {
+  WTile t;
+  t.e = __builtin_amdgcn_readfirstlane(tile / per_e);
+  const int rem = tile - t.e * per_e;
+  t.mt = __builtin_amdgcn_readfirstlane(rem / n_tiles);
+  t.nt = __builtin_amdgcn_readfirstlane(rem - t.mt * n_tiles);
+  t.k0 = __builtin_amdgcn_readfirstlane(prefix[t.e]);
+  t.nk = __builtin_amdgcn_readfirstlane(prefix[t.e + 1] - prefix[t.e]);
+  return t;
+}
+
+__global__ void __launch_bounds__(kThreads, 2) wgrad_v2_kernel(
+    const uint8_t* __restrict__ p, const float* __restrict__ p_scale, int Mf,
+    const uint8_t* __restrict__ q, const float* __restrict__ q_scale, int Nf, int padded,
+    const int32_t* __restrict__ offsets, int experts, void* __restrict__ out, int out_fp32) {
+  __shared__ __align__(1024) uint8_t smem[kStages * STAGE_BYTES];
+  __shared__ int prefix[kMaxExperts + 1];
+  __shared__ int tmp[kThreads];
+  tile_prefix(offsets, experts, 128, prefix, tmp);  // padded 128-row blocks per expert
+  const int n_tiles = Nf / BN;
+  const int per_e = (Mf / BM) * n_tiles;
+  const int total = experts * per_e;
+  const int tid = threadIdx.x, lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 wave grid
+
+  auto issue = [&](const WTile& t, int kb, int stage) {
+    uint8_t* base = smem + stage * STAGE_BYTES;
+    const size_t kblock = (size_t)(t.k0 + kb);
+    const uint8_t* abase = p + kblock * 128;
+    const uint8_t* bbase = q + kblock * 128;
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+      const int r = (wave * A_LOADS + i) * 8 + (lane >> 3);
+      const uint32_t off = (uint32_t)(t.mt * BM + r) * (uint32_t)padded + 16 * ((lane & 7) ^ swz(r));
+      dma16(abase, off, base + (wave * A_LOADS + i) * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i) {
+      const int tr = (wave * B_LOADS + i) * 8 + (lane >> 3);
+      const uint32_t off = (uint32_t)feature_col(tr, t.nt) * (uint32_t)padded + 16 * ((lane & 7) ^ swz(tr));
+      dma16(bbase, off, base + A_BYTES + (wave * B_LOADS + i) * 1024);
+    }
+    // Scales of this K block: waves 0-3 the 256 P rows, waves 4-7 the 256 Q
+    // rows in B-tile row order.
+    uint8_t* sbase = base + A_BYTES + B_BYTES;
+    if (wave < 4) {
+      dma4(p_scale + kblock * Mf + t.mt * BM, 4u * (uint32_t)(wave * 64 + lane), sbase + wave * 256);
+    } else {
+      dma4(q_scale + kblock * Nf, 4u * (uint32_t)feature_col((wave - 4) * 64 + lane, t.nt),
+           sbase + SA_BYTES + (wave - 4) * 256);
+    }
+  };
+
+  int round = 0;
+  int tile = tile_of(0, blockIdx.x, gridDim.x);
+  if (tile >= total) return;
+  WTile ct = wdescribe(prefix, per_e, n_tiles, tile);
+  bool issued = false;  // whether the current tile's first step is in flight
+  int stage = 0;
+  for (;;) {
+    if (!issued && ct.nk > 0) issue(ct, 0, stage);
+    issued = false;
+    const int next_tile = tile_of(round + 1, blockIdx.x, gridDim.x);
+    v4f acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int kb = 0; kb < ct.nk; ++kb) {
+      wait_and_sync<0>();
+      if (kb + 1 < ct.nk) {
+        issue(ct, kb + 1, stage ^ 1);
+      } else if (next_tile < total) {
+        const WTile nt = wdescribe(prefix, per_e, n_tiles, next_tile);
+        if (nt.nk > 0) {
+          issue(nt, 0, stage ^ 1);
+          issued = true;
+        }
+      }
+      const uint8_t* base = smem + stage * STAGE_BYTES;
+      const uint8_t* ta = base;
+      const uint8_t* tb = base + A_BYTES;
+      const float* sa = (const float*)(base + A_BYTES + B_BYTES);
+      const float* sb = sa + BM;
+      v8i af[4];
+      int ea[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = wm * 64 + i * 16 + (lane & 15);
+        af[i] = frag(ta, row, lane);
+        ea[i] = e8m0(sa[row]);
+      }
+      v8i bcur = frag(tb, wn * 128 + (lane & 15), lane);
+      int ecur = e8m0(sb[wn * 128 + (lane & 15)]);
+#pragma unroll
+      for (int jb = 0; jb < 8; ++jb) {
+        v8i bnext = bcur;
+        int enext = ecur;
+        if (jb < 7) {
+          const int row = wn * 128 + (jb + 1) * 16 + (lane & 15);
+          bnext = frag(tb, row, lane);
+          enext = e8m0(sb[row]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][jb] = mfma_e8(af[i], bcur, acc[i][jb], ea[i], ecur);
+        bcur = bnext;
+        ecur = enext;
+      }
+      stage ^= 1;
+    }
+
+    // Epilogue from registers: lane (row, 8 consecutive columns).
+    const size_t row0 = (size_t)ct.e * Mf + ct.mt * BM + wm * 64;
+    const size_t col0 = (size_t)ct.nt * BN + wn * 128 + (lane & 15) * 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int lrow = i * 16 + 4 * (lane >> 4) + r;
+        const size_t off = (row0 + lrow) * Nf + col0;
+        if (out_fp32) {
+          float* o = (float*)out + off;
+          *(float4*)o = make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
+          *(float4*)(o + 4) = make_float4(acc[i][4][r], acc[i][5][r], acc[i][6][r], acc[i][7][r]);
+        } else {
+          uint4 o;
+          o.x = pack_bf16x2(acc[i][0][r], acc[i][1][r]);
+          o.y = pack_bf16x2(acc[i][2][r], acc[i][3][r]);
+          o.z = pack_bf16x2(acc[i][4][r], acc[i][5][r]);
+          o.w = pack_bf16x2(acc[i][6][r], acc[i][7][r]);
+          *(uint4*)((uint16_t*)out + off) = o;
+        }
+      }
+    }
+    if (next_tile >= total) break;
+    ++round;
+    ct = wdescribe(prefix, per_e, n_tiles, next_tile);
+  }
+}
+
+int cu_count() {
+  static int cus[64] = {0};
+  int dev = 0;
+  hipGetDevice(&dev);
+  if (dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+}  // namespace
+
+// Launches the pipelined kernel; returns 1 if the shape is not its form
+// (feature counts not multiples of 256, or operands beyond 32-bit offsets),
+// in which case the caller uses the general kernel.
+int mi355x_wgrad_v2_launch(const uint8_t* p, const float* p_scale, int m_features,
+                           const uint8_t* q, const float* q_scale, int n_features, int padded,
+                           const int32_t* offsets, int experts, void* out, int out_fp32,
+                           void* stream) {
+  if (m_features % BM != 0 || n_features % BN != 0 || experts > kMaxExperts) return 1;
+  if ((uint64_t)m_features * (uint64_t)padded >= (1ull << 32) ||
+      (uint64_t)n_features * (uint64_t)padded >= (1ull << 32))
+    return 1;
+  const int total = experts * (m_features / BM) * (n_features / BN);
+  const int grid = total < cu_count() ? total : cu_count();
+  hipLaunchKernelGGL(wgrad_v2_kernel, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream, p,
+                     p_scale, m_features, q, q_scale, n_features, padded, offsets, experts, out,
+                     out_fp32);
+  MI355X_LAUNCH_CHECK();
+  return 0;
+}

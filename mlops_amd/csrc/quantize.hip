@@ -251,78 +251,108 @@ __global__ void __launch_bounds__(256) swiglu_quantize_kernel(const uint16_t* __
 // Weight-gradient operand: routed rows (optionally gathered) transposed to
 // feature-major e4m3, each expert's rows at its 128-aligned padded offset.
 // Block = (padded 128-row block, 128 source columns).
+constexpr int kQtPitch = 128 + 8;  // bf16 per LDS row: 272 B keeps 16-byte row alignment
+
 __global__ void __launch_bounds__(256) quantize_transpose_kernel(
     const uint16_t* __restrict__ x, int64_t pitch, int width, const int32_t* __restrict__ gather,
     int gather_div, int gate_up, const int32_t* __restrict__ offsets, int experts, int padded,
     uint8_t* __restrict__ qt, float* __restrict__ scales) {
   __shared__ int ptile[1025];
-  __shared__ uint16_t tile[128][128 + 8];
-  __shared__ float colmax[2][128];
-  const int pb = blockIdx.x, cb = blockIdx.y;
-  // Padded tile prefix per expert (exclusive), computed by thread 0's scan.
-  if (threadIdx.x == 0) {
-    int acc = 0;
-    for (int e = 0; e < experts; ++e) {
-      ptile[e] = acc;
-      acc += (offsets[e + 1] - offsets[e] + 127) >> 7;
-    }
-    ptile[experts] = acc;
+  __shared__ int scan[256];
+  __shared__ __align__(16) uint16_t tile[128 * kQtPitch];
+  __shared__ __align__(16) float pmax[8][128];
+  const int pb = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
+  // Padded 128-row block prefix over experts (exclusive): thread t owns
+  // experts 4t .. 4t + 3.
+  int local[4], sum = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = tid * 4 + j;
+    local[j] = e < experts ? (offsets[e + 1] - offsets[e] + 127) >> 7 : 0;
+    sum += local[j];
   }
+  scan[tid] = sum;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {
+    const int v = tid >= o ? scan[tid - o] : 0;
+    __syncthreads();
+    scan[tid] += v;
+    __syncthreads();
+  }
+  int run = scan[tid] - sum;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = tid * 4 + j;
+    if (e <= experts) ptile[e] = run;
+    run += local[j];
+  }
+  if (tid == 255 && experts == 1024) ptile[1024] = run;
   __syncthreads();
   if (pb >= ptile[experts]) return;
   int lo = 0, hi = experts - 1;
   while (lo < hi) {  // last e with ptile[e] <= pb
-    int mid = (lo + hi + 1) >> 1;
+    const int mid = (lo + hi + 1) >> 1;
     if (ptile[mid] <= pb) lo = mid; else hi = mid - 1;
   }
   const int e = lo;
   const int r0 = offsets[e] + (pb - ptile[e]) * 128;
   const int nvalid = min(128, offsets[e + 1] - r0);
-  // Load 128 rows x 128 source columns (bf16) into LDS.
-  const int lane16 = threadIdx.x & 15, rsub = threadIdx.x >> 4;
   const int c0 = cb * 128;
+  // 128 rows x 128 source columns (bf16) into LDS, zeros past the expert.
+  {
+    const int lane16 = tid & 15, rsub = tid >> 4;
 #pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    const int rr = p * 16 + rsub;
-    uint4 val = make_uint4(0, 0, 0, 0);
-    if (rr < nvalid && c0 + lane16 * 8 < width) {
-      int src_row = r0 + rr;
-      if (gather != nullptr) src_row = gather[src_row] / gather_div;
-      val = *(const uint4*)(x + (size_t)src_row * pitch + c0 + lane16 * 8);
+    for (int p = 0; p < 8; ++p) {
+      const int rr = p * 16 + rsub;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (rr < nvalid) {
+        int src_row = r0 + rr;
+        if (gather != nullptr) src_row = gather[src_row] / gather_div;
+        val = *(const uint4*)(x + (size_t)src_row * pitch + c0 + lane16 * 8);
+      }
+      *(uint4*)&tile[rr * kQtPitch + lane16 * 8] = val;
     }
-    *(uint4*)&tile[rr][lane16 * 8] = val;
   }
   __syncthreads();
-  // Two threads per column, 64 rows each.
-  const int c = threadIdx.x >> 1, half = threadIdx.x & 1;
-  float v[64];
-  float amax = 0.0f;
+  // Thread: 4 columns (fg) x 16 rows (rb); column amax over the 8 row blocks.
+  const int fg = tid & 31, rb = tid >> 5;
+  float v[16][4];
+  float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int i = 0; i < 64; ++i) {
-    v[i] = bf16_to_f32(tile[half * 64 + i][c]);
-    amax = fmaxf(amax, fabsf(v[i]));
+  for (int i = 0; i < 16; ++i) {
+    const uint2 d = *(const uint2*)&tile[(rb * 16 + i) * kQtPitch + 4 * fg];
+    v[i][0] = bf16_to_f32(d.x & 0xffff);
+    v[i][1] = bf16_to_f32(d.x >> 16);
+    v[i][2] = bf16_to_f32(d.y & 0xffff);
+    v[i][3] = bf16_to_f32(d.y >> 16);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m[j] = fmaxf(m[j], fabsf(v[i][j]));
   }
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-  const float s = fmaxf(amax * kInv448, kMinScale);
-  const int src_col = c0 + c;
-  if (src_col >= width) return;
-  const int feat = gate_up ? ((src_col & 1) ? width / 2 + (src_col >> 1) : (src_col >> 1)) : src_col;
-  uint8_t* dst = qt + (size_t)feat * padded + (size_t)pb * 128 + half * 64;
+  *(float4*)&pmax[rb][4 * fg] = make_float4(m[0], m[1], m[2], m[3]);
+  __syncthreads();
 #pragma unroll
-  for (int i = 0; i < 64; i += 16) {
+  for (int r = 0; r < 8; ++r) {
+    const float4 q = *(const float4*)&pmax[r][4 * fg];
+    m[0] = fmaxf(m[0], q.x);
+    m[1] = fmaxf(m[1], q.y);
+    m[2] = fmaxf(m[2], q.z);
+    m[3] = fmaxf(m[3], q.w);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int src_col = c0 + 4 * fg + j;
+    const int feat = gate_up ? ((src_col & 1) ? width / 2 + (src_col >> 1) : (src_col >> 1)) : src_col;
+    const float sc = pow2_ceil(fmaxf(m[j] * kInv448, kMinScale));
+    const float inv = 1.0f / sc;  // exact: sc is a power of two
+    auto q = [&](int i) { return fminf(fmaxf(v[i][j] * inv, -kE4M3Max), kE4M3Max); };
     uint4 w;
-    w.x = f32x4_to_e4m3(quant_div(v[i], s), quant_div(v[i + 1], s), quant_div(v[i + 2], s),
-                        quant_div(v[i + 3], s));
-    w.y = f32x4_to_e4m3(quant_div(v[i + 4], s), quant_div(v[i + 5], s), quant_div(v[i + 6], s),
-                        quant_div(v[i + 7], s));
-    w.z = f32x4_to_e4m3(quant_div(v[i + 8], s), quant_div(v[i + 9], s), quant_div(v[i + 10], s),
-                        quant_div(v[i + 11], s));
-    w.w = f32x4_to_e4m3(quant_div(v[i + 12], s), quant_div(v[i + 13], s),
-                        quant_div(v[i + 14], s), quant_div(v[i + 15], s));
-    *(uint4*)(dst + i) = w;
+    w.x = f32x4_to_e4m3(q(0), q(1), q(2), q(3));
+    w.y = f32x4_to_e4m3(q(4), q(5), q(6), q(7));
+    w.z = f32x4_to_e4m3(q(8), q(9), q(10), q(11));
+    w.w = f32x4_to_e4m3(q(12), q(13), q(14), q(15));
+    *(uint4*)(qt + (size_t)feat * padded + (size_t)pb * 128 + rb * 16) = w;
+    if (rb == 0) scales[(size_t)pb * width + feat] = sc;
   }
-  if (half == 0) scales[(size_t)feat * (padded / 128) + pb] = s;
-  (void)colmax;
 }
 
 // ---------------------------------------------------------------------------

@@ -289,6 +289,94 @@ __global__ void __launch_bounds__(256) router_stats_final_kernel(
     aux[0] = mode == MI355X_ROUTE_SIGMOID_NOAUX_TC ? red[0] : (float)experts * red[0];
 }
 
+// Parallel form of the final reduction: each (segment, expert) sum is spread
+// over G lanes of one wave (chunks part, part + G, ...), reduced by a fixed
+// butterfly, so results are deterministic. Sizes beyond the LDS tables use the
+// serial kernel above.
+constexpr int kReduceThreads = 1024;
+constexpr int kReduceMaxSegments = 1024;
+constexpr int kReduceMaxPairs = 8192;
+
+__global__ void __launch_bounds__(kReduceThreads) router_stats_reduce_kernel(
+    const float* __restrict__ part_p, const int32_t* __restrict__ part_c, int nchunks,
+    int tokens, int experts, int top_k, int mode, int segments,
+    const int32_t* __restrict__ seg_offsets, const int32_t* __restrict__ chunk_table,
+    float* __restrict__ aux, float* __restrict__ prob_sum, int32_t* __restrict__ seg_counts) {
+  __shared__ int seg_start[kReduceMaxSegments + 1];
+  __shared__ float sp_lds[kReduceMaxPairs];
+  __shared__ int sc_lds[kReduceMaxPairs];
+  __shared__ float red[kReduceThreads / 64];
+  const int tid = threadIdx.x;
+  // First chunk of every segment (chunks are ordered by segment).
+  if (chunk_table == nullptr) {
+    if (tid == 0) {
+      seg_start[0] = 0;
+      seg_start[1] = nchunks;
+    }
+  } else {
+    for (int c = tid; c < nchunks; c += kReduceThreads) {
+      const int s = chunk_table[2 * c + 1];
+      const int prev = c == 0 ? -1 : chunk_table[2 * c - 1];
+      for (int q = prev + 1; q <= s; ++q) seg_start[q] = c;
+      if (c == nchunks - 1)
+        for (int q = s + 1; q <= segments; ++q) seg_start[q] = nchunks;
+    }
+  }
+  __syncthreads();
+  const int pairs = segments * experts;
+  int G = 64;
+  while (G > 1 && pairs * G > kReduceThreads) G >>= 1;
+  for (int base = 0; base < pairs * G; base += kReduceThreads) {
+    const int idx = base + tid;
+    const int pair = idx / G, part = idx % G;
+    float sp = 0.0f;
+    int sc = 0;
+    if (pair < pairs) {
+      const int seg = pair / experts, e = pair % experts;
+      for (int c = seg_start[seg] + part; c < seg_start[seg + 1]; c += G) {
+        sp += part_p[(size_t)c * experts + e];
+        sc += part_c[(size_t)c * experts + e];
+      }
+    }
+    for (int o = G >> 1; o >= 1; o >>= 1) {
+      sp += __shfl_xor(sp, o, 64);
+      sc += __shfl_xor(sc, o, 64);
+    }
+    if (pair < pairs && part == 0) {
+      sp_lds[pair] = sp;
+      sc_lds[pair] = sc;
+      seg_counts[pair] = sc;
+    }
+  }
+  __syncthreads();
+  float aux_part = 0.0f;
+  for (int e = tid; e < experts; e += kReduceThreads) {
+    float total_p = 0.0f;
+    for (int s = 0; s < segments; ++s) {
+      const float sp = sp_lds[s * experts + e];
+      total_p += sp;
+      if (mode == MI355X_ROUTE_SIGMOID_NOAUX_TC) {
+        const int len = seg_offsets == nullptr ? tokens : seg_offsets[s + 1] - seg_offsets[s];
+        const float freq = (float)sc_lds[s * experts + e] * (float)experts / (float)(top_k * len);
+        aux_part += freq * (sp / (float)len);
+      }
+    }
+    prob_sum[e] = total_p;
+    if (mode != MI355X_ROUTE_SIGMOID_NOAUX_TC) {
+      const float freq = (float)sc_lds[e] / (float)(tokens * top_k);
+      aux_part += freq * (total_p / (float)tokens);
+    }
+  }
+  aux_part = wave_sum(aux_part);
+  if (lane_id() == 0) red[tid >> 6] = aux_part;
+  __syncthreads();
+  if (tid == 0) {
+    float total = 0.0f;
+    for (int w = 0; w < kReduceThreads / 64; ++w) total += red[w];
+    aux[0] = mode == MI355X_ROUTE_SIGMOID_NOAUX_TC ? total : (float)experts * total;
+  }
+}
+
 __global__ void __launch_bounds__(256) router_bwd_kernel(
     const float* __restrict__ logits, const float* __restrict__ weights,
     const int32_t* __restrict__ ids, const float* __restrict__ dscore,
@@ -505,9 +593,15 @@ extern "C" int mi355x_router_stats(const float* logits, const int32_t* ids, int 
   hipLaunchKernelGGL(router_stats_partial_kernel, dim3(nchunks), dim3(256), 0, s, logits, ids,
                      tokens, experts, top_k, mode, seg_offsets, chunk_table, part_p, part_c);
   MI355X_LAUNCH_CHECK();
-  hipLaunchKernelGGL(router_stats_final_kernel, dim3(1), dim3(256), 0, s, part_p, part_c,
-                     nchunks, tokens, experts, top_k, mode, segments, seg_offsets, chunk_table,
-                     aux, prob_sum, seg_counts);
+  if (segments <= kReduceMaxSegments && (size_t)segments * experts <= kReduceMaxPairs) {
+    hipLaunchKernelGGL(router_stats_reduce_kernel, dim3(1), dim3(kReduceThreads), 0, s, part_p,
+                       part_c, nchunks, tokens, experts, top_k, mode, segments, seg_offsets,
+                       chunk_table, aux, prob_sum, seg_counts);
+  } else {
+    hipLaunchKernelGGL(router_stats_final_kernel, dim3(1), dim3(256), 0, s, part_p, part_c,
+                       nchunks, tokens, experts, top_k, mode, segments, seg_offsets, chunk_table,
+                       aux, prob_sum, seg_counts);
+  }
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
 }

@@ -306,8 +306,8 @@ def quantize_transpose(
     gather_div: int = 1, gate_up: bool = False, padded: int | None = None,
 ):
     """Feature-major e4m3 wgrad operand of the routed rows of ``x``:
-    ``(qt [W, P], scales [W, P/128], P)``, each expert's rows at its
-    128-aligned padded offset (zeros between)."""
+    ``(qt [W, P], scales [P/128, W], P)``, each expert's rows at its
+    128-aligned padded offset (zeros between); the scales are powers of two."""
     if x.dtype != torch.bfloat16 or x.ndim != 2:
         raise ValueError("quantize_transpose takes bf16 [rows, width]")
     width = x.shape[1]
@@ -316,7 +316,7 @@ def quantize_transpose(
     if padded is None:
         padded = wgrad_padded_rows(assignments, experts)
     qt = torch.empty((width, padded), dtype=FP8, device=device)
-    scales = torch.empty((width, padded // 128), dtype=torch.float32, device=device)
+    scales = torch.empty((padded // 128, width), dtype=torch.float32, device=device)
     _native.call(
         "mi355x_quantize_transpose_fp8", _ptr(x), x.stride(0), width, _ptr(gather),
         int(gather_div), int(gate_up), _ptr(offsets), experts, int(assignments), int(padded),
@@ -395,8 +395,8 @@ def wgrad(p, p_scale, q, q_scale, offsets, *, out_dtype=torch.bfloat16, rows=Non
     n = q.shape[0]
     experts = offsets.numel() - 1
     _check(q, (n, padded), FP8, "q")
-    _check(p_scale, (m, padded // 128), torch.float32, "p scales")
-    _check(q_scale, (n, padded // 128), torch.float32, "q scales")
+    _check(p_scale, (padded // 128, m), torch.float32, "p scales")
+    _check(q_scale, (padded // 128, n), torch.float32, "q scales")
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("wgrad writes bf16 or fp32")
     device = _on_gpu(p, p_scale, q, q_scale, offsets)

@@ -34,7 +34,7 @@ PINNED = {
     "quantize_blocks": "zero block stays zero; amax element maps to +-448; <= 1 e4m3 step;"
                        " torch float8 cast as the rounding library",
     "quantize_rows_1x128": "as quantize_blocks, per 1x128 group, reciprocal-multiply descale",
-    "quantize_transpose_padded": "transpose of quantize_rows on padded per-expert blocks",
+    "quantize_transpose_padded": "pow2 descales: power-of-two and amax/scale in (224, 448] properties",
     "grouped_gemm": "fp64 dequantized product vs a per-row dot-product loop",
     "swiglu / routed_swiglu_backward": "torch autograd of silu(min(g,L))*clamp(u,L)",
     "native_moe": "dense-masked (reference) vs sparse-gathered evaluation; autograd gradients",
@@ -256,11 +256,21 @@ def padded_layout(offsets):
     return starts, acc
 
 
+def pow2_ceil(x):
+    """Smallest power of two >= x, for positive normal fp32 x (exact: bit
+    arithmetic on the exponent field)."""
+    bits = x.float().contiguous().view(torch.int32)
+    up = (bits & 0x7F800000) + 0x00800000
+    return torch.where((bits & 0x007FFFFF) != 0, up, bits).view(torch.float32)
+
+
 def quantize_transpose_padded(rows_bf16, offsets, padded):
-    """Feature-major e4m3 ``[W, P]`` + scales ``[W, P/128]``: each expert's rows
-    at its 128-aligned padded start, one ``amax*(1/448)`` descale per (feature,
-    128-row block) -- the per-feature quantizer of
-    kernels/quack_moe/quantize_transpose.py:126-313 on 128-row blocks."""
+    """Feature-major e4m3 ``[W, P]`` + scales ``[P/128, W]``: each expert's rows
+    at its 128-aligned padded start, one descale per (feature, 128-row block).
+    The descale is ``max(amax * (1/448), 1e-12)`` -- the per-feature rule of
+    kernels/quack_moe/quantize_transpose.py:116-117 -- rounded up to a power of
+    two (the MFMA applies power-of-two scales in hardware), then ``q =
+    e4m3(clip(x / scale, +-448))`` as at :117."""
     x = rows_bf16.float()
     width = x.shape[1]
     starts, total = padded_layout(offsets)
@@ -268,7 +278,10 @@ def quantize_transpose_padded(rows_bf16, offsets, padded):
     for e, start in enumerate(starts):
         lo, hi = int(offsets[e]), int(offsets[e + 1])
         full[start:start + hi - lo] = x[lo:hi]
-    q, scales = quantize_rows_1x128(full.t().contiguous())
+    groups = full.t().contiguous().view(width, padded // 128, 128)
+    amax = groups.abs().amax(-1)
+    scales = pow2_ceil(torch.clamp_min(amax * torch.tensor(INV448, dtype=torch.float32), 1e-12))
+    q = _e4m3((groups / scales.unsqueeze(-1)).clamp(-E4M3_MAX, E4M3_MAX)).view(width, padded)
     return q, scales.t().contiguous(), total
 
 
@@ -296,8 +309,8 @@ def grouped_gemm(aq, a_scales, wq, w_scale, offsets, *, transposed=False, interl
 
 def wgrad(pq, p_scales, qq, q_scales, offsets):
     """``dW[e] = sum_rows p q^T`` over expert e's padded rows (fp64, dequantized)."""
-    p = dequantize_rows(pq, p_scales.t().contiguous()).double()
-    q = dequantize_rows(qq, q_scales.t().contiguous()).double()
+    p = dequantize_rows(pq, p_scales).double()
+    q = dequantize_rows(qq, q_scales).double()
     starts, _ = padded_layout(offsets)
     experts = len(starts)
     out = torch.zeros(experts, p.shape[0], q.shape[0], dtype=torch.float64)

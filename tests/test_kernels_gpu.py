@@ -199,7 +199,7 @@ def test_quantize_transpose_bit_exact(device, gather, gate_up):
         rows = rows[:, O.gate_up_columns(width)]
     oq, os_, total = O.quantize_transpose_padded(rows, offsets, padded)
     assert torch.equal(_bytes(qt)[:, :total], oq.view(torch.uint8)[:, :total])
-    assert torch.equal(st.cpu()[:, : total // 128], os_[:, : total // 128])
+    assert torch.equal(st.cpu()[: total // 128], os_[: total // 128])
 
 
 # ------------------------------------------------------------------- GEMMs
@@ -278,14 +278,18 @@ def test_grouped_gemm_baseline_config2_sampled(device):
         assert max_rel(out[sample], want) < 1e-2, e
 
 
+# (256, 384): general kernel; (512, 768): the pipelined hardware-scaled one.
+@pytest.mark.parametrize("features", [(256, 384), (512, 768)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
-def test_wgrad_matches_fp64(device, out_dtype):
+def test_wgrad_matches_fp64(device, out_dtype, features):
     g = torch.Generator().manual_seed(19)
     counts = [0, 300, 50, 129]
     offsets = _ragged(counts)
     rows = int(offsets[-1])
-    p_rows = torch.randn(rows, 256, generator=g).to(torch.bfloat16)
-    q_rows = torch.randn(rows, 384, generator=g).to(torch.bfloat16)
+    p_rows = torch.randn(rows, features[0], generator=g).to(torch.bfloat16)
+    q_rows = torch.randn(rows, features[1], generator=g).to(torch.bfloat16)
+    p_rows[7] *= 1e4  # spread the per-block scales over many binades
+    q_rows[:, 5] *= 1e-5
     pt, pts, padded = K.quantize_transpose(p_rows.to(device), offsets.to(device), rows)
     qt, qts, _ = K.quantize_transpose(q_rows.to(device), offsets.to(device), rows, padded=padded)
     out = K.wgrad(pt, pts, qt, qts, offsets.to(device), out_dtype=out_dtype).cpu()

@@ -119,11 +119,27 @@ def test_gate_up_columns_and_transpose_layout():
     starts, total = O.padded_layout(offsets)
     assert starts == [0, 128, 128] and total == 128 + 256
     qt, st, _ = O.quantize_transpose_padded(rows, offsets, 512)
-    assert qt.shape == (128, 512) and st.shape == (128, 4)
+    assert qt.shape == (128, 512) and st.shape == (4, 128)
     # expert 2's rows start at padded column 128; padding is zero
-    q_rows, s_rows = O.quantize_rows_1x128(rows[100:228].t().contiguous())
-    assert torch.equal(qt[:, 128:256].view(torch.uint8), q_rows.view(torch.uint8))
     assert torch.all(qt[:, 100:128].float() == 0)
+    # Scales by frexp on Python floats (independent of the oracle's exponent
+    # bit arithmetic): the smallest power of two >= fp32(amax * fp32(1/448)).
+    x = rows.float()
+    block_rows = {0: x[0:100], 1: x[100:228], 2: x[228:300]}
+    for b, src in block_rows.items():
+        amax = src.abs().amax(0)
+        for f in range(0, 128, 7):
+            prod = float(np.float32(np.float32(amax[f].item()) * np.float32(1.0 / 448.0)))
+            prod = max(prod, float(np.float32(1e-12)))
+            m, e = math.frexp(prod)
+            want = prod if m == 0.5 else math.ldexp(1.0, e)
+            assert st[b, f].item() == want
+            # amax lands in (224, 448] (saturating at 448)
+            assert 224.0 < amax[f].item() / want <= 448.0 * (1 + 2 ** -20)
+            got = qt[f, 128 * b:128 * b + src.shape[0]].float() * want
+            step = (src[:, f].abs() * 2 ** -3).clamp_min(want * 2 ** -9)
+            assert torch.all((got - src[:, f]).abs() <= step / 2 * (1 + 1e-6))
+    assert torch.all(st[3] == 2.0 ** -39)  # all-zero block: pow2 ceiling of 1e-12
 
 
 # ---------------------------------------------------------------- routing
