@@ -120,6 +120,9 @@ def main():
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--config", default="qwen3_30b_a3b", choices=sorted(CONFIGS))
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--calibration-copy-mib", type=int, default=0,
+                        help="after the timed steps, run one device copy of this many MiB "
+                             "(the known-size kernel that calibrates rocprofv3 byte counters)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
@@ -204,6 +207,14 @@ def main():
         },
         "kernels": per_kernel,
     }
+    if args.calibration_copy_mib > 0:
+        n = args.calibration_copy_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        result["calibration_copy_bytes"] = n
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result))

@@ -84,14 +84,29 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     }
   };
 
+  // XCD-affine order: workgroup b runs on XCD b % 8, and XCD x takes the
+  // x-th eighth of the expert-major tile list (every tile costs the same K
+  // steps), so the N tiles of one row block share its activation rows, and
+  // the row blocks of one expert share its weight panel, in one XCD's L2.
+  // The G/8 workgroups of an XCD take its range round-robin. Needs a grid
+  // that is a multiple of 8; otherwise plain order.
+  const bool affine = (gridDim.x & 7) == 0;
+  const int xcd = blockIdx.x & 7, cu = blockIdx.x >> 3, per_xcd = gridDim.x >> 3;
+  const int first = affine ? (int)((long long)total * xcd / 8) : 0;
+  const int last = affine ? (int)((long long)total * (xcd + 1) / 8) : total;
+  auto tile_at = [&](int r) -> int {
+    if (!affine) return tile_of(r, blockIdx.x, gridDim.x);
+    const int t = first + r * per_xcd + cu;
+    return t < last ? t : total;
+  };
   int round = 0;
-  int tile = tile_of(0, blockIdx.x, gridDim.x);
+  int tile = tile_at(0);
   if (tile >= total) return;
   Tile ct = describe(prefix, offsets, experts, n_tiles, tile);
   issue(ct, 0, 0);
   int stage = 0;
   for (;;) {
-    const int next_tile = tile_of(round + 1, blockIdx.x, gridDim.x);
+    const int next_tile = tile_at(round + 1);
     v4f acc[4][8];
 #pragma unroll
     for (int i = 0; i < 4; ++i)

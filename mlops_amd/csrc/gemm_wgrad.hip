@@ -82,19 +82,55 @@ __global__ void __launch_bounds__(kThreads, 2) wgrad_v2_kernel(
       const uint32_t off = (uint32_t)feature_col(tr, t.nt) * (uint32_t)padded + 16 * ((lane & 7) ^ swz(tr));
       dma16(bbase, off, base + A_BYTES + (wave * B_LOADS + i) * 1024);
     }
-    // Scales of this K block: waves 0-3 the 256 P rows, waves 4-7 the 256 Q
-    // rows in B-tile row order.
+    // Scales of this K block, stored in lane order: LDS slot wm*64 + c*4 + i
+    // holds P row wm*64 + i*16 + c, slot wn*128 + c*8 + jb holds the Q row
+    // of B-tile row wn*128 + jb*16 + c, so that a fragment lane (c = lane %
+    // 16) fetches its 4 row scales and 8 column scales with 16-byte reads.
+    // Waves 0-3 load the P scales, waves 4-7 the Q scales.
     uint8_t* sbase = base + A_BYTES + B_BYTES;
     if (wave < 4) {
-      dma4(p_scale + kblock * Mf + t.mt * BM, 4u * (uint32_t)(wave * 64 + lane), sbase + wave * 256);
+      const int slot = wave * 64 + lane;
+      const int row = (slot & ~63) + (slot & 3) * 16 + ((slot >> 2) & 15);
+      dma4(p_scale + kblock * Mf + t.mt * BM, 4u * (uint32_t)row, sbase + wave * 256);
     } else {
-      dma4(q_scale + kblock * Nf, 4u * (uint32_t)feature_col((wave - 4) * 64 + lane, t.nt),
+      const int slot = (wave - 4) * 64 + lane;
+      const int tr = (slot & ~127) + (slot & 7) * 16 + ((slot >> 3) & 15);
+      dma4(q_scale + kblock * Nf, 4u * (uint32_t)feature_col(tr, t.nt),
            sbase + SA_BYTES + (wave - 4) * 256);
     }
   };
 
+  // XCD-affine order: workgroup b runs on XCD b % 8, and XCD x takes a
+  // contiguous range of the expert-major tile list holding 1/8 of the total
+  // work (a tile costs its expert's K blocks), so an expert's operand panels
+  // are fetched into one or two XCD L2s instead of all eight. The 8 x G/8
+  // workgroups of an XCD take its range round-robin. Needs a grid that is a
+  // multiple of 8; otherwise plain order.
+  const bool affine = (gridDim.x & 7) == 0;
+  const int xcd = blockIdx.x & 7, cu = blockIdx.x >> 3, per_xcd = gridDim.x >> 3;
+  auto range_start = [&](int x) -> int {  // first tile of XCD x's range
+    if (x <= 0) return 0;
+    if (x >= 8) return total;
+    const long long bound = (long long)per_e * prefix[experts] * x / 8;
+    int lo = 0, hi = experts - 1;  // last e with cost before it <= bound
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if ((long long)per_e * prefix[mid] <= bound) lo = mid; else hi = mid - 1;
+    }
+    const int nk = prefix[lo + 1] - prefix[lo];
+    const long long rem = bound - (long long)per_e * prefix[lo];
+    const long long j = nk > 0 ? (rem + nk - 1) / nk : per_e;
+    return lo * per_e + (int)(j < per_e ? j : per_e);
+  };
+  const int first = __builtin_amdgcn_readfirstlane(affine ? range_start(xcd) : 0);
+  const int last = __builtin_amdgcn_readfirstlane(affine ? range_start(xcd + 1) : total);
+  auto tile_at = [&](int r) -> int {
+    if (!affine) return tile_of(r, blockIdx.x, gridDim.x);
+    const int t = first + r * per_xcd + cu;
+    return t < last ? t : total;
+  };
   int round = 0;
-  int tile = tile_of(0, blockIdx.x, gridDim.x);
+  int tile = tile_at(0);
   if (tile >= total) return;
   WTile ct = wdescribe(prefix, per_e, n_tiles, tile);
   bool issued = false;  // whether the current tile's first step is in flight
@@ -102,7 +138,7 @@ __global__ void __launch_bounds__(kThreads, 2) wgrad_v2_kernel(
   for (;;) {
     if (!issued && ct.nk > 0) issue(ct, 0, stage);
     issued = false;
-    const int next_tile = tile_of(round + 1, blockIdx.x, gridDim.x);
+    const int next_tile = tile_at(round + 1);
     v4f acc[4][8];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -125,29 +161,35 @@ __global__ void __launch_bounds__(kThreads, 2) wgrad_v2_kernel(
       const uint8_t* tb = base + A_BYTES;
       const float* sa = (const float*)(base + A_BYTES + B_BYTES);
       const float* sb = sa + BM;
-      v8i af[4];
-      int ea[4];
+      const int c = lane & 15;
+      const float4 sa4 = *(const float4*)&sa[wm * 64 + c * 4];
+      const float4 sb_lo = *(const float4*)&sb[wn * 128 + c * 8];
+      const float4 sb_hi = *(const float4*)&sb[wn * 128 + c * 8 + 4];
+      // Reads in the order the first MFMAs consume them (the step starts
+      // with every wave of the CU reading at once, so what comes first
+      // decides when the matrix cores start), B fragments through a
+      // three-slot ring, read two blocks ahead.
+      v8i af[4], bf[3];
+      bf[0] = frag(tb, wn * 128 + c, lane);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = wm * 64 + i * 16 + (lane & 15);
-        af[i] = frag(ta, row, lane);
-        ea[i] = e8m0(sa[row]);
-      }
-      v8i bcur = frag(tb, wn * 128 + (lane & 15), lane);
-      int ecur = e8m0(sb[wn * 128 + (lane & 15)]);
+      for (int i = 0; i < 4; ++i) af[i] = frag(ta, wm * 64 + i * 16 + c, lane);
+      bf[1] = frag(tb, wn * 128 + 16 + c, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      // Exponent bytes after the fragment reads are in flight: waiting for
+      // the scales then does not hold back the fragment reads.
+      const int ea[4] = {e8m0(sa4.x), e8m0(sa4.y), e8m0(sa4.z), e8m0(sa4.w)};
+      const int eb[8] = {e8m0(sb_lo.x), e8m0(sb_lo.y), e8m0(sb_lo.z), e8m0(sb_lo.w),
+                         e8m0(sb_hi.x), e8m0(sb_hi.y), e8m0(sb_hi.z), e8m0(sb_hi.w)};
 #pragma unroll
       for (int jb = 0; jb < 8; ++jb) {
-        v8i bnext = bcur;
-        int enext = ecur;
-        if (jb < 7) {
-          const int row = wn * 128 + (jb + 1) * 16 + (lane & 15);
-          bnext = frag(tb, row, lane);
-          enext = e8m0(sb[row]);
-        }
+        if (jb + 2 < 8) bf[(jb + 2) % 3] = frag(tb, wn * 128 + (jb + 2) * 16 + c, lane);
+        // Keep the read ahead of this block's MFMAs (the scheduler would
+        // otherwise sink it to shorten live ranges, leaving one group of
+        // MFMAs to cover the LDS latency).
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i][jb] = mfma_e8(af[i], bcur, acc[i][jb], ea[i], ecur);
-        bcur = bnext;
-        ecur = enext;
+        for (int i = 0; i < 4; ++i) acc[i][jb] = mfma_e8(af[i], bf[jb % 3], acc[i][jb], ea[i], eb[jb]);
+        __builtin_amdgcn_sched_barrier(0);
       }
       stage ^= 1;
     }
