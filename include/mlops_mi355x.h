@@ -165,6 +165,30 @@ int mi355x_routed_swiglu_bwd(const void* r, const void* h, const float* weights,
                              const int32_t* order, int rows, int width, float limit, void* dh,
                              void* a_prime, float* dscore, void* stream);
 
+/* Fused routed SwiGLU backward and the quantizers its outputs feed, from
+ * r = dy @ W2 [rows, I] (bf16), h [rows, 2I] interleaved and the route score
+ * of each sorted row (weights[order[row]]), with dh and a' rounded to bf16 as
+ * mi355x_routed_swiglu_bwd stores them:
+ *   dhq, dh_scales: dh row-quantized gate-first, as mi355x_quantize_rows_fp8
+ *                   (gate_up = 1) would from that dh;
+ *   dh_t, dh_t_scales / ap_t, ap_t_scales: dh (gate-first) and a' in the
+ *                   weight-gradient layout of mi355x_quantize_transpose_fp8
+ *                   (each may be NULL, with its scales, to skip it);
+ *   dscore[rows]:   <r, act> per sorted row (fp32, summed per 128 columns in
+ *                   a fixed order).
+ * workspace: mi355x_swiglu_bwd_quantize_workspace_size(rows, I) bytes. Replaces
+ * the dSwiGLU epilogue of block_fp8_gemm's dgrad-down (kernels/quack_moe/
+ * block_fp8_gemm.py:1215-1258, :1520) with the row quantizer of
+ * quantize_rows.py:140 and the transposing quantizer of quantize_transpose.py
+ * :126 fused behind it: one read of r and h instead of four passes. */
+size_t mi355x_swiglu_bwd_quantize_workspace_size(int rows, int width);
+int mi355x_swiglu_bwd_quantize(const void* r, const void* h, const float* weights,
+                               const int32_t* order, const int32_t* offsets, int experts,
+                               int rows, int width, int padded, float limit, uint8_t* dhq,
+                               float* dh_scales, uint8_t* dh_t, float* dh_t_scales,
+                               uint8_t* ap_t, float* ap_t_scales, float* dscore,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------- GEMMs ---- */
 
 /* Ragged grouped block-FP8 GEMM, fp8 MFMA with fp32 accumulation:

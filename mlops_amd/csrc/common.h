@@ -55,6 +55,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
+// Streaming 16-byte store (non-temporal): for GEMM outputs, which are far
+// larger than L2 and are not re-read by the kernel writing them; keeps them
+// from evicting the operand panels other workgroups are about to read.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store_stream(void* p, uint4 v) {
+  __builtin_nontemporal_store((u32x4_t){v.x, v.y, v.z, v.w}, (u32x4_t*)p);
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return (uint16_t)(pack_bf16x2(f, 0.0f) & 0xffffu);
 }

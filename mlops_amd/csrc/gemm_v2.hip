@@ -207,7 +207,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
           o.y = pack_bf16x2(v[2], v[3]);
           o.z = pack_bf16x2(v[4], v[5]);
           o.w = pack_bf16x2(v[6], v[7]);
-          *(uint4*)(obase + off) = o;
+          store_stream(obase + off, o);
         }
       }
     }

@@ -205,15 +205,15 @@ __global__ void __launch_bounds__(kThreads, 2) wgrad_v2_kernel(
         const size_t off = (row0 + lrow) * Nf + col0;
         if (out_fp32) {
           float* o = (float*)out + off;
-          *(float4*)o = make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
-          *(float4*)(o + 4) = make_float4(acc[i][4][r], acc[i][5][r], acc[i][6][r], acc[i][7][r]);
+          store_stream(o, make_uint4(__float_as_uint(acc[i][0][r]), __float_as_uint(acc[i][1][r]), __float_as_uint(acc[i][2][r]), __float_as_uint(acc[i][3][r])));
+          store_stream(o + 4, make_uint4(__float_as_uint(acc[i][4][r]), __float_as_uint(acc[i][5][r]), __float_as_uint(acc[i][6][r]), __float_as_uint(acc[i][7][r])));
         } else {
           uint4 o;
           o.x = pack_bf16x2(acc[i][0][r], acc[i][1][r]);
           o.y = pack_bf16x2(acc[i][2][r], acc[i][3][r]);
           o.z = pack_bf16x2(acc[i][4][r], acc[i][5][r]);
           o.w = pack_bf16x2(acc[i][6][r], acc[i][7][r]);
-          *(uint4*)((uint16_t*)out + off) = o;
+          store_stream((uint16_t*)out + off, o);
         }
       }
     }

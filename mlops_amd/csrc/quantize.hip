@@ -413,6 +413,214 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
   if (lane == 0) dscore[row] = dot;
 }
 
+
+// ---------------------------------------------------------------------------
+// Fused routed SwiGLU backward + every quantizer its outputs feed. Block =
+// (padded 128-row block pb, 128 columns cb of I), 512 threads. Per block:
+//  1. r [128 rows x 128 j] and the matching interleaved h are read once; dh
+//     (gate, up) and a' are computed as in routed_swiglu_bwd_kernel and
+//     rounded to bf16 (the values the unfused path stores);
+//  2. dh rows are quantized 1x128 (gate block cb and up block I/128 + cb of
+//     the gate-first layout) by 16-lane groups, straight from registers;
+//  3. the per-row score dot over these 128 j goes to dsp[cb][row] (summed in
+//     a fixed order by dscore_reduce_kernel);
+//  4. the three bf16 tiles are staged in LDS and written transposed (dh
+//     features cb*128 + j and I + cb*128 + j, a' features cb*128 + j) with
+//     power-of-two scales, as quantize_transpose_kernel does.
+constexpr int kSbThreads = 512;
+
+// Every thread of the block calls this (it holds a barrier); `active` ones
+// (t in [0, 256): 4 features fg x 16 rows rb) do the work.
+__device__ __forceinline__ void transpose_tile_pow2(bool active, const uint16_t* tile,
+                                                    float (*pmax)[128], int t, uint8_t* qt,
+                                                    float* scales, int feat0, int width_f,
+                                                    int padded, int pb) {
+  const int fg = t & 31, rb = t >> 5;
+  float v[16][4];
+  float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (active) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint2 d = *(const uint2*)&tile[(rb * 16 + i) * kQtPitch + 4 * fg];
+    v[i][0] = bf16_to_f32(d.x & 0xffff);
+    v[i][1] = bf16_to_f32(d.x >> 16);
+    v[i][2] = bf16_to_f32(d.y & 0xffff);
+    v[i][3] = bf16_to_f32(d.y >> 16);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m[j] = fmaxf(m[j], fabsf(v[i][j]));
+  }
+  *(float4*)&pmax[rb][4 * fg] = make_float4(m[0], m[1], m[2], m[3]);
+  }
+  __syncthreads();
+  if (!active) return;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const float4 q = *(const float4*)&pmax[r][4 * fg];
+    m[0] = fmaxf(m[0], q.x);
+    m[1] = fmaxf(m[1], q.y);
+    m[2] = fmaxf(m[2], q.z);
+    m[3] = fmaxf(m[3], q.w);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int feat = feat0 + 4 * fg + j;
+    const float sc = pow2_ceil(fmaxf(m[j] * kInv448, kMinScale));
+    const float inv = 1.0f / sc;
+    auto q = [&](int i) { return fminf(fmaxf(v[i][j] * inv, -kE4M3Max), kE4M3Max); };
+    uint4 w;
+    w.x = f32x4_to_e4m3(q(0), q(1), q(2), q(3));
+    w.y = f32x4_to_e4m3(q(4), q(5), q(6), q(7));
+    w.z = f32x4_to_e4m3(q(8), q(9), q(10), q(11));
+    w.w = f32x4_to_e4m3(q(12), q(13), q(14), q(15));
+    *(uint4*)(qt + (size_t)feat * padded + (size_t)pb * 128 + rb * 16) = w;
+    if (rb == 0) scales[(size_t)pb * width_f + feat] = sc;
+  }
+}
+
+__global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
+    const uint16_t* __restrict__ rmat, const uint16_t* __restrict__ h,
+    const float* __restrict__ weights, const int32_t* __restrict__ order,
+    const int32_t* __restrict__ offsets, int experts, int rows, int width, int padded,
+    float limit, uint8_t* __restrict__ dhq, float* __restrict__ dhs, uint8_t* __restrict__ dht,
+    float* __restrict__ dhts, uint8_t* __restrict__ apt, float* __restrict__ apts,
+    float* __restrict__ dsp) {
+  __shared__ int ptile[1025];
+  __shared__ int scan[kSbThreads];
+  __shared__ __align__(16) uint16_t tiles[3][128 * kQtPitch];  // dgate, dup, a'
+  __shared__ __align__(16) float pmax[2][8][128];
+  const int pb = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
+  // Padded 128-row block prefix over experts (thread t owns experts 2t, 2t+1).
+  int local[2], sum = 0;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = tid * 2 + j;
+    local[j] = e < experts ? (offsets[e + 1] - offsets[e] + 127) >> 7 : 0;
+    sum += local[j];
+  }
+  scan[tid] = sum;
+  __syncthreads();
+  for (int o = 1; o < kSbThreads; o <<= 1) {
+    const int v = tid >= o ? scan[tid - o] : 0;
+    __syncthreads();
+    scan[tid] += v;
+    __syncthreads();
+  }
+  int run = scan[tid] - sum;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = tid * 2 + j;
+    if (e <= experts) ptile[e] = run;
+    run += local[j];
+  }
+  if (tid == kSbThreads - 1 && experts == 1024) ptile[1024] = run;
+  __syncthreads();
+  if (pb >= ptile[experts]) return;
+  int lo = 0, hi = experts - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (ptile[mid] <= pb) lo = mid; else hi = mid - 1;
+  }
+  const int r0 = offsets[lo] + (pb - ptile[lo]) * 128;
+  const int nvalid = min(128, offsets[lo + 1] - r0);
+
+  // Phases 1-3: 16 lanes per row (8 j each), 32 rows per pass.
+  const int lane16 = tid & 15, rsub = tid >> 4;
+  const int jl = lane16 * 8, j = cb * 128 + jl;
+  const int nblk = width / 128;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int rr = pass * 32 + rsub;
+    const bool valid = rr < nvalid;  // uniform over the 16-lane group
+    uint4 og = make_uint4(0, 0, 0, 0), ou = og, oa = og;
+    if (valid) {
+      const int row = r0 + rr;
+      const float score = weights[order[row]];
+      float a[8], b[8], rv[8];
+      load_bf16x8(h + (size_t)row * 2 * width + 2 * j, a);
+      load_bf16x8(h + (size_t)row * 2 * width + 2 * j + 8, b);
+      load_bf16x8(rmat + (size_t)row * width + j, rv);
+      float dg[8], du[8], ap[8], dot = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float rg = i < 4 ? a[2 * i] : b[2 * (i - 4)];
+        const float ru = i < 4 ? a[2 * i + 1] : b[2 * (i - 4) + 1];
+        float gv = rg, uv = ru;
+        clamp_gate_up(gv, uv, limit);
+        const float sig = sigmoid_f(gv);
+        const float silu = gv * sig;
+        const float act = silu * uv;
+        dot += rv[i] * act;
+        const float gg = rv[i] * score;
+        float dgate = gg * uv * (sig + silu * (1.0f - sig));
+        float dup = gg * silu;
+        if (limit > 0.0f) {
+          dgate = rg <= limit ? dgate : 0.0f;
+          dup = (ru >= -limit && ru <= limit) ? dup : 0.0f;
+        }
+        dg[i] = dgate;
+        du[i] = dup;
+        ap[i] = act * score;
+      }
+      og = make_uint4(pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3]),
+                      pack_bf16x2(dg[4], dg[5]), pack_bf16x2(dg[6], dg[7]));
+      ou = make_uint4(pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3]),
+                      pack_bf16x2(du[4], du[5]), pack_bf16x2(du[6], du[7]));
+      oa = make_uint4(pack_bf16x2(ap[0], ap[1]), pack_bf16x2(ap[2], ap[3]),
+                      pack_bf16x2(ap[4], ap[5]), pack_bf16x2(ap[6], ap[7]));
+      // Row quantization of the bf16 values (gate-first 1x128 layout).
+      float gq[8], uq[8];
+      const uint32_t gw[4] = {og.x, og.y, og.z, og.w}, uw[4] = {ou.x, ou.y, ou.z, ou.w};
+      float ga = 0.0f, ua = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        gq[2 * i] = bf16_to_f32(gw[i] & 0xffff);
+        gq[2 * i + 1] = bf16_to_f32(gw[i] >> 16);
+        uq[2 * i] = bf16_to_f32(uw[i] & 0xffff);
+        uq[2 * i + 1] = bf16_to_f32(uw[i] >> 16);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        ga = fmaxf(ga, fabsf(gq[i]));
+        ua = fmaxf(ua, fabsf(uq[i]));
+      }
+      ga = group_max<16>(ga);
+      ua = group_max<16>(ua);
+      dot = group_sum<16>(dot);
+      const float sg = fmaxf(ga * kInv448, kMinScale), su = fmaxf(ua * kInv448, kMinScale);
+      *(uint2*)(dhq + (size_t)row * 2 * width + j) = quant8(gq, sg);
+      *(uint2*)(dhq + (size_t)row * 2 * width + width + j) = quant8(uq, su);
+      if (lane16 == 0) {
+        dhs[(size_t)cb * rows + row] = sg;
+        dhs[(size_t)(nblk + cb) * rows + row] = su;
+        dsp[(size_t)cb * rows + row] = dot;
+      }
+    }
+    *(uint4*)&tiles[0][rr * kQtPitch + jl] = og;
+    *(uint4*)&tiles[1][rr * kQtPitch + jl] = ou;
+    *(uint4*)&tiles[2][rr * kQtPitch + jl] = oa;
+  }
+  if (dht == nullptr && apt == nullptr) return;
+  __syncthreads();
+  // Phase 4: transposed outputs; threads 0-255 and 256-511 each take a tile.
+  const int half = tid >> 8, t = tid & 255;
+  if (dht != nullptr)
+    transpose_tile_pow2(true, tiles[half], pmax[half], t, dht, dhts, half * width + cb * 128,
+                        2 * width, padded, pb);
+  if (apt != nullptr) {
+    __syncthreads();  // pmax[0] reuse
+    transpose_tile_pow2(half == 0, tiles[2], pmax[0], t, apt, apts, cb * 128, width, padded, pb);
+  }
+}
+
+__global__ void __launch_bounds__(256) dscore_reduce_kernel(const float* __restrict__ dsp,
+                                                            int rows, int nblk,
+                                                            float* __restrict__ dscore) {
+  const int row = blockIdx.x * 256 + threadIdx.x;
+  if (row >= rows) return;
+  float s = 0.0f;
+  for (int b = 0; b < nblk; ++b) s += dsp[(size_t)b * rows + row];
+  dscore[row] = s;
+}
+
 }  // namespace
 
 extern "C" int mi355x_quantize_weight_blocks(const void* w, int is_fp32, int experts, int out,
@@ -501,6 +709,40 @@ extern "C" int mi355x_routed_swiglu_bwd(const void* r, const void* h, const floa
   hipLaunchKernelGGL(routed_swiglu_bwd_kernel, dim3((rows + 3) / 4), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)r, (const uint16_t*)h, weights, order,
                      rows, width, limit, (uint16_t*)dh, (uint16_t*)a_prime, dscore);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" size_t mi355x_swiglu_bwd_quantize_workspace_size(int rows, int width) {
+  return (size_t)rows * (size_t)(width / 128) * sizeof(float);
+}
+
+extern "C" int mi355x_swiglu_bwd_quantize(const void* r, const void* h, const float* weights,
+                                          const int32_t* order, const int32_t* offsets,
+                                          int experts, int rows, int width, int padded,
+                                          float limit, uint8_t* dhq, float* dh_scales,
+                                          uint8_t* dh_t, float* dh_t_scales, uint8_t* ap_t,
+                                          float* ap_t_scales, float* dscore, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= 1024, "swiglu_bwd_quantize: experts must be in [1, 1024]");
+  MI355X_REQUIRE(width > 0 && width % 128 == 0, "swiglu_bwd_quantize: I must be a multiple of 128");
+  MI355X_REQUIRE(padded % 128 == 0 && (size_t)padded >= mi355x_wgrad_padded_rows(rows, experts),
+                 "swiglu_bwd_quantize: padded must be a multiple of 128 >= mi355x_wgrad_padded_rows");
+  MI355X_REQUIRE((dh_t == nullptr) == (dh_t_scales == nullptr) &&
+                     (ap_t == nullptr) == (ap_t_scales == nullptr),
+                 "swiglu_bwd_quantize: transposed outputs need their scales");
+  MI355X_REQUIRE(workspace_bytes >= mi355x_swiglu_bwd_quantize_workspace_size(rows, width),
+                 "swiglu_bwd_quantize: workspace too small");
+  if (rows == 0) return MI355X_OK;
+  hipStream_t s = (hipStream_t)stream;
+  float* dsp = (float*)workspace;
+  hipLaunchKernelGGL(swiglu_bwd_quantize_kernel, dim3(padded / 128, width / 128), dim3(kSbThreads),
+                     0, s, (const uint16_t*)r, (const uint16_t*)h, weights, order, offsets,
+                     experts, rows, width, padded, limit, dhq, dh_scales, dh_t, dh_t_scales, ap_t,
+                     ap_t_scales, dsp);
+  MI355X_LAUNCH_CHECK();
+  hipLaunchKernelGGL(dscore_reduce_kernel, dim3((rows + 255) / 256), dim3(256), 0, s, dsp, rows,
+                     width / 128, dscore);
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
 }

@@ -363,6 +363,38 @@ def routed_swiglu_backward(r, h, weights, order, limit=None):
     return dh, a_prime, dscore
 
 
+def swiglu_bwd_quantize(r, h, weights, order, offsets, *, padded=None, limit=None,
+                        transposed_dh=True, transposed_ap=True):
+    """Fused routed SwiGLU backward + quantizers (see the C header):
+    ``(dhq [A,2I] e4m3 gate-first, dh_scales [2I/128, A], dh_t [2I, P] | None,
+    dh_t_scales [P/128, 2I] | None, ap_t [I, P] | None, ap_t_scales [P/128, I]
+    | None, dscore fp32 [A], P)``."""
+    rows, width = r.shape
+    _check(h, (rows, 2 * width), torch.bfloat16, "h")
+    experts = offsets.numel() - 1
+    device = _on_gpu(r, h, weights, order, offsets)
+    if padded is None:
+        padded = wgrad_padded_rows(rows, experts)
+    dhq = torch.empty((rows, 2 * width), dtype=FP8, device=device)
+    dhs = torch.empty((2 * width // 128, rows), dtype=torch.float32, device=device)
+    dht = dhts = apt = apts = None
+    if transposed_dh:
+        dht = torch.empty((2 * width, padded), dtype=FP8, device=device)
+        dhts = torch.empty((padded // 128, 2 * width), dtype=torch.float32, device=device)
+    if transposed_ap:
+        apt = torch.empty((width, padded), dtype=FP8, device=device)
+        apts = torch.empty((padded // 128, width), dtype=torch.float32, device=device)
+    dscore = torch.empty(rows, dtype=torch.float32, device=device)
+    nbytes = _native.query("mi355x_swiglu_bwd_quantize_workspace_size", rows, width)
+    work = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+    traffic = 6 * rows * width + 2 * rows * width + (3 * width * padded if rows else 0)
+    _timed("swiglu_bwd_quantize", device, 0, traffic, "mi355x_swiglu_bwd_quantize", _ptr(r),
+           _ptr(h), _ptr(weights), _ptr(order), _ptr(offsets), experts, rows, width, int(padded),
+           _limit(limit), _ptr(dhq), _ptr(dhs), _ptr(dht), _ptr(dhts), _ptr(apt), _ptr(apts),
+           _ptr(dscore), _ptr(work), nbytes, _stream(device))
+    return dhq, dhs, dht, dhts, apt, apts, dscore, padded
+
+
 # ------------------------------------------------------------------- GEMMs
 def gemm(a, a_scale, w, w_scale, offsets, *, transposed_scale=False, interleave=False,
          addend=None):

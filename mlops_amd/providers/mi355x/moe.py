@@ -19,7 +19,7 @@ Forward (sorted rows ``A = T * k``):
   out = residual + sum_j w * y[slot]          token-parallel combine
 Backward:
   r = gemm(quant(dy)[slots], W2^T)            input gradient through W2
-  dh, a', dscore = routed_swiglu_bwd(r, h)
+  dh, a', dscore = swiglu_bwd_quantize(r, h)  fused: quant(dh), dh^T, a'^T
   dW2 = wgrad(dy^T, a'^T), dW13 = wgrad(dh^T, x^T)   fp8 wgrad, 128-row blocks
   dx = gemm(quant(dh), W13^T); grad_x = sum_j dx[slot] + grad_logits @ Wr
   grad_logits = router_bwd(dscore[slots], aux / prob-sum cotangents)
@@ -202,27 +202,26 @@ def backward_routed(
         dyq, dys = kernels.permute_quantize(dy, slots)
         w2_t = kernels.transpose_fp8(w2_data)
         r = kernels.gemm(dyq, dys, w2_t, w2_scale, offsets, transposed_scale=True)
-        dh, a_prime, dscore = kernels.routed_swiglu_backward(
-            r, h13, route_weights.reshape(-1), order, swiglu_limit
+        # SwiGLU backward fused with the quantizers of its outputs: dh row-
+        # quantized for the input gradient, dh and a' transposed for the
+        # weight gradients (each only when that gradient is wanted).
+        dhq, dhs, dh_t, dh_ts, ap_t, ap_ts, dscore, padded = kernels.swiglu_bwd_quantize(
+            r, h13, route_weights.reshape(-1), order, offsets, limit=swiglu_limit,
+            transposed_dh=need_w13, transposed_ap=need_w2,
         )
-        padded = kernels.wgrad_padded_rows(assignments, experts)
         if need_w2:
             dy_t, dy_ts, _ = kernels.quantize_transpose(
                 dy, offsets, assignments, gather=order, gather_div=int(top_k), padded=padded
             )
-            ap_t, ap_ts, _ = kernels.quantize_transpose(a_prime, offsets, assignments, padded=padded)
             grad_w2 = _grad_at(kernels.wgrad(dy_t, dy_ts, ap_t, ap_ts, offsets, out_dtype=direct,
                                              rows=assignments),
                                weight_grad_dtype)
         else:
             grad_w2 = skipped_gradient(h2, weight_grad_dtype)
         # Through the up projection: dx = dh @ W13 (gate rows, then up rows).
-        dhq, dhs = kernels.quantize_rows(dh, gate_up=True)
         w13_t = kernels.transpose_fp8(w13_data)
         dx = kernels.gemm(dhq, dhs, w13_t, w13_scale, offsets, transposed_scale=True)
         if need_w13:
-            dh_t, dh_ts, _ = kernels.quantize_transpose(dh, offsets, assignments, gate_up=True,
-                                                        padded=padded)
             x_t, x_ts, _ = kernels.quantize_transpose(
                 x, offsets, assignments, gather=order, gather_div=int(top_k), padded=padded
             )

@@ -332,3 +332,40 @@ def test_routed_swiglu_backward(device, limit):
     assert max_rel(ds.cpu(), ods) < 1e-4
     assert max_rel(dh.cpu().float(), odh) < 1e-2
     assert max_rel(ap.cpu().float(), oap) < 1e-2
+
+
+@pytest.mark.parametrize("limit", [None, 0.7])
+def test_swiglu_bwd_quantize_matches_unfused(device, limit):
+    """The fused kernel's outputs are, byte for byte, the unfused kernels'
+    (routed SwiGLU backward -> bf16 dh / a' -> row and transposing quantizers),
+    which the tests above pin to the oracle; dscore to summation order."""
+    g = torch.Generator().manual_seed(33)
+    experts, top_k, tokens, width = 6, 2, 700, 384
+    ids = torch.stack([torch.randperm(experts, generator=g)[:top_k] for _ in range(tokens)]).int()
+    ids[ids == 3] = 4  # an empty expert
+    order, offsets, slots = O.sort_assignments(ids, experts)
+    rows = tokens * top_k
+    r = torch.randn(rows, width, generator=g).to(torch.bfloat16).to(device)
+    h = torch.randn(rows, 2 * width, generator=g).to(torch.bfloat16).to(device)
+    h[5] *= 50.0  # a row past the clamp limit
+    weights = torch.rand(tokens * top_k, generator=g).to(device)
+    order_d, offsets_d = order.to(device), offsets.to(device)
+    dhq, dhs, dht, dhts, apt, apts, ds, padded = K.swiglu_bwd_quantize(
+        r, h, weights, order_d, offsets_d, limit=limit)
+    dh, ap, ds_ref = K.routed_swiglu_backward(r, h, weights, order_d, limit)
+    q_ref, s_ref = K.quantize_rows(dh, gate_up=True)
+    assert torch.equal(_bytes(dhq), _bytes(q_ref))
+    assert torch.equal(dhs, s_ref)
+    t_ref, ts_ref, _ = K.quantize_transpose(dh, offsets_d, rows, gate_up=True, padded=padded)
+    a_ref, as_ref, _ = K.quantize_transpose(ap, offsets_d, rows, padded=padded)
+    total = O.padded_layout(offsets)[1]
+    assert torch.equal(_bytes(dht)[:, :total], _bytes(t_ref)[:, :total])
+    assert torch.equal(dhts[: total // 128], ts_ref[: total // 128])
+    assert torch.equal(_bytes(apt)[:, :total], _bytes(a_ref)[:, :total])
+    assert torch.equal(apts[: total // 128], as_ref[: total // 128])
+    assert max_rel(ds.cpu(), ds_ref.cpu()) < 1e-5
+    # Transposed outputs skipped: the row outputs are unchanged.
+    dhq2, dhs2, dht2, _, apt2, _, _, _ = K.swiglu_bwd_quantize(
+        r, h, weights, order_d, offsets_d, limit=limit, transposed_dh=False, transposed_ap=False)
+    assert dht2 is None and apt2 is None
+    assert torch.equal(_bytes(dhq2), _bytes(dhq)) and torch.equal(dhs2, dhs)
