@@ -112,6 +112,42 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+// Exclusive prefix over experts of their padded 128-row block counts,
+// ceil(rows_e / 128), into ptile[0..experts] (ptile[experts] = total), for a
+// block of THREADS threads: a 64-lane scan per wave plus one pass over the
+// wave totals per THREADS experts. wsum: THREADS / 64 ints of scratch.
+template <int THREADS>
+__device__ inline void padded_block_prefix(const int32_t* __restrict__ offsets, int experts,
+                                           int* ptile, int* wsum) {
+  constexpr int kWaves = THREADS / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int carry = 0;
+  for (int base = 0; base < experts; base += THREADS) {
+    const int e = base + tid;
+    const int v = e < experts ? (offsets[e + 1] - offsets[e] + 127) >> 7 : 0;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const int t = wsum[w];
+      before += w < wave ? t : 0;
+      total += t;
+    }
+    if (e < experts) ptile[e] = carry + before + x - v;
+    carry += total;
+    __syncthreads();
+  }
+  if (tid == 0) ptile[experts] = carry;
+  __syncthreads();
+}
+
 // Max over aligned groups of `width` lanes (width a power of two <= 64).
 template <int W>
 __device__ __forceinline__ float group_max(float v) {

@@ -16,6 +16,15 @@ __device__ __forceinline__ void load_bf16x8(const uint16_t* p, float* v) {
   }
 }
 
+__device__ __forceinline__ void unpack_bf16x8(uint4 r, float* v) {
+  const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16_to_f32(w4[i] & 0xffff);
+    v[2 * i + 1] = bf16_to_f32(w4[i] >> 16);
+  }
+}
+
 __device__ __forceinline__ uint2 quant8(const float* v, float s) {
   uint32_t lo = f32x4_to_e4m3(quant_div(v[0], s), quant_div(v[1], s), quant_div(v[2], s),
                               quant_div(v[3], s));
@@ -258,36 +267,11 @@ __global__ void __launch_bounds__(256) quantize_transpose_kernel(
     int gather_div, int gate_up, const int32_t* __restrict__ offsets, int experts, int padded,
     uint8_t* __restrict__ qt, float* __restrict__ scales) {
   __shared__ int ptile[1025];
-  __shared__ int scan[256];
+  __shared__ int scan[4];
   __shared__ __align__(16) uint16_t tile[128 * kQtPitch];
   __shared__ __align__(16) float pmax[8][128];
   const int pb = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
-  // Padded 128-row block prefix over experts (exclusive): thread t owns
-  // experts 4t .. 4t + 3.
-  int local[4], sum = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = tid * 4 + j;
-    local[j] = e < experts ? (offsets[e + 1] - offsets[e] + 127) >> 7 : 0;
-    sum += local[j];
-  }
-  scan[tid] = sum;
-  __syncthreads();
-  for (int o = 1; o < 256; o <<= 1) {
-    const int v = tid >= o ? scan[tid - o] : 0;
-    __syncthreads();
-    scan[tid] += v;
-    __syncthreads();
-  }
-  int run = scan[tid] - sum;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = tid * 4 + j;
-    if (e <= experts) ptile[e] = run;
-    run += local[j];
-  }
-  if (tid == 255 && experts == 1024) ptile[1024] = run;
-  __syncthreads();
+  padded_block_prefix<256>(offsets, experts, ptile, scan);
   if (pb >= ptile[experts]) return;
   int lo = 0, hi = experts - 1;
   while (lo < hi) {  // last e with ptile[e] <= pb
@@ -424,7 +408,7 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
 //     the gate-first layout) by 16-lane groups, straight from registers;
 //  3. the per-row score dot over these 128 j goes to dsp[cb][row] (summed in
 //     a fixed order by dscore_reduce_kernel);
-//  4. the three bf16 tiles are staged in LDS and written transposed (dh
+//  4. the three bf16 tiles are staged in LDS (a' after dh) and written transposed (dh
 //     features cb*128 + j and I + cb*128 + j, a' features cb*128 + j) with
 //     power-of-two scales, as quantize_transpose_kernel does.
 constexpr int kSbThreads = 512;
@@ -484,36 +468,15 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
     float limit, uint8_t* __restrict__ dhq, float* __restrict__ dhs, uint8_t* __restrict__ dht,
     float* __restrict__ dhts, uint8_t* __restrict__ apt, float* __restrict__ apts,
     float* __restrict__ dsp) {
-  __shared__ int ptile[1025];
-  __shared__ int scan[kSbThreads];
-  __shared__ __align__(16) uint16_t tiles[3][128 * kQtPitch];  // dgate, dup, a'
+  // dgate and dup tiles (a' is staged through tile 0 afterwards); the expert
+  // prefix lives in tile 1 until the tiles are written: ~78 KB, two blocks
+  // per CU.
+  __shared__ __align__(16) uint16_t tiles[2][128 * kQtPitch];
   __shared__ __align__(16) float pmax[2][8][128];
+  __shared__ int wsum[kSbThreads / 64];
+  int* ptile = (int*)tiles[1];
   const int pb = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
-  // Padded 128-row block prefix over experts (thread t owns experts 2t, 2t+1).
-  int local[2], sum = 0;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int e = tid * 2 + j;
-    local[j] = e < experts ? (offsets[e + 1] - offsets[e] + 127) >> 7 : 0;
-    sum += local[j];
-  }
-  scan[tid] = sum;
-  __syncthreads();
-  for (int o = 1; o < kSbThreads; o <<= 1) {
-    const int v = tid >= o ? scan[tid - o] : 0;
-    __syncthreads();
-    scan[tid] += v;
-    __syncthreads();
-  }
-  int run = scan[tid] - sum;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int e = tid * 2 + j;
-    if (e <= experts) ptile[e] = run;
-    run += local[j];
-  }
-  if (tid == kSbThreads - 1 && experts == 1024) ptile[1024] = run;
-  __syncthreads();
+  padded_block_prefix<kSbThreads>(offsets, experts, ptile, wsum);
   if (pb >= ptile[experts]) return;
   int lo = 0, hi = experts - 1;
   while (lo < hi) {
@@ -522,22 +485,40 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
   }
   const int r0 = offsets[lo] + (pb - ptile[lo]) * 128;
   const int nvalid = min(128, offsets[lo + 1] - r0);
+  __syncthreads();  // ptile (in tile 1) is dead from here on
 
-  // Phases 1-3: 16 lanes per row (8 j each), 32 rows per pass.
+  // Phases 1-3: 16 lanes per row (8 j each), 32 rows per pass, 4 passes;
+  // every pass's loads are issued before any compute (memory parallelism).
   const int lane16 = tid & 15, rsub = tid >> 4;
   const int jl = lane16 * 8, j = cb * 128 + jl;
   const int nblk = width / 128;
+  uint4 hv0[4], hv1[4], rv4[4], apk[4];
+  float score[4];
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int rr = pass * 32 + rsub;
+    hv0[pass] = hv1[pass] = rv4[pass] = make_uint4(0, 0, 0, 0);
+    score[pass] = 0.0f;
+    if (rr < nvalid) {
+      const int row = r0 + rr;
+      const uint16_t* hp = h + (size_t)row * 2 * width + 2 * j;
+      hv0[pass] = *(const uint4*)hp;
+      hv1[pass] = *(const uint4*)(hp + 8);
+      rv4[pass] = *(const uint4*)(rmat + (size_t)row * width + j);
+      score[pass] = weights[order[row]];
+    }
+  }
+#pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int rr = pass * 32 + rsub;
     const bool valid = rr < nvalid;  // uniform over the 16-lane group
     uint4 og = make_uint4(0, 0, 0, 0), ou = og, oa = og;
     if (valid) {
       const int row = r0 + rr;
-      const float score = weights[order[row]];
       float a[8], b[8], rv[8];
-      load_bf16x8(h + (size_t)row * 2 * width + 2 * j, a);
-      load_bf16x8(h + (size_t)row * 2 * width + 2 * j + 8, b);
-      load_bf16x8(rmat + (size_t)row * width + j, rv);
+      unpack_bf16x8(hv0[pass], a);
+      unpack_bf16x8(hv1[pass], b);
+      unpack_bf16x8(rv4[pass], rv);
       float dg[8], du[8], ap[8], dot = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -549,7 +530,7 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
         const float silu = gv * sig;
         const float act = silu * uv;
         dot += rv[i] * act;
-        const float gg = rv[i] * score;
+        const float gg = rv[i] * score[pass];
         float dgate = gg * uv * (sig + silu * (1.0f - sig));
         float dup = gg * silu;
         if (limit > 0.0f) {
@@ -558,7 +539,7 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
         }
         dg[i] = dgate;
         du[i] = dup;
-        ap[i] = act * score;
+        ap[i] = act * score[pass];
       }
       og = make_uint4(pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3]),
                       pack_bf16x2(dg[4], dg[5]), pack_bf16x2(dg[6], dg[7]));
@@ -568,15 +549,9 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
                       pack_bf16x2(ap[4], ap[5]), pack_bf16x2(ap[6], ap[7]));
       // Row quantization of the bf16 values (gate-first 1x128 layout).
       float gq[8], uq[8];
-      const uint32_t gw[4] = {og.x, og.y, og.z, og.w}, uw[4] = {ou.x, ou.y, ou.z, ou.w};
+      unpack_bf16x8(og, gq);
+      unpack_bf16x8(ou, uq);
       float ga = 0.0f, ua = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        gq[2 * i] = bf16_to_f32(gw[i] & 0xffff);
-        gq[2 * i + 1] = bf16_to_f32(gw[i] >> 16);
-        uq[2 * i] = bf16_to_f32(uw[i] & 0xffff);
-        uq[2 * i + 1] = bf16_to_f32(uw[i] >> 16);
-      }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         ga = fmaxf(ga, fabsf(gq[i]));
@@ -596,7 +571,7 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
     }
     *(uint4*)&tiles[0][rr * kQtPitch + jl] = og;
     *(uint4*)&tiles[1][rr * kQtPitch + jl] = ou;
-    *(uint4*)&tiles[2][rr * kQtPitch + jl] = oa;
+    apk[pass] = oa;
   }
   if (dht == nullptr && apt == nullptr) return;
   __syncthreads();
@@ -606,8 +581,12 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
     transpose_tile_pow2(true, tiles[half], pmax[half], t, dht, dhts, half * width + cb * 128,
                         2 * width, padded, pb);
   if (apt != nullptr) {
-    __syncthreads();  // pmax[0] reuse
-    transpose_tile_pow2(half == 0, tiles[2], pmax[0], t, apt, apts, cb * 128, width, padded, pb);
+    __syncthreads();  // tile 0 and pmax[0] reuse
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass)
+      *(uint4*)&tiles[0][(pass * 32 + rsub) * kQtPitch + jl] = apk[pass];
+    __syncthreads();
+    transpose_tile_pow2(half == 0, tiles[0], pmax[0], t, apt, apts, cb * 128, width, padded, pb);
   }
 }
 
