@@ -143,7 +143,7 @@ def forward_routed(
     width = h2.shape[-1]
     rows = h2.numel() // width
     lengths = _normalized((rows,) if lengths is None else lengths, rows)
-    (w13_data, w13_scale), (w2_data, w2_scale) = w13, w2
+    (w13_data, w13_scale), (w2_data, w2_scale) = w13[:2], w2[:2]
     experts = router_weight.shape[0]
     with torch.no_grad():
         x = h2.reshape(rows, width).contiguous()
@@ -187,7 +187,7 @@ def backward_routed(
     width = h2.shape[-1]
     rows = h2.numel() // width
     lengths = _normalized(lengths, rows)
-    (w13_data, w13_scale), (w2_data, w2_scale) = w13, w2
+    (w13_data, w13_scale), (w2_data, w2_scale) = w13[:2], w2[:2]
     experts = router_weight.shape[0]
     assignments = order.numel()
     router_dtype = router_weight.dtype if weight_grad_dtype is None else weight_grad_dtype
@@ -200,7 +200,7 @@ def backward_routed(
             dy = dy.to(torch.bfloat16)
         # Through the down projection: r = dy_routed @ W2, then SwiGLU backward.
         dyq, dys = kernels.permute_quantize(dy, slots)
-        w2_t = kernels.transpose_fp8(w2_data)
+        w2_t = _transposed(w2, w2_data)
         r = kernels.gemm(dyq, dys, w2_t, w2_scale, offsets, transposed_scale=True)
         # SwiGLU backward fused with the quantizers of its outputs: dh row-
         # quantized for the input gradient, dh and a' transposed for the
@@ -219,7 +219,7 @@ def backward_routed(
         else:
             grad_w2 = skipped_gradient(h2, weight_grad_dtype)
         # Through the up projection: dx = dh @ W13 (gate rows, then up rows).
-        w13_t = kernels.transpose_fp8(w13_data)
+        w13_t = _transposed(w13, w13_data)
         dx = kernels.gemm(dhq, dhs, w13_t, w13_scale, offsets, transposed_scale=True)
         if need_w13:
             x_t, x_ts, _ = kernels.quantize_transpose(
@@ -262,9 +262,22 @@ def backward_routed(
 # ``weight_components`` (the reference's container protocol,
 # providers/sonicmoe/fp8.py:204-236).
 def _split(w13, w2, weight_components):
-    if len(weight_components) != 2:
-        raise ValueError("the block-FP8 operators take the two weights' scales as components")
-    return (w13, weight_components[0]), (w2, weight_components[1])
+    """``((w13, scale[, data_t]), (w2, scale[, data_t]))``: the two scales,
+    optionally followed by the two transposed e4m3 copies the per-call
+    quantizer writes in the same pass (containers built elsewhere have none;
+    the input-gradient GEMMs then transpose on the fly)."""
+    if len(weight_components) == 2:
+        return (w13, weight_components[0]), (w2, weight_components[1])
+    if len(weight_components) == 4:
+        return ((w13, weight_components[0], weight_components[2]),
+                (w2, weight_components[1], weight_components[3]))
+    raise ValueError("the block-FP8 operators take the two weights' scales (and optionally "
+                     "their transposed data) as components")
+
+
+def _transposed(weight, data):
+    """The weight's transposed e4m3 copy: carried along, or made now."""
+    return weight[2] if len(weight) == 3 else kernels.transpose_fp8(data)
 
 
 @torch.library.custom_op("mlops_mi355x::moe_mi355x_block_fp8_fwd", mutates_args=())
@@ -366,10 +379,14 @@ def _container_rule(cls, func, types, args, kwargs):
         raise ValueError("use positional operator arguments")
     args = list(args)
     components = list(args[-1])
+    transposed = []
     for index, value in enumerate(args):
         if isinstance(value, BlockFP8Weight):
             args[index] = value._data
             components.append(value._scale)
+            transposed.append(getattr(value, "_transposed", None))
+    if len(transposed) == 2 and all(t is not None for t in transposed):
+        components.extend(transposed)
     args[-1] = components
     return func(*args)
 
@@ -391,6 +408,10 @@ def _setup_context(ctx, inputs, output):
     ctx.weight_grad_dtype = weight_grad_dtype
     ctx.swiglu_limit = swiglu_limit
     ctx.n_components = len(components)
+    # Unused cotangents arrive as None (the backward builds the small ones it
+    # needs) instead of autograd materializing zeros, h13's 2 bytes x A x 2I
+    # among them.
+    ctx.set_materialize_grads(False)
     ctx.mark_non_differentiable(counts, logits, route_weights, route_ids, order, offsets, slots,
                                 h13)
 
@@ -422,9 +443,27 @@ _forward_op.register_autograd(_autograd_backward, setup_context=_setup_context)
 
 
 # --------------------------------------------------------------------------
+class _QuantizePerCall(torch.autograd.Function):
+    """A plain weight quantized for one call (``BlockFP8Weight.quantize``
+    semantics, straight-through gradient). The same kernel pass also writes
+    the transposed e4m3 copy the input-gradient GEMMs read, carried on the
+    container for the operator (``_transposed``)."""
+
+    @staticmethod
+    def forward(ctx, weight):
+        data, scale, data_t = kernels.quantize_weight_blocks(weight.detach(), transposed=True)
+        container = BlockFP8Weight(data, scale, dtype=weight.dtype)
+        container._transposed = data_t
+        return container
+
+    @staticmethod
+    def backward(ctx, grad):
+        return grad
+
+
 def _containers(w13, w2):
     """Plain weights quantized per call (straight-through); containers as they are."""
-    return tuple(w if isinstance(w, BlockFP8Weight) else BlockFP8Weight.quantize(w)
+    return tuple(w if isinstance(w, BlockFP8Weight) else _QuantizePerCall.apply(w)
                  for w in (w13, w2))
 
 

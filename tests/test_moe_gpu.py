@@ -229,3 +229,32 @@ def test_qwen3_shape_properties(device):
         lengths=(tokens,))
     for gtensor in grads:
         assert torch.isfinite(gtensor.float()).all()
+
+
+def test_per_call_transposed_weights_match_containers_bitwise(device, monkeypatch):
+    """Plain weights quantized per call carry the transposed copies written in
+    the same kernel pass (no transpose in backward); the results equal those
+    of pre-built containers, which transpose on the fly, bit for bit."""
+    from mlops_amd import kernels as K
+
+    calls = []
+    original = K.transpose_fp8
+    monkeypatch.setattr(K, "transpose_fp8", lambda data: calls.append(1) or original(data))
+    x, res, wr, w13, w2, dy = _inputs(device, tokens=256, hidden=256, experts=4, inter=256,
+                                      seed=9)
+    results = []
+    for per_call in (True, False):
+        xg = x.clone().requires_grad_(True)
+        if per_call:
+            a, b = w13.clone().requires_grad_(True), w2.clone().requires_grad_(True)
+        else:
+            a = BlockFP8Weight.quantize(w13).detach().requires_grad_(True)
+            b = BlockFP8Weight.quantize(w2).detach().requires_grad_(True)
+        calls.clear()
+        out, *_ = mlops_amd.moe(xg, res, wr, a, b, top_k=2, routing_mode="topk_then_softmax",
+                                compute_precision="fp8_block")
+        out.backward(dy)
+        assert len(calls) == (0 if per_call else 2)
+        results.append((out, xg.grad, a.grad, b.grad))
+    for u, v in zip(*results):
+        assert torch.equal(u.float(), v.float())
