@@ -12,10 +12,11 @@ constexpr int kMaxExperts = 512;
 // Scalar description of one output tile.
 struct Tile {
   int e, row0, nvalid, nt;
+  int rot;  // K-step rotation: the tile walks K steps rot, rot + 1, ... (mod nk)
 };
 
 __device__ __forceinline__ Tile describe(const int* prefix, const int32_t* __restrict__ offsets,
-                                         int experts, int n_tiles, int tile) {
+                                         int experts, int n_tiles, int tile, int nk) {
   // Every field is wave-uniform; readfirstlane lets the compiler keep them
   // (and everything derived: weight bases, scale addresses) in SGPRs.
   Tile t;
@@ -24,6 +25,11 @@ __device__ __forceinline__ Tile describe(const int* prefix, const int32_t* __res
   t.e = __builtin_amdgcn_readfirstlane(find_expert(prefix, experts, mt));
   t.row0 = __builtin_amdgcn_readfirstlane(offsets[t.e] + (mt - prefix[t.e]) * BM);
   t.nvalid = __builtin_amdgcn_readfirstlane(min(BM, offsets[t.e + 1] - t.row0));
+  // Tiles that share an operand panel run at the same time on neighbouring
+  // CUs of one XCD; starting each at a different K step means one of them
+  // takes a panel step's L2 miss and the others find it in L2 later,
+  // instead of all of them waiting on the same miss together.
+  t.rot = __builtin_amdgcn_readfirstlane((tile * 7) % nk);
   return t;
 }
 
@@ -60,7 +66,8 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
   const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 wave grid
 
   // Direct loads of one K step of tile t into stage `stage`.
-  auto issue = [&](const Tile& t, int kb, int stage) {
+  auto issue = [&](const Tile& t, int step, int stage) {
+    const int kb = __builtin_amdgcn_readfirstlane(step + t.rot < nk ? step + t.rot : step + t.rot - nk);
     uint8_t* base = smem + stage * STAGE_BYTES;
     const size_t koff = (size_t)kb * BK;
     const uint8_t* abase = a + koff;
@@ -78,9 +85,10 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
                            16 * ((lane & 7) ^ swz(tr));
       dma16(bbase, off, base + A_BYTES + (wave * B_LOADS + i) * 1024);
     }
+    const float* sbase = a_scale + (size_t)kb * rows;
     if (lane < 32) {
       const uint32_t off = 4u * (uint32_t)min(t.row0 + wave * 32 + lane, rows - 1);
-      dma4(a_scale + (size_t)kb * rows, off, base + A_BYTES + B_BYTES + wave * 128);
+      dma4(sbase, off, base + A_BYTES + B_BYTES + wave * 128);
     }
   };
 
@@ -102,7 +110,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
   int round = 0;
   int tile = tile_at(0);
   if (tile >= total) return;
-  Tile ct = describe(prefix, offsets, experts, n_tiles, tile);
+  Tile ct = describe(prefix, offsets, experts, n_tiles, tile, nk);
   issue(ct, 0, 0);
   int stage = 0;
   for (;;) {
@@ -122,17 +130,18 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       if (kb + 1 < nk) {
         issue(ct, kb + 1, stage ^ 1);
       } else if (next_tile < total) {
-        const Tile nt = describe(prefix, offsets, experts, n_tiles, next_tile);
+        const Tile nt = describe(prefix, offsets, experts, n_tiles, next_tile, nk);
         issue(nt, 0, stage ^ 1);
       }
       const uint8_t* base = smem + stage * STAGE_BYTES;
       const uint8_t* ta = base;
       const uint8_t* tb = base + A_BYTES;
       const float* sa = (const float*)(base + A_BYTES + B_BYTES);
-      const float sb_lo = w_scale_t ? w_scale[((size_t)ct.e * kbw + kb) * nbw + nb_lo]
-                                    : w_scale[((size_t)ct.e * nbw + nb_lo) * kbw + kb];
-      const float sb_hi = w_scale_t ? w_scale[((size_t)ct.e * kbw + kb) * nbw + nb_hi]
-                                    : w_scale[((size_t)ct.e * nbw + nb_hi) * kbw + kb];
+      const int kbr = __builtin_amdgcn_readfirstlane(kb + ct.rot < nk ? kb + ct.rot : kb + ct.rot - nk);
+      const float sb_lo = w_scale_t ? w_scale[((size_t)ct.e * kbw + kbr) * nbw + nb_lo]
+                                    : w_scale[((size_t)ct.e * nbw + nb_lo) * kbw + kbr];
+      const float sb_hi = w_scale_t ? w_scale[((size_t)ct.e * kbw + kbr) * nbw + nb_hi]
+                                    : w_scale[((size_t)ct.e * nbw + nb_hi) * kbw + kbr];
       v8i af[4];
       float s4[4][4];
 #pragma unroll
@@ -214,7 +223,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     if (next_tile >= total) break;
     ++round;
     tile = next_tile;
-    ct = describe(prefix, offsets, experts, n_tiles, tile);
+    ct = describe(prefix, offsets, experts, n_tiles, tile, nk);
   }
 }
 

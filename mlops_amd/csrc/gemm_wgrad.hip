@@ -37,6 +37,7 @@ __device__ __forceinline__ v4f mfma_e8(v8i a, v8i b, v4f c, int sa, int sb) {
 
 struct WTile {
   int e, mt, nt, k0, nk;  // expert, tile coordinates, first padded block, blocks
+  int rot;                // K-step rotation (see wdescribe)
 };
 
 __device__ __forceinline__ WTile wdescribe(const int* prefix, int per_e, int n_tiles, int tile) {
@@ -47,6 +48,10 @@ __device__ __forceinline__ WTile wdescribe(const int* prefix, int per_e, int n_t
   t.nt = __builtin_amdgcn_readfirstlane(rem - t.mt * n_tiles);
   t.k0 = __builtin_amdgcn_readfirstlane(prefix[t.e]);
   t.nk = __builtin_amdgcn_readfirstlane(prefix[t.e + 1] - prefix[t.e]);
+  // Tiles sharing an operand panel run together on neighbouring CUs; each
+  // starts at a different K step so that one takes a step's L2 miss and the
+  // others hit later instead of all waiting on the same miss.
+  t.rot = t.nk > 0 ? __builtin_amdgcn_readfirstlane((tile * 7) % t.nk) : 0;
   return t;
 }
 
@@ -65,7 +70,8 @@ __global__ void __launch_bounds__(kThreads, 2) wgrad_v2_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 wave grid
 
-  auto issue = [&](const WTile& t, int kb, int stage) {
+  auto issue = [&](const WTile& t, int step, int stage) {
+    const int kb = __builtin_amdgcn_readfirstlane(step + t.rot < t.nk ? step + t.rot : step + t.rot - t.nk);
     uint8_t* base = smem + stage * STAGE_BYTES;
     const size_t kblock = (size_t)(t.k0 + kb);
     const uint8_t* abase = p + kblock * 128;
