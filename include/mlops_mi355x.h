@@ -128,21 +128,31 @@ int mi355x_quantize_weight_blocks(const void* w, int is_fp32, int experts, int o
 int mi355x_transpose_fp8(const uint8_t* q, int experts, int rows, int cols, uint8_t* q_t,
                          void* stream);
 
+/* Padded 128-row block table of the weight-gradient layout: each expert's
+ * sorted rows start at a 128-aligned padded offset; for padded block pb of
+ * padded/128, blocks[2 pb] = its first sorted row and blocks[2 pb + 1] the
+ * number of those rows it holds (1..128; 0 past the last expert's blocks).
+ * Computed once per routing and read by the kernels that write that layout.
+ * No reference counterpart (the reference sizes its transposes per expert on
+ * the host, quack_moe/fp8.py:129-157). */
+size_t mi355x_wgrad_padded_rows(int assignments, int experts);
+int mi355x_padded_row_blocks(const int32_t* offsets, int experts, int padded, int32_t* blocks,
+                             void* stream);
+
 /* Feature-major e4m3 operand of the weight-gradient GEMM: routed rows of x
  * (bf16, row pitch `pitch`; with gather != NULL sorted row r reads source row
  * gather[r] / gather_div) are written transposed, [width][padded], each
- * expert's rows starting at its 128-aligned padded offset, zero filled, with
- * one descale per (feature, 128-row block): max(amax / 448, 1e-12) rounded
- * up to a power of two, so that the weight-gradient GEMM can apply it as an
- * MFMA E8M0 block scale. gate_up de-interleaves columns as in
- * mi355x_quantize_rows_fp8. Replaces quantize_transpose_fp8
- * (kernels/quack_moe/quantize_transpose.py:126-313) with per-128-token
- * power-of-two instead of per-expert fp32 scales. scales: [padded/128][width]. */
-size_t mi355x_wgrad_padded_rows(int assignments, int experts);
+ * padded block pb holding rows row_blocks[2 pb] .. + row_blocks[2 pb + 1]
+ * (mi355x_padded_row_blocks) and zeros after them, with one descale per
+ * (feature, 128-row block): max(amax / 448, 1e-12) rounded up to a power of
+ * two, so that the weight-gradient GEMM can apply it as an MFMA E8M0 block
+ * scale. gate_up de-interleaves columns as in mi355x_quantize_rows_fp8.
+ * Replaces quantize_transpose_fp8 (kernels/quack_moe/quantize_transpose.py
+ * :126-313) with per-128-token power-of-two instead of per-expert fp32
+ * scales. scales: [padded/128][width]. */
 int mi355x_quantize_transpose_fp8(const void* x, int64_t pitch, int width, const int32_t* gather,
-                                  int gather_div, int gate_up, const int32_t* offsets,
-                                  int experts, int assignments, int padded, uint8_t* qt,
-                                  float* scales, void* stream);
+                                  int gather_div, int gate_up, const int32_t* row_blocks,
+                                  int padded, uint8_t* qt, float* scales, void* stream);
 
 /* out[t] = bf16(residual[t] + sum_j weights[t,j] * y[slots[t,j]]), fp32 sum in
  * j order. Replaces combine (moe_dispatch.py:21-72, :168-196). */
@@ -183,8 +193,8 @@ int mi355x_routed_swiglu_bwd(const void* r, const void* h, const float* weights,
  * :126 fused behind it: one read of r and h instead of four passes. */
 size_t mi355x_swiglu_bwd_quantize_workspace_size(int rows, int width);
 int mi355x_swiglu_bwd_quantize(const void* r, const void* h, const float* weights,
-                               const int32_t* order, const int32_t* offsets, int experts,
-                               int rows, int width, int padded, float limit, uint8_t* dhq,
+                               const int32_t* order, const int32_t* row_blocks, int rows,
+                               int width, int padded, float limit, uint8_t* dhq,
                                float* dh_scales, uint8_t* dh_t, float* dh_t_scales,
                                uint8_t* ap_t, float* ap_t_scales, float* dscore,
                                void* workspace, size_t workspace_bytes, void* stream);

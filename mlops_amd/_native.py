@@ -40,17 +40,15 @@ SIGNATURES = {
     "mi355x_quantize_weight_blocks": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P]),
     "mi355x_transpose_fp8": (_I, [_P, _I, _I, _I, _P, _P]),
     "mi355x_wgrad_padded_rows": (_S, [_I, _I]),
-    "mi355x_quantize_transpose_fp8": (
-        _I,
-        [_P, _I64, _I, _P, _I, _I, _P, _I, _I, _I, _P, _P, _P],
-    ),
+    "mi355x_padded_row_blocks": (_I, [_P, _I, _I, _P, _P]),
+    "mi355x_quantize_transpose_fp8": (_I, [_P, _I64, _I, _P, _I, _I, _P, _I, _P, _P, _P]),
     "mi355x_unpermute_combine": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
     "mi355x_unpermute_sum": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "mi355x_routed_swiglu_bwd": (_I, [_P, _P, _P, _P, _I, _I, _F, _P, _P, _P, _P]),
     "mi355x_swiglu_bwd_quantize_workspace_size": (_S, [_I, _I]),
     "mi355x_swiglu_bwd_quantize": (
         _I,
-        [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _P, _S, _P],
+        [_P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _P, _S, _P],
     ),
     "mi355x_gemm_fp8_block": (
         _I,

@@ -264,23 +264,13 @@ constexpr int kQtPitch = 128 + 8;  // bf16 per LDS row: 272 B keeps 16-byte row 
 
 __global__ void __launch_bounds__(256) quantize_transpose_kernel(
     const uint16_t* __restrict__ x, int64_t pitch, int width, const int32_t* __restrict__ gather,
-    int gather_div, int gate_up, const int32_t* __restrict__ offsets, int experts, int padded,
+    int gather_div, int gate_up, const int32_t* __restrict__ row_blocks, int padded,
     uint8_t* __restrict__ qt, float* __restrict__ scales) {
-  __shared__ int ptile[1025];
-  __shared__ int scan[4];
   __shared__ __align__(16) uint16_t tile[128 * kQtPitch];
   __shared__ __align__(16) float pmax[8][128];
   const int pb = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
-  padded_block_prefix<256>(offsets, experts, ptile, scan);
-  if (pb >= ptile[experts]) return;
-  int lo = 0, hi = experts - 1;
-  while (lo < hi) {  // last e with ptile[e] <= pb
-    const int mid = (lo + hi + 1) >> 1;
-    if (ptile[mid] <= pb) lo = mid; else hi = mid - 1;
-  }
-  const int e = lo;
-  const int r0 = offsets[e] + (pb - ptile[e]) * 128;
-  const int nvalid = min(128, offsets[e + 1] - r0);
+  const int r0 = row_blocks[2 * pb], nvalid = row_blocks[2 * pb + 1];
+  if (nvalid <= 0) return;  // past the last expert's rows
   const int c0 = cb * 128;
   // 128 rows x 128 source columns (bf16) into LDS, zeros past the expert.
   {
@@ -464,28 +454,17 @@ __device__ __forceinline__ void transpose_tile_pow2(bool active, const uint16_t*
 __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
     const uint16_t* __restrict__ rmat, const uint16_t* __restrict__ h,
     const float* __restrict__ weights, const int32_t* __restrict__ order,
-    const int32_t* __restrict__ offsets, int experts, int rows, int width, int padded,
-    float limit, uint8_t* __restrict__ dhq, float* __restrict__ dhs, uint8_t* __restrict__ dht,
+    const int32_t* __restrict__ row_blocks, int rows, int width, int padded, float limit,
+    uint8_t* __restrict__ dhq, float* __restrict__ dhs, uint8_t* __restrict__ dht,
     float* __restrict__ dhts, uint8_t* __restrict__ apt, float* __restrict__ apts,
     float* __restrict__ dsp) {
-  // dgate and dup tiles (a' is staged through tile 0 afterwards); the expert
-  // prefix lives in tile 1 until the tiles are written: ~78 KB, two blocks
-  // per CU.
+  // dgate and dup tiles (a' is staged through tile 0 afterwards): ~74 KB,
+  // two blocks per CU.
   __shared__ __align__(16) uint16_t tiles[2][128 * kQtPitch];
   __shared__ __align__(16) float pmax[2][8][128];
-  __shared__ int wsum[kSbThreads / 64];
-  int* ptile = (int*)tiles[1];
   const int pb = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
-  padded_block_prefix<kSbThreads>(offsets, experts, ptile, wsum);
-  if (pb >= ptile[experts]) return;
-  int lo = 0, hi = experts - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (ptile[mid] <= pb) lo = mid; else hi = mid - 1;
-  }
-  const int r0 = offsets[lo] + (pb - ptile[lo]) * 128;
-  const int nvalid = min(128, offsets[lo + 1] - r0);
-  __syncthreads();  // ptile (in tile 1) is dead from here on
+  const int r0 = row_blocks[2 * pb], nvalid = row_blocks[2 * pb + 1];
+  if (nvalid <= 0) return;  // past the last expert's rows
 
   // Phases 1-3: 16 lanes per row (8 j each), 32 rows per pass, 4 passes;
   // every pass's loads are issued before any compute (memory parallelism).
@@ -600,6 +579,31 @@ __global__ void __launch_bounds__(256) dscore_reduce_kernel(const float* __restr
   dscore[row] = s;
 }
 
+// Padded 128-row block table of the weight-gradient layout: block pb ->
+// (first sorted row, valid rows), valid = 0 past the last expert's blocks.
+// Computed once per layout so the per-block kernels above need one load
+// instead of an expert scan and search each.
+__global__ void __launch_bounds__(1024) padded_row_blocks_kernel(
+    const int32_t* __restrict__ offsets, int experts, int nblocks, int32_t* __restrict__ blocks) {
+  __shared__ int ptile[1025];
+  __shared__ int wsum[16];
+  padded_block_prefix<1024>(offsets, experts, ptile, wsum);
+  for (int pb = threadIdx.x; pb < nblocks; pb += 1024) {
+    int r0 = 0, nvalid = 0;
+    if (pb < ptile[experts]) {
+      int lo = 0, hi = experts - 1;
+      while (lo < hi) {  // last e with ptile[e] <= pb
+        const int mid = (lo + hi + 1) >> 1;
+        if (ptile[mid] <= pb) lo = mid; else hi = mid - 1;
+      }
+      r0 = offsets[lo] + (pb - ptile[lo]) * 128;
+      nvalid = min(128, offsets[lo + 1] - r0);
+    }
+    blocks[2 * pb] = r0;
+    blocks[2 * pb + 1] = nvalid;
+  }
+}
+
 }  // namespace
 
 extern "C" int mi355x_quantize_weight_blocks(const void* w, int is_fp32, int experts, int out,
@@ -660,22 +664,30 @@ extern "C" size_t mi355x_wgrad_padded_rows(int assignments, int experts) {
   return (bound + 127) / 128 * 128;
 }
 
+extern "C" int mi355x_padded_row_blocks(const int32_t* offsets, int experts, int padded,
+                                        int32_t* blocks, void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= 1024, "padded_row_blocks: experts must be in [1, 1024]");
+  MI355X_REQUIRE(padded >= 0 && padded % 128 == 0, "padded_row_blocks: padded must be a multiple of 128");
+  if (padded == 0) return MI355X_OK;
+  hipLaunchKernelGGL(padded_row_blocks_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream,
+                     offsets, experts, padded / 128, blocks);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
 extern "C" int mi355x_quantize_transpose_fp8(const void* x, int64_t pitch, int width,
                                              const int32_t* gather, int gather_div, int gate_up,
-                                             const int32_t* offsets, int experts, int assignments,
-                                             int padded, uint8_t* qt, float* scales,
-                                             void* stream) {
-  MI355X_REQUIRE(experts > 0 && experts <= 1024, "quantize_transpose: experts must be in [1, 1024]");
+                                             const int32_t* row_blocks, int padded, uint8_t* qt,
+                                             float* scales, void* stream) {
   MI355X_REQUIRE(width > 0 && width % 128 == 0, "quantize_transpose: width must be a multiple of 128");
   MI355X_REQUIRE(!gate_up || width % 2 == 0, "quantize_transpose: gate/up width must be even");
-  MI355X_REQUIRE(padded % 128 == 0 && (size_t)padded >= mi355x_wgrad_padded_rows(assignments, experts),
-                 "quantize_transpose: padded must be a multiple of 128 >= mi355x_wgrad_padded_rows");
+  MI355X_REQUIRE(padded >= 0 && padded % 128 == 0, "quantize_transpose: padded must be a multiple of 128");
   MI355X_REQUIRE(gather == nullptr || gather_div > 0, "quantize_transpose: gather_div must be > 0");
-  if (assignments == 0) return MI355X_OK;
+  if (padded == 0) return MI355X_OK;
   dim3 grid(padded / 128, width / 128);
   hipLaunchKernelGGL(quantize_transpose_kernel, grid, dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, pitch, width, gather, gather_div, gate_up, offsets,
-                     experts, padded, qt, scales);
+                     (const uint16_t*)x, pitch, width, gather, gather_div, gate_up, row_blocks,
+                     padded, qt, scales);
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
 }
@@ -697,16 +709,15 @@ extern "C" size_t mi355x_swiglu_bwd_quantize_workspace_size(int rows, int width)
 }
 
 extern "C" int mi355x_swiglu_bwd_quantize(const void* r, const void* h, const float* weights,
-                                          const int32_t* order, const int32_t* offsets,
-                                          int experts, int rows, int width, int padded,
-                                          float limit, uint8_t* dhq, float* dh_scales,
-                                          uint8_t* dh_t, float* dh_t_scales, uint8_t* ap_t,
-                                          float* ap_t_scales, float* dscore, void* workspace,
-                                          size_t workspace_bytes, void* stream) {
-  MI355X_REQUIRE(experts > 0 && experts <= 1024, "swiglu_bwd_quantize: experts must be in [1, 1024]");
+                                          const int32_t* order, const int32_t* row_blocks,
+                                          int rows, int width, int padded, float limit,
+                                          uint8_t* dhq, float* dh_scales, uint8_t* dh_t,
+                                          float* dh_t_scales, uint8_t* ap_t, float* ap_t_scales,
+                                          float* dscore, void* workspace, size_t workspace_bytes,
+                                          void* stream) {
   MI355X_REQUIRE(width > 0 && width % 128 == 0, "swiglu_bwd_quantize: I must be a multiple of 128");
-  MI355X_REQUIRE(padded % 128 == 0 && (size_t)padded >= mi355x_wgrad_padded_rows(rows, experts),
-                 "swiglu_bwd_quantize: padded must be a multiple of 128 >= mi355x_wgrad_padded_rows");
+  MI355X_REQUIRE(padded >= 0 && padded % 128 == 0 && (size_t)padded >= (size_t)rows,
+                 "swiglu_bwd_quantize: padded must be a multiple of 128 covering the rows");
   MI355X_REQUIRE((dh_t == nullptr) == (dh_t_scales == nullptr) &&
                      (ap_t == nullptr) == (ap_t_scales == nullptr),
                  "swiglu_bwd_quantize: transposed outputs need their scales");
@@ -716,8 +727,8 @@ extern "C" int mi355x_swiglu_bwd_quantize(const void* r, const void* h, const fl
   hipStream_t s = (hipStream_t)stream;
   float* dsp = (float*)workspace;
   hipLaunchKernelGGL(swiglu_bwd_quantize_kernel, dim3(padded / 128, width / 128), dim3(kSbThreads),
-                     0, s, (const uint16_t*)r, (const uint16_t*)h, weights, order, offsets,
-                     experts, rows, width, padded, limit, dhq, dh_scales, dh_t, dh_t_scales, ap_t,
+                     0, s, (const uint16_t*)r, (const uint16_t*)h, weights, order, row_blocks,
+                     rows, width, padded, limit, dhq, dh_scales, dh_t, dh_t_scales, ap_t,
                      ap_t_scales, dsp);
   MI355X_LAUNCH_CHECK();
   hipLaunchKernelGGL(dscore_reduce_kernel, dim3((rows + 255) / 256), dim3(256), 0, s, dsp, rows,

@@ -301,13 +301,26 @@ def wgrad_padded_rows(assignments: int, experts: int) -> int:
     return _native.query("mi355x_wgrad_padded_rows", int(assignments), int(experts))
 
 
+def padded_row_blocks(offsets: torch.Tensor, padded: int) -> torch.Tensor:
+    """int32 ``[padded/128, 2]``: (first sorted row, valid rows) of each padded
+    128-row block of the weight-gradient layout."""
+    experts = offsets.numel() - 1
+    device = _on_gpu(offsets)
+    blocks = torch.empty((padded // 128, 2), dtype=torch.int32, device=device)
+    _native.call("mi355x_padded_row_blocks", _ptr(offsets), experts, int(padded), _ptr(blocks),
+                 _stream(device))
+    return blocks
+
+
 def quantize_transpose(
     x: torch.Tensor, offsets: torch.Tensor, assignments: int, *, gather=None,
-    gather_div: int = 1, gate_up: bool = False, padded: int | None = None,
+    gather_div: int = 1, gate_up: bool = False, padded: int | None = None, row_blocks=None,
 ):
     """Feature-major e4m3 wgrad operand of the routed rows of ``x``:
     ``(qt [W, P], scales [P/128, W], P)``, each expert's rows at its
-    128-aligned padded offset (zeros between); the scales are powers of two."""
+    128-aligned padded offset (zeros between); the scales are powers of two.
+    ``row_blocks`` (from :func:`padded_row_blocks`, same ``P``) may be passed
+    to share it between calls."""
     if x.dtype != torch.bfloat16 or x.ndim != 2:
         raise ValueError("quantize_transpose takes bf16 [rows, width]")
     width = x.shape[1]
@@ -315,13 +328,17 @@ def quantize_transpose(
     device = _on_gpu(x, offsets, gather)
     if padded is None:
         padded = wgrad_padded_rows(assignments, experts)
+    if row_blocks is None:
+        row_blocks = padded_row_blocks(offsets, padded)
+    _check(row_blocks, (padded // 128, 2), torch.int32, "row_blocks")
     qt = torch.empty((width, padded), dtype=FP8, device=device)
     scales = torch.empty((padded // 128, width), dtype=torch.float32, device=device)
-    _native.call(
-        "mi355x_quantize_transpose_fp8", _ptr(x), x.stride(0), width, _ptr(gather),
-        int(gather_div), int(gate_up), _ptr(offsets), experts, int(assignments), int(padded),
-        _ptr(qt), _ptr(scales), _stream(device),
-    )
+    if assignments > 0:
+        _native.call(
+            "mi355x_quantize_transpose_fp8", _ptr(x), x.stride(0), width, _ptr(gather),
+            int(gather_div), int(gate_up), _ptr(row_blocks), int(padded), _ptr(qt), _ptr(scales),
+            _stream(device),
+        )
     return qt, scales, padded
 
 
@@ -364,7 +381,7 @@ def routed_swiglu_backward(r, h, weights, order, limit=None):
 
 
 def swiglu_bwd_quantize(r, h, weights, order, offsets, *, padded=None, limit=None,
-                        transposed_dh=True, transposed_ap=True):
+                        transposed_dh=True, transposed_ap=True, row_blocks=None):
     """Fused routed SwiGLU backward + quantizers (see the C header):
     ``(dhq [A,2I] e4m3 gate-first, dh_scales [2I/128, A], dh_t [2I, P] | None,
     dh_t_scales [P/128, 2I] | None, ap_t [I, P] | None, ap_t_scales [P/128, I]
@@ -375,6 +392,9 @@ def swiglu_bwd_quantize(r, h, weights, order, offsets, *, padded=None, limit=Non
     device = _on_gpu(r, h, weights, order, offsets)
     if padded is None:
         padded = wgrad_padded_rows(rows, experts)
+    if row_blocks is None:
+        row_blocks = padded_row_blocks(offsets, padded)
+    _check(row_blocks, (padded // 128, 2), torch.int32, "row_blocks")
     dhq = torch.empty((rows, 2 * width), dtype=FP8, device=device)
     dhs = torch.empty((2 * width // 128, rows), dtype=torch.float32, device=device)
     dht = dhts = apt = apts = None
@@ -389,7 +409,7 @@ def swiglu_bwd_quantize(r, h, weights, order, offsets, *, padded=None, limit=Non
     work = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
     traffic = 6 * rows * width + 2 * rows * width + (3 * width * padded if rows else 0)
     _timed("swiglu_bwd_quantize", device, 0, traffic, "mi355x_swiglu_bwd_quantize", _ptr(r),
-           _ptr(h), _ptr(weights), _ptr(order), _ptr(offsets), experts, rows, width, int(padded),
+           _ptr(h), _ptr(weights), _ptr(order), _ptr(row_blocks), rows, width, int(padded),
            _limit(limit), _ptr(dhq), _ptr(dhs), _ptr(dht), _ptr(dhts), _ptr(apt), _ptr(apts),
            _ptr(dscore), _ptr(work), nbytes, _stream(device))
     return dhq, dhs, dht, dhts, apt, apts, dscore, padded

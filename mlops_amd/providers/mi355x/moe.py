@@ -205,13 +205,16 @@ def backward_routed(
         # SwiGLU backward fused with the quantizers of its outputs: dh row-
         # quantized for the input gradient, dh and a' transposed for the
         # weight gradients (each only when that gradient is wanted).
-        dhq, dhs, dh_t, dh_ts, ap_t, ap_ts, dscore, padded = kernels.swiglu_bwd_quantize(
-            r, h13, route_weights.reshape(-1), order, offsets, limit=swiglu_limit,
-            transposed_dh=need_w13, transposed_ap=need_w2,
+        padded = kernels.wgrad_padded_rows(assignments, experts)
+        blocks = kernels.padded_row_blocks(offsets, padded)
+        dhq, dhs, dh_t, dh_ts, ap_t, ap_ts, dscore, _ = kernels.swiglu_bwd_quantize(
+            r, h13, route_weights.reshape(-1), order, offsets, padded=padded, limit=swiglu_limit,
+            transposed_dh=need_w13, transposed_ap=need_w2, row_blocks=blocks,
         )
         if need_w2:
             dy_t, dy_ts, _ = kernels.quantize_transpose(
-                dy, offsets, assignments, gather=order, gather_div=int(top_k), padded=padded
+                dy, offsets, assignments, gather=order, gather_div=int(top_k), padded=padded,
+                row_blocks=blocks,
             )
             grad_w2 = _grad_at(kernels.wgrad(dy_t, dy_ts, ap_t, ap_ts, offsets, out_dtype=direct,
                                              rows=assignments),
@@ -223,7 +226,8 @@ def backward_routed(
         dx = kernels.gemm(dhq, dhs, w13_t, w13_scale, offsets, transposed_scale=True)
         if need_w13:
             x_t, x_ts, _ = kernels.quantize_transpose(
-                x, offsets, assignments, gather=order, gather_div=int(top_k), padded=padded
+                x, offsets, assignments, gather=order, gather_div=int(top_k), padded=padded,
+                row_blocks=blocks,
             )
             grad_w13 = _grad_at(kernels.wgrad(dh_t, dh_ts, x_t, x_ts, offsets, out_dtype=direct,
                                               rows=assignments),

@@ -369,3 +369,19 @@ def test_swiglu_bwd_quantize_matches_unfused(device, limit):
         r, h, weights, order_d, offsets_d, limit=limit, transposed_dh=False, transposed_ap=False)
     assert dht2 is None and apt2 is None
     assert torch.equal(_bytes(dhq2), _bytes(dhq)) and torch.equal(dhs2, dhs)
+
+
+def test_padded_row_blocks_table(device):
+    """(first row, valid rows) of every padded 128-row block, from the oracle's
+    padded layout; zeros past the last expert's blocks."""
+    counts = [0, 300, 128, 1, 0, 257]
+    offsets = _ragged(counts)
+    starts, total = O.padded_layout(offsets)
+    padded = total + 3 * 128
+    blocks = K.padded_row_blocks(offsets.to(device), padded).cpu()
+    want = torch.zeros(padded // 128, 2, dtype=torch.int32)
+    for e, start in enumerate(starts):
+        n = counts[e]
+        for j in range(-(-n // 128)):
+            want[start // 128 + j] = torch.tensor([int(offsets[e]) + 128 * j, min(128, n - 128 * j)])
+    assert torch.equal(blocks, want)
