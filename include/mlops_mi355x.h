@@ -217,6 +217,19 @@ int mi355x_gemm_fp8_block(const uint8_t* a, const float* a_scale, int rows, cons
                           const int32_t* offsets, int interleave, const void* addend, void* out,
                           void* stream);
 
+/* The up projection with SwiGLU fused: mi355x_gemm_fp8_block in gate/up mode
+ * (w13 [E, 2I, K], interleave = 1) writing h [rows, 2I] bf16 interleaved, and
+ * from the same bf16 values act = silu(min(g, L)) * clamp(u, +-L) (limit <=
+ * 0: no clamp), row-quantized 1x128 into act_q [rows, I] e4m3 with
+ * act_scales [I/128][rows], bit-identical to mi355x_swiglu_quantize_fp8 on h.
+ * 2I must be a multiple of 256. Replaces the SwiGLU epilogue of the up GEMM
+ * (kernels/quack_moe/block_fp8_gemm.py:1196, :1484) with the row quantizer
+ * of swiglu_rows.py:246 behind it. */
+int mi355x_gemm_fp8_block_swiglu(const uint8_t* a, const float* a_scale, int rows,
+                                 const uint8_t* w, const float* w_scale, int experts, int n,
+                                 int k, const int32_t* offsets, const void* addend, float limit,
+                                 void* h, uint8_t* act_q, float* act_scales, void* stream);
+
 /* Grouped weight-gradient GEMM over feature-major e4m3 operands of the same
  * padded layout (see mi355x_quantize_transpose_fp8):
  *   out[e][m][n] = sum_{rows of e} p[m][row] q[n][row], block-scaled,

@@ -98,6 +98,13 @@ __device__ __forceinline__ float quant_div(float x, float scale) {
   return fminf(fmaxf(q, -kE4M3Max), kE4M3Max);
 }
 
+// SwiGLU clamp (limit <= 0: none): gate from above, up on both sides.
+__device__ __forceinline__ void clamp_gate_up(float& g, float& u, float limit) {
+  if (limit > 0.0f) {
+    g = fminf(g, limit);
+    u = fminf(fmaxf(u, -limit), limit);
+  }
+}
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
 __device__ __forceinline__ float sigmoid_f(float g) { return 1.0f / (1.0f + __expf(-g)); }
 

@@ -401,7 +401,7 @@ int persistent_grid(int tiles) {
 int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, const uint8_t* w,
                           const float* w_scale, int w_scale_t, int experts, int n, int k,
                           const int32_t* offsets, int interleave, const void* addend, void* out,
-                          void* stream);
+                          uint8_t* act_q, float* act_scales, float limit, void* stream);
 
 int mi355x_wgrad_v2_launch(const uint8_t* p, const float* p_scale, int m_features,
                            const uint8_t* q, const float* q_scale, int n_features, int padded,
@@ -422,7 +422,8 @@ extern "C" int mi355x_gemm_fp8_block(const uint8_t* a, const float* a_scale, int
   MI355X_REQUIRE(rows >= 0, "gemm: negative rows");
   if (rows == 0) return MI355X_OK;
   const int v2 = mi355x_gemm_v2_launch(a, a_scale, rows, w, w_scale, w_scale_t, experts, n, k,
-                                       offsets, interleave, addend, out, stream);
+                                       offsets, interleave, addend, out, nullptr, nullptr, 0.0f,
+                                       stream);
   if (v2 <= 0) return v2;
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   hipLaunchKernelGGL(grouped_gemm_kernel, dim3(persistent_grid(upper)), dim3(kThreads), 0,
@@ -430,6 +431,28 @@ extern "C" int mi355x_gemm_fp8_block(const uint8_t* a, const float* a_scale, int
                      offsets, interleave, (const uint16_t*)addend, (uint16_t*)out);
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
+}
+
+extern "C" int mi355x_gemm_fp8_block_swiglu(const uint8_t* a, const float* a_scale, int rows,
+                                            const uint8_t* w, const float* w_scale, int experts,
+                                            int n, int k, const int32_t* offsets,
+                                            const void* addend, float limit, void* h,
+                                            uint8_t* act_q, float* act_scales, void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= kMaxExperts, "gemm_swiglu: experts must be in [1, %d]",
+                 kMaxExperts);
+  MI355X_REQUIRE(n > 0 && n % BN == 0 && (n / 2) % 128 == 0,
+                 "gemm_swiglu: 2I must be a multiple of 256, got %d", n);
+  MI355X_REQUIRE(k > 0 && k % BK == 0, "gemm_swiglu: K must be a multiple of %d, got %d", BK, k);
+  MI355X_REQUIRE(rows >= 0, "gemm_swiglu: negative rows");
+  if (rows == 0) return MI355X_OK;
+  const int v2 = mi355x_gemm_v2_launch(a, a_scale, rows, w, w_scale, 0, experts, n, k, offsets, 1,
+                                       addend, h, act_q, act_scales, limit, stream);
+  if (v2 <= 0) return v2;
+  // Shapes outside the pipelined kernel: the GEMM, then the SwiGLU pass.
+  const int rc = mi355x_gemm_fp8_block(a, a_scale, rows, w, w_scale, 0, experts, n, k, offsets, 1,
+                                       addend, h, stream);
+  if (rc != MI355X_OK) return rc;
+  return mi355x_swiglu_quantize_fp8(h, rows, n / 2, limit, act_q, act_scales, stream);
 }
 
 extern "C" int mi355x_gemm_fp8_block_wgrad(const uint8_t* p, const float* p_scale,

@@ -71,6 +71,16 @@ __device__ __forceinline__ void wait_and_sync() {
   asm volatile("" ::: "memory");
 }
 
+// Barrier that waits for this wave's LDS operations only (not for its
+// in-flight global loads and stores).
+__device__ __forceinline__ void lds_sync() {
+  // vmcnt = 63 (no wait), expcnt = 7, lgkmcnt = 0
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ void sync_all() {
   __builtin_amdgcn_s_waitcnt(0);
   asm volatile("" ::: "memory");

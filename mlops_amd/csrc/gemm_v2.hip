@@ -48,12 +48,15 @@ __device__ __forceinline__ int weight_row(int tr, int nt, int interleave, int ha
   return jb < 4 ? j : half_n + j;
 }
 
+template <bool kAct>
 __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ a_scale, int rows,
     const uint8_t* __restrict__ w, const float* __restrict__ w_scale, int w_scale_t, int experts,
     int N, int K, const int32_t* __restrict__ offsets, int interleave,
-    const uint16_t* __restrict__ addend, uint16_t* __restrict__ out) {
+    const uint16_t* __restrict__ addend, uint16_t* __restrict__ out,
+    uint8_t* __restrict__ act_q, float* __restrict__ act_scales, float limit) {
   __shared__ __align__(1024) uint8_t smem[kStages * STAGE_BYTES];
+  __shared__ float act_amax[2][BM];  // per-row amax of each wave column's 64 act columns
   __shared__ int prefix[kMaxExperts + 1];
   __shared__ int tmp[kThreads];
   tile_prefix(offsets, experts, BM, prefix, tmp);
@@ -184,39 +187,86 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     const uint16_t* cbase = addend == nullptr ? nullptr
         : addend + (size_t)(ct.row0 + wm * 64) * N + ct.nt * BN + wn * 128;
     const uint32_t lane_col = (lane & 15) * 8;
+    // SwiGLU fused into the up projection (gate/up mode with act_q): the
+    // activation of the stored bf16 gate/up pairs, quantized 1x128 as
+    // swiglu_quantize_kernel does. A lane holds 4 of a row's 64 act columns
+    // in this wave; the 128-column group spans both wave columns (wn), whose
+    // row maxima meet in LDS.
+    constexpr bool act_out = kAct;  // act_q != nullptr
+    // Two halves of the wave's rows (i = 0-1, then 2-3), each: store h and
+    // keep the activations, exchange row maxima, quantize and store act.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int half = 0; half < 2; ++half) {
+      float act[2][4][4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int lrow = i * 16 + 4 * (lane >> 4) + r;  // row within the wave's 64
-        float v[8];
-        if (interleave) {
+      for (int ii = 0; ii < 2; ++ii) {
+        const int i = half * 2 + ii;
 #pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            v[2 * m] = acc[i][m][r];
-            v[2 * m + 1] = acc[i][4 + m][r];
-          }
-        } else {
-#pragma unroll
-          for (int m = 0; m < 8; ++m) v[m] = acc[i][m][r];
-        }
-        if (wm * 64 + lrow < ct.nvalid) {
-          const uint32_t off = (uint32_t)lrow * (uint32_t)N + lane_col;
-          if (cbase != nullptr) {
-            uint4 c = *(const uint4*)(cbase + off);
-            uint32_t w4[4] = {c.x, c.y, c.z, c.w};
+        for (int r = 0; r < 4; ++r) {
+          const int lrow = i * 16 + 4 * (lane >> 4) + r;  // row within the wave's 64
+          float v[8];
+          if (interleave) {
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-              v[2 * m] += bf16_to_f32(w4[m] & 0xffff);
-              v[2 * m + 1] += bf16_to_f32(w4[m] >> 16);
+              v[2 * m] = acc[i][m][r];
+              v[2 * m + 1] = acc[i][4 + m][r];
+            }
+          } else {
+#pragma unroll
+            for (int m = 0; m < 8; ++m) v[m] = acc[i][m][r];
+          }
+          if (wm * 64 + lrow < ct.nvalid) {
+            const uint32_t off = (uint32_t)lrow * (uint32_t)N + lane_col;
+            if (cbase != nullptr) {
+              uint4 c = *(const uint4*)(cbase + off);
+              uint32_t w4[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+              for (int m = 0; m < 4; ++m) {
+                v[2 * m] += bf16_to_f32(w4[m] & 0xffff);
+                v[2 * m + 1] += bf16_to_f32(w4[m] >> 16);
+              }
+            }
+            uint4 o;
+            o.x = pack_bf16x2(v[0], v[1]);
+            o.y = pack_bf16x2(v[2], v[3]);
+            o.z = pack_bf16x2(v[4], v[5]);
+            o.w = pack_bf16x2(v[6], v[7]);
+            store_stream(obase + off, o);
+            if (act_out) {
+              const uint32_t w4[4] = {o.x, o.y, o.z, o.w};
+              float pmax = 0.0f;
+#pragma unroll
+              for (int m = 0; m < 4; ++m) {
+                float g = bf16_to_f32(w4[m] & 0xffff), u = bf16_to_f32(w4[m] >> 16);
+                clamp_gate_up(g, u, limit);
+                act[ii][r][m] = silu_f(g) * u;
+                pmax = fmaxf(pmax, fabsf(act[ii][r][m]));
+              }
+              pmax = group_max<16>(pmax);  // the 16 lanes of this row: 64 columns
+              if ((lane & 15) == 0) act_amax[wn][wm * 64 + lrow] = pmax;
             }
           }
-          uint4 o;
-          o.x = pack_bf16x2(v[0], v[1]);
-          o.y = pack_bf16x2(v[2], v[3]);
-          o.z = pack_bf16x2(v[4], v[5]);
-          o.w = pack_bf16x2(v[6], v[7]);
-          store_stream(obase + off, o);
+        }
+      }
+      if (act_out) {
+        lds_sync();
+        const int half_w = N / 2;
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int trow = wm * 64 + (half * 2 + ii) * 16 + 4 * (lane >> 4) + r;
+            if (trow < ct.nvalid) {
+              const float amax = fmaxf(act_amax[0][trow], act_amax[1][trow]);
+              const float sc = fmaxf(amax * kInv448, kMinScale);
+              const uint32_t qv =
+                  f32x4_to_e4m3(quant_div(act[ii][r][0], sc), quant_div(act[ii][r][1], sc),
+                                quant_div(act[ii][r][2], sc), quant_div(act[ii][r][3], sc));
+              const size_t row = (size_t)(ct.row0 + trow);
+              *(uint32_t*)(act_q + row * half_w + ct.nt * 128 + wn * 64 + (lane & 15) * 4) = qv;
+              if (wn == 0 && (lane & 15) == 0) act_scales[(size_t)ct.nt * rows + row] = sc;
+            }
+          }
         }
       }
     }
@@ -248,13 +298,20 @@ int cu_count() {
 int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, const uint8_t* w,
                           const float* w_scale, int w_scale_t, int experts, int n, int k,
                           const int32_t* offsets, int interleave, const void* addend, void* out,
-                          void* stream) {
+                          uint8_t* act_q, float* act_scales, float limit, void* stream) {
   if (n % BN != 0 || experts > kMaxExperts || (interleave && (n / 2) % 128 != 0)) return 1;
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   const int grid = upper < cu_count() ? upper : cu_count();
-  hipLaunchKernelGGL(grouped_gemm_v2_kernel, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream, a,
-                     a_scale, rows, w, w_scale, w_scale_t, experts, n, k, offsets, interleave,
-                     (const uint16_t*)addend, (uint16_t*)out);
+  if (act_q != nullptr)
+    hipLaunchKernelGGL(grouped_gemm_v2_kernel<true>, dim3(grid), dim3(kThreads), 0,
+                       (hipStream_t)stream, a, a_scale, rows, w, w_scale, w_scale_t, experts, n, k,
+                       offsets, interleave, (const uint16_t*)addend, (uint16_t*)out, act_q,
+                       act_scales, limit);
+  else
+    hipLaunchKernelGGL(grouped_gemm_v2_kernel<false>, dim3(grid), dim3(kThreads), 0,
+                       (hipStream_t)stream, a, a_scale, rows, w, w_scale, w_scale_t, experts, n, k,
+                       offsets, interleave, (const uint16_t*)addend, (uint16_t*)out, nullptr,
+                       nullptr, 0.0f);
   MI355X_LAUNCH_CHECK();
   return 0;
 }

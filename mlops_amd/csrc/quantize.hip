@@ -207,12 +207,6 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __re
   }
 }
 
-__device__ __forceinline__ void clamp_gate_up(float& g, float& u, float limit) {
-  if (limit > 0.0f) {
-    g = fminf(g, limit);
-    u = fminf(fmaxf(u, -limit), limit);
-  }
-}
 
 // SwiGLU of interleaved h [rows, 2I] -> e4m3 act [rows, I] + 1x128 scales.
 __global__ void __launch_bounds__(256) swiglu_quantize_kernel(const uint16_t* __restrict__ h,

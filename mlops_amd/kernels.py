@@ -440,6 +440,28 @@ def gemm(a, a_scale, w, w_scale, offsets, *, transposed_scale=False, interleave=
     return out
 
 
+def gemm_swiglu(a, a_scale, w, w_scale, offsets, *, limit=None, addend=None):
+    """Up projection with SwiGLU fused: ``(h bf16 [A, 2I] interleaved, act e4m3
+    [A, I], act_scales [I/128, A])``; ``act`` equals :func:`swiglu_quantize` of
+    ``h`` bit for bit."""
+    rows, k = a.shape
+    experts, n, kw = w.shape
+    if kw != k:
+        raise ValueError(f"weight K {kw} != activation K {k}")
+    _check(a_scale, (k // 128, rows), torch.float32, "activation scales")
+    device = _on_gpu(a, a_scale, w, w_scale, offsets, addend)
+    h = torch.empty((rows, n), dtype=torch.bfloat16, device=device)
+    act = torch.empty((rows, n // 2), dtype=FP8, device=device)
+    act_scales = torch.empty((n // 256, rows), dtype=torch.float32, device=device)
+    _timed(
+        "gemm_fp8_block", device, 2 * rows * n * k, rows * k + experts * n * k + 2 * rows * n,
+        "mi355x_gemm_fp8_block_swiglu", _ptr(a), _ptr(a_scale), rows, _ptr(w), _ptr(w_scale),
+        experts, n, k, _ptr(offsets), _ptr(addend), _limit(limit), _ptr(h), _ptr(act),
+        _ptr(act_scales), _stream(device),
+    )
+    return h, act, act_scales
+
+
 def wgrad(p, p_scale, q, q_scale, offsets, *, out_dtype=torch.bfloat16, rows=None):
     """``out[e] = sum over expert e's rows of p[:, row] q[:, row]^T`` -> ``[E, M, N]``.
     ``rows`` (the routed row count, for the launch timer's FLOP count) is optional."""

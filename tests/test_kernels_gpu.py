@@ -385,3 +385,24 @@ def test_padded_row_blocks_table(device):
         for j in range(-(-n // 128)):
             want[start // 128 + j] = torch.tensor([int(offsets[e]) + 128 * j, min(128, n - 128 * j)])
     assert torch.equal(blocks, want)
+
+
+@pytest.mark.parametrize("limit", [None, 0.9])
+@pytest.mark.parametrize("inter", [256, 384])  # 2I = 512: pipelined epilogue; 768: GEMM then SwiGLU pass
+def test_gemm_swiglu_fused_matches_separate_pass(device, limit, inter):
+    """The up projection's fused SwiGLU output equals swiglu_quantize of its
+    own h bit for bit; h equals the plain gate/up GEMM's."""
+    g = torch.Generator().manual_seed(41)
+    counts = [300, 0, 77, 512, 129]
+    offsets = _ragged(counts)
+    rows, hidden = int(offsets[-1]), 256
+    x = torch.randn(rows, hidden, generator=g).to(torch.bfloat16).to(device)
+    w = (torch.randn(len(counts), 2 * inter, hidden, generator=g) * 0.3).to(device)
+    xq, xs = K.quantize_rows(x)
+    wq, ws = K.quantize_weight_blocks(w)
+    h, act, act_s = K.gemm_swiglu(xq, xs, wq, ws, offsets.to(device), limit=limit)
+    h_ref = K.gemm(xq, xs, wq, ws, offsets.to(device), interleave=True)
+    assert torch.equal(h, h_ref)
+    q_ref, s_ref = K.swiglu_quantize(h, limit)
+    assert torch.equal(_bytes(act), _bytes(q_ref))
+    assert torch.equal(act_s, s_ref)
