@@ -11,7 +11,8 @@ expert weights N(0,0.02).
 Prints ONE JSON line with tokens/s, the grouped-GEMM roofline (fp8 MFMA peak)
 measured live with device events around every GEMM launch on its stream, and
 the CPU baseline: the reference's native PyTorch path (restated in
-``oracle.native_moe``) on BASELINE config 1, timed on the host cores.
+``oracle.native_moe``) on a bounded sample (128 tokens) of the same layer
+shape, timed on the host cores.
 """
 
 from __future__ import annotations
@@ -63,28 +64,33 @@ def gpu_step(moe, args, cfg):
     torch.autograd.backward([out, aux], [dy, torch.full_like(aux, 0.01)])
 
 
-def cpu_baseline(budget_s=15.0, max_iters=20):
-    """Reference native path (dense per-expert loop, torch autograd, bf16) on
-    BASELINE config 1, on the host CPU; median of up to ``max_iters`` runs
-    after 3 warmups, bounded by ``budget_s`` seconds."""
+def cpu_baseline(cfg_name, sample_tokens=128, budget_s=20.0, max_iters=10):
+    """The reference's native path (``oracle.native_moe``, the restatement of
+    moe_reference.py:20-109: every expert on every token, masked, torch
+    autograd, fp32 as the reference computes off the GPU) on a bounded sample of the benchmark's own workload: the
+    same layer shape with ``sample_tokens`` tokens, on the host CPU. Median of
+    up to ``max_iters`` fwd+bwd runs after 2 warmups, bounded by ``budget_s``;
+    reported as tokens/s of that sample."""
     from oracle import moe_oracle as O
 
     threads = max(1, min(os.cpu_count() or 1, 16))
     torch.set_num_threads(threads)
-    cfg = CONFIGS["config1"]
+    cfg = dict(CONFIGS[cfg_name], tokens=int(sample_tokens))
     x, res, wr, w13, w2, dy = make_inputs(cfg, torch.device("cpu"))
     x.requires_grad_(True)
     wr.requires_grad_(True)
-    w13.requires_grad_(True)
-    w2.requires_grad_(True)
+    # Per-expert leaf weights (same values): the gradients are the same, without
+    # autograd materializing a full [E, ...] gradient for every expert's slice.
+    w13 = [w.clone().requires_grad_(True) for w in w13]
+    w2 = [w.clone().requires_grad_(True) for w in w2]
 
     def step():
         out, aux, counts, psum = O.native_moe(x, res, wr, w13, w2, top_k=cfg["top_k"],
                                               routing_mode="topk_then_softmax",
-                                              compute_dtype=torch.bfloat16)
+                                              compute_dtype=torch.float32)
         torch.autograd.backward([out, aux], [dy, torch.full_like(aux, 0.01)])
 
-    for _ in range(3):
+    for _ in range(2):
         step()
     times = []
     start = time.perf_counter()
@@ -98,8 +104,10 @@ def cpu_baseline(budget_s=15.0, max_iters=20):
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"BASELINE config 1 (T=256, H=512, E=8, k=2, I=1024) native dense per-expert "
-                   f"fwd+bwd in bf16, median of {len(times)} runs after 3 warmups"),
+        "sample": (f"{cfg_name} layer shape (H={cfg['hidden']}, I={cfg['inter']}, E={cfg['experts']}, "
+                   f"k={cfg['top_k']}) with {cfg['tokens']} tokens: reference native path (dense "
+                   f"per-expert loop, masked, per-expert weight leaves) fwd+bwd in fp32 via torch autograd, median of "
+                   f"{len(times)} runs after 2 warmups"),
         "ms_per_step": median * 1e3,
     }
 
@@ -120,6 +128,7 @@ def main():
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--config", default="qwen3_30b_a3b", choices=sorted(CONFIGS))
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-sample-tokens", type=int, default=128)
     parser.add_argument("--calibration-copy-mib", type=int, default=0,
                         help="after the timed steps, run one device copy of this many MiB "
                              "(the known-size kernel that calibrates rocprofv3 byte counters)")
@@ -216,7 +225,7 @@ def main():
         torch.cuda.synchronize()
         result["calibration_copy_bytes"] = n
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline()
+        result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_sample_tokens)
     print(json.dumps(result))
 
 

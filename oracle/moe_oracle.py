@@ -366,7 +366,10 @@ def native_moe(h2, residual, router_weight, w13, w2, *, top_k, routing_mode, rou
                compute_dtype=torch.float32):
     """The reference's native oracle -- kernels/moe_reference.py:20-109: every
     expert runs on every row, masked by its route coefficient. Differentiable
-    (plain autograd). Computed at ``compute_dtype`` (fp32 by default)."""
+    (plain autograd). Computed at ``compute_dtype`` (fp32 by default).
+    ``w13``/``w2`` are ``[E, ...]`` tensors or lists of per-expert ``[...]``
+    tensors (same values; per-expert leaves avoid autograd materializing a
+    full ``[E, ...]`` gradient for every expert's slice)."""
     shape = h2.shape
     x = h2.reshape(-1, shape[-1])
     res = residual.reshape_as(x)
@@ -380,7 +383,7 @@ def native_moe(h2, residual, router_weight, w13, w2, *, top_k, routing_mode, rou
     weights = _live_weights(logits, ids, routing_mode, routed_scaling)
     experts = router_weight.shape[0]
     aux, counts, prob_sum = _live_statistics(logits, ids, routing_mode, lengths, experts)
-    width = w2.shape[2]
+    width = w2[0].shape[-1]
     xc = x.to(compute_dtype)
     routed = torch.zeros(rows, shape[-1], dtype=torch.float32)
     for e in range(experts):
