@@ -59,7 +59,7 @@ def route(logits, top_k, mode, *, bias=None, n_group=1, topk_group=1, routed_sca
             grouped, _ = torch.sort(grouped, dim=-1, descending=True, stable=True)
             gscore = grouped[..., : min(2, grouped.shape[-1])].sum(-1)
             _, gids = torch.sort(gscore, dim=-1, descending=True, stable=True)
-            gmask = torch.zeros(tokens, int(n_group), dtype=torch.bool)
+            gmask = torch.zeros(tokens, int(n_group), dtype=torch.bool, device=sel.device)
             gmask.scatter_(1, gids[:, : int(topk_group)], True)
             sel = sel.masked_fill(~gmask.repeat_interleave(experts // int(n_group), 1), -math.inf)
         _, ids = torch.sort(sel, dim=-1, descending=True, stable=True)
@@ -95,7 +95,7 @@ def routing_statistics(logits, ids, mode, lengths, experts):
     prob_sum = p.sum(0)
     counts = torch.bincount(ids.reshape(-1).long(), minlength=experts)
     if mode == "sigmoid_noaux_tc":
-        aux = torch.zeros((), dtype=torch.float32)
+        aux = torch.zeros((), dtype=torch.float32, device=logits.device)
         start = 0
         for length in lengths:
             stop = start + int(length)
@@ -385,7 +385,7 @@ def native_moe(h2, residual, router_weight, w13, w2, *, top_k, routing_mode, rou
     aux, counts, prob_sum = _live_statistics(logits, ids, routing_mode, lengths, experts)
     width = w2[0].shape[-1]
     xc = x.to(compute_dtype)
-    routed = torch.zeros(rows, shape[-1], dtype=torch.float32)
+    routed = torch.zeros(rows, shape[-1], dtype=torch.float32, device=x.device)
     for e in range(experts):
         coef = (weights * (ids == e)).sum(-1)
         h13 = xc @ w13[e].to(compute_dtype).t()
@@ -415,7 +415,7 @@ def _live_statistics(logits, ids, mode, lengths, experts):
     counts = torch.bincount(ids.reshape(-1).long(), minlength=experts)
     prob_sum = p.sum(0)
     if mode == "sigmoid_noaux_tc":
-        aux = torch.zeros((), dtype=torch.float32)
+        aux = torch.zeros((), dtype=torch.float32, device=logits.device)
         start = 0
         for length in lengths:
             stop = start + int(length)

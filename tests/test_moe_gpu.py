@@ -258,3 +258,40 @@ def test_per_call_transposed_weights_match_containers_bitwise(device, monkeypatc
         results.append((out, xg.grad, a.grad, b.grad))
     for u, v in zip(*results):
         assert torch.equal(u.float(), v.float())
+
+
+@pytest.mark.parametrize("shape", [
+    # BASELINE config 4 (DeepSeek-V3 shard: H=7168, I=2048, 32 local experts,
+    # k=8, Zipf(1.2)-skewed routing, weights N(0, 0.006)) at 512 tokens.
+    dict(tokens=512, hidden=7168, inter=2048, experts=32, top_k=8, std=0.006, skew="zipf"),
+    # BASELINE config 5 (Mixtral: H=4096, I=14336, E=8, k=2, logits + 2 on
+    # expert 0) at 256 tokens.
+    dict(tokens=256, hidden=4096, inter=14336, experts=8, top_k=2, std=0.02, skew="expert0"),
+], ids=["deepseek_v3_shard", "mixtral_8x7b"])
+def test_large_shapes_match_native_on_gpu(device, shape):
+    """Layer fwd+bwd at the C4 / C5 widths against the reference's native
+    path (oracle.native_moe, fp32, on the GPU) on the dequantized weights."""
+    t, h, i, e, k = (shape[n] for n in ("tokens", "hidden", "inter", "experts", "top_k"))
+    x, res, wr, w13, w2, dy = _inputs(device, t, h, e, i, seed=21, std=shape["std"])
+    # Skewed routing: a constant input column times per-expert router offsets.
+    x[:, 0] = 1.0
+    if shape["skew"] == "zipf":
+        wr[:, 0] = 1.2 * torch.log(1.0 / torch.arange(1, e + 1, device=device, dtype=torch.float32))
+    else:
+        wr[:, 0] = 0.0
+        wr[0, 0] = 2.0
+    r = _run(x, res, wr, w13, w2, dy, top_k=k, routing_mode="topk_then_softmax")
+    w13d = [w.requires_grad_(True) for w in r["w13c"].dequantize().detach().float()]
+    w2d = [w.requires_grad_(True) for w in r["w2c"].dequantize().detach().float()]
+    xr = x.detach().float().requires_grad_(True)
+    wrr = wr.detach().clone().requires_grad_(True)
+    out, aux, counts, psum = O.native_moe(xr, res.float(), wrr, w13d, w2d, top_k=k,
+                                          routing_mode="topk_then_softmax")
+    torch.autograd.backward([out, aux], [dy.float(), torch.tensor(0.1, device=device)])
+    # logits from different GEMM orders may flip a near-tie: allow one route
+    assert int((r["counts"] - counts).abs().sum()) <= 2
+    assert frob_rel(r["out"].float(), out.detach()) < 4e-2
+    assert frob_rel(r["gx"].float(), xr.grad) < 8e-2
+    assert frob_rel(r["g13"].float(), torch.stack([w.grad for w in w13d])) < 8e-2
+    assert frob_rel(r["g2"].float(), torch.stack([w.grad for w in w2d])) < 8e-2
+    assert frob_rel(r["gr"].float(), wrr.grad) < 8e-2
