@@ -105,8 +105,13 @@ __device__ __forceinline__ void clamp_gate_up(float& g, float& u, float limit) {
     u = fminf(fmaxf(u, -limit), limit);
   }
 }
-__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
-__device__ __forceinline__ float sigmoid_f(float g) { return 1.0f / (1.0f + __expf(-g)); }
+// sigmoid / silu with the hardware exp and reciprocal (v_exp_f32, v_rcp_f32,
+// 1 ulp) instead of an IEEE division: these run per element in the SwiGLU
+// passes, which are ALU-bound on them.
+__device__ __forceinline__ float sigmoid_f(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
+__device__ __forceinline__ float silu_f(float g) { return g * sigmoid_f(g); }
 
 // ---------------------------------------------------------------- waves
 __device__ __forceinline__ float wave_max(float v) {

@@ -209,44 +209,58 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __re
 
 
 // SwiGLU of interleaved h [rows, 2I] -> e4m3 act [rows, I] + 1x128 scales.
+// Unit of work = (row, 128-column act group), taken by a 16-lane group (8
+// columns = 16 interleaved h values per lane); each group handles kSwUnits
+// units with every load issued before any math (memory parallelism), and
+// stores full 128-byte act lines.
+constexpr int kSwUnits = 4;
+
 __global__ void __launch_bounds__(256) swiglu_quantize_kernel(const uint16_t* __restrict__ h,
                                                               int rows, int width, float limit,
                                                               uint8_t* __restrict__ q,
                                                               float* __restrict__ scales) {
-  const int wave = threadIdx.x >> 6, lane = lane_id();
-  const int r = blockIdx.x * 4 + wave;
-  if (r >= rows) return;
-  const uint16_t* src = h + (size_t)r * 2 * width;
-  for (int base = 0; base < width; base += 512) {
-    const int j = base + lane * 8;
-    const bool ok = j < width;
-    float act[8];
-    if (ok) {
-      float a[8], b[8];
-      load_bf16x8(src + 2 * j, a);
-      load_bf16x8(src + 2 * j + 8, b);
+  const int groups = width / 128;
+  const long long units = (long long)rows * groups;
+  const int lane16 = threadIdx.x & 15;
+  const long long g0 = ((long long)blockIdx.x * 16 + (threadIdx.x >> 4)) * kSwUnits;
+  uint4 ha[kSwUnits], hb[kSwUnits];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float g0 = a[2 * i], u0 = a[2 * i + 1], g1 = b[2 * i], u1 = b[2 * i + 1];
-        clamp_gate_up(g0, u0, limit);
-        clamp_gate_up(g1, u1, limit);
-        act[i] = silu_f(g0) * u0;
-        act[4 + i] = silu_f(g1) * u1;
-      }
-    } else {
+  for (int u = 0; u < kSwUnits; ++u) {
+    const long long unit = g0 + u;
+    ha[u] = hb[u] = make_uint4(0, 0, 0, 0);
+    if (unit < units) {
+      const long long r = unit / groups;
+      const int j = (int)(unit - r * groups) * 128 + lane16 * 8;
+      const uint16_t* src = h + r * 2 * width + 2 * j;
+      ha[u] = *(const uint4*)src;
+      hb[u] = *(const uint4*)(src + 8);
+    }
+  }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) act[i] = 0.0f;
+  for (int u = 0; u < kSwUnits; ++u) {
+    const long long unit = g0 + u;
+    if (unit >= units) break;  // uniform over the 16-lane group
+    const long long r = unit / groups;
+    const int grp = (int)(unit - r * groups);
+    const int j = grp * 128 + lane16 * 8;
+    float a[8], b[8], act[8];
+    unpack_bf16x8(ha[u], a);
+    unpack_bf16x8(hb[u], b);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float g0v = a[2 * i], u0 = a[2 * i + 1], g1 = b[2 * i], u1 = b[2 * i + 1];
+      clamp_gate_up(g0v, u0, limit);
+      clamp_gate_up(g1, u1, limit);
+      act[i] = silu_f(g0v) * u0;
+      act[4 + i] = silu_f(g1) * u1;
     }
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(act[i]));
     amax = group_max<16>(amax);
-    const float s = fmaxf(amax * kInv448, kMinScale);
-    uint2 packed = quant8(act, s);
-    if (ok) {
-      *(uint2*)(q + (size_t)r * width + j) = packed;
-      if ((lane & 15) == 0) scales[(size_t)(j >> 7) * rows + r] = s;
-    }
+    const float sc = fmaxf(amax * kInv448, kMinScale);
+    *(uint2*)(q + r * width + j) = quant8(act, sc);
+    if (lane16 == 0) scales[(size_t)grp * rows + r] = sc;
   }
 }
 
@@ -647,7 +661,9 @@ extern "C" int mi355x_swiglu_quantize_fp8(const void* h, int rows, int width, fl
                                           uint8_t* q, float* scales, void* stream) {
   MI355X_REQUIRE(width > 0 && width % 128 == 0, "swiglu_quantize: I must be a multiple of 128");
   if (rows == 0) return MI355X_OK;
-  hipLaunchKernelGGL(swiglu_quantize_kernel, dim3((rows + 3) / 4), dim3(256), 0,
+  const long long units = (long long)rows * (width / 128);
+  const long long blocks = (units + 16 * kSwUnits - 1) / (16 * kSwUnits);
+  hipLaunchKernelGGL(swiglu_quantize_kernel, dim3((unsigned)blocks), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)h, rows, width, limit, q, scales);
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
