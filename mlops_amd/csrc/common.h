@@ -98,6 +98,19 @@ __device__ __forceinline__ float quant_div(float x, float scale) {
   return fminf(fmaxf(q, -kE4M3Max), kE4M3Max);
 }
 
+// x / scale, correctly rounded like the division above, for many x sharing
+// one scale: with inv = RN(1 / scale) (one IEEE division per scale),
+// q0 = RN(x inv), the residual e = x - scale q0 is exact (FMA) and
+// RN(q0 + e inv) = RN(x / scale) (Markstein) for quotients that neither
+// overflow nor underflow, which covers every quotient that reaches a nonzero
+// e4m3 value. Then the same clip to +-448.
+__device__ __forceinline__ float quant_div_inv(float x, float scale, float inv) {
+  const float q0 = x * inv;
+  const float e = fmaf(-scale, q0, x);
+  const float q = fmaf(e, inv, q0);
+  return fminf(fmaxf(q, -kE4M3Max), kE4M3Max);
+}
+
 // SwiGLU clamp (limit <= 0: none): gate from above, up on both sides.
 __device__ __forceinline__ void clamp_gate_up(float& g, float& u, float limit) {
   if (limit > 0.0f) {

@@ -138,10 +138,11 @@ __global__ void __launch_bounds__(256) permute_quantize_kernel(
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
     amax = group_max<16>(amax);
     const float s = fmaxf(amax * kInv448, kMinScale);
-    uint32_t lo = f32x4_to_e4m3(quant_div(v[0], s), quant_div(v[1], s), quant_div(v[2], s),
-                                quant_div(v[3], s));
-    uint32_t hi = f32x4_to_e4m3(quant_div(v[4], s), quant_div(v[5], s), quant_div(v[6], s),
-                                quant_div(v[7], s));
+    const float inv = 1.0f / s;
+    uint32_t lo = f32x4_to_e4m3(quant_div_inv(v[0], s, inv), quant_div_inv(v[1], s, inv),
+                                quant_div_inv(v[2], s, inv), quant_div_inv(v[3], s, inv));
+    uint32_t hi = f32x4_to_e4m3(quant_div_inv(v[4], s, inv), quant_div_inv(v[5], s, inv),
+                                quant_div_inv(v[6], s, inv), quant_div_inv(v[7], s, inv));
     if (ok) {
       const int kb = col >> 7;
 #pragma unroll

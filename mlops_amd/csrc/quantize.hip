@@ -26,10 +26,11 @@ __device__ __forceinline__ void unpack_bf16x8(uint4 r, float* v) {
 }
 
 __device__ __forceinline__ uint2 quant8(const float* v, float s) {
-  uint32_t lo = f32x4_to_e4m3(quant_div(v[0], s), quant_div(v[1], s), quant_div(v[2], s),
-                              quant_div(v[3], s));
-  uint32_t hi = f32x4_to_e4m3(quant_div(v[4], s), quant_div(v[5], s), quant_div(v[6], s),
-                              quant_div(v[7], s));
+  const float inv = 1.0f / s;
+  uint32_t lo = f32x4_to_e4m3(quant_div_inv(v[0], s, inv), quant_div_inv(v[1], s, inv),
+                              quant_div_inv(v[2], s, inv), quant_div_inv(v[3], s, inv));
+  uint32_t hi = f32x4_to_e4m3(quant_div_inv(v[4], s, inv), quant_div_inv(v[5], s, inv),
+                              quant_div_inv(v[6], s, inv), quant_div_inv(v[7], s, inv));
   return make_uint2(lo, hi);
 }
 
