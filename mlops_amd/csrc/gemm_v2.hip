@@ -93,6 +93,17 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       const uint32_t off = 4u * (uint32_t)min(t.row0 + wave * 32 + lane, rows - 1);
       dma4(sbase, off, base + A_BYTES + B_BYTES + wave * 128);
     }
+    // The wave's two weight block scales (its columns' low and high 128-column
+    // blocks) into the stage as well: an ordinary load here would make the
+    // compiler wait on it, and in-order completion would make that wait
+    // cover this step's operand copies too.
+    if (lane < 2) {
+      const int nb = lane == 0 ? (interleave ? t.nt : 2 * t.nt + wn)
+                               : (interleave ? half_n / 128 + t.nt : 2 * t.nt + wn);
+      const uint32_t idx = w_scale_t ? (uint32_t)((t.e * kbw + kb) * nbw + nb)
+                                     : (uint32_t)((t.e * nbw + nb) * kbw + kb);
+      dma4(w_scale, 4u * idx, base + A_BYTES + B_BYTES + SA_BYTES + wave * 8);
+    }
   };
 
   // XCD-affine order: workgroup b runs on XCD b % 8, and XCD x takes the
@@ -123,8 +134,6 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
-    const int nb_lo = interleave ? ct.nt : 2 * ct.nt + wn;
-    const int nb_hi = interleave ? (half_n / 128) + ct.nt : 2 * ct.nt + wn;
 
     for (int kb = 0; kb < nk; ++kb) {
       wait_and_sync<0>();  // two stages: the only loads in flight are this step's
@@ -140,11 +149,8 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       const uint8_t* ta = base;
       const uint8_t* tb = base + A_BYTES;
       const float* sa = (const float*)(base + A_BYTES + B_BYTES);
-      const int kbr = __builtin_amdgcn_readfirstlane(kb + ct.rot < nk ? kb + ct.rot : kb + ct.rot - nk);
-      const float sb_lo = w_scale_t ? w_scale[((size_t)ct.e * kbw + kbr) * nbw + nb_lo]
-                                    : w_scale[((size_t)ct.e * nbw + nb_lo) * kbw + kbr];
-      const float sb_hi = w_scale_t ? w_scale[((size_t)ct.e * kbw + kbr) * nbw + nb_hi]
-                                    : w_scale[((size_t)ct.e * nbw + nb_hi) * kbw + kbr];
+      const float2 sbw = *(const float2*)(base + A_BYTES + B_BYTES + SA_BYTES + wave * 8);
+      const float sb_lo = sbw.x, sb_hi = sbw.y;
       v8i af[4];
       float s4[4][4];
 #pragma unroll
