@@ -111,9 +111,11 @@ int mi355x_quantize_rows_fp8(const void* x, int rows, int width, int64_t pitch, 
 /* SwiGLU of the interleaved pre-activation h [rows, 2I], clamped at limit
  * when limit > 0, quantized to e4m3 with 1x128 scales.
  * Replaces swiglu_quantize_rows_fp8 (kernels/quack_moe/swiglu_rows.py:246-258,
- * _swiglu_rows :50-76). q: [rows,I]; scales: [I/128][rows]. */
+ * _swiglu_rows :50-76). q: [rows,I]; scales: [I/128][rows]. act (NULL to
+ * skip): the activation itself, bf16 [rows,I], for a consumer that needs it
+ * unquantized (the expert-LoRA rank projection, lora/experts.py:162-163). */
 int mi355x_swiglu_quantize_fp8(const void* h, int rows, int width, float limit, uint8_t* q,
-                               float* scales, void* stream);
+                               float* scales, void* act, void* stream);
 
 /* 128x128 block quantizer of expert weights [E,out,in] (bf16, or fp32 when
  * is_fp32): s = max(amax / 448, 1e-12) (true division), zero-padded partial

@@ -36,7 +36,7 @@ SIGNATURES = {
     "mi355x_permute_plan": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _S, _P]),
     "mi355x_permute_quantize_fp8": (_I, [_P, _I, _I, _I, _P, _P, _P, _P]),
     "mi355x_quantize_rows_fp8": (_I, [_P, _I, _I, _I64, _I, _P, _P, _P]),
-    "mi355x_swiglu_quantize_fp8": (_I, [_P, _I, _I, _F, _P, _P, _P]),
+    "mi355x_swiglu_quantize_fp8": (_I, [_P, _I, _I, _F, _P, _P, _P, _P]),
     "mi355x_quantize_weight_blocks": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P]),
     "mi355x_transpose_fp8": (_I, [_P, _I, _I, _I, _P, _P]),
     "mi355x_wgrad_padded_rows": (_S, [_I, _I]),

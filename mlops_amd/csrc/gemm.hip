@@ -452,7 +452,7 @@ extern "C" int mi355x_gemm_fp8_block_swiglu(const uint8_t* a, const float* a_sca
   const int rc = mi355x_gemm_fp8_block(a, a_scale, rows, w, w_scale, 0, experts, n, k, offsets, 1,
                                        addend, h, stream);
   if (rc != MI355X_OK) return rc;
-  return mi355x_swiglu_quantize_fp8(h, rows, n / 2, limit, act_q, act_scales, stream);
+  return mi355x_swiglu_quantize_fp8(h, rows, n / 2, limit, act_q, act_scales, nullptr, stream);
 }
 
 extern "C" int mi355x_gemm_fp8_block_wgrad(const uint8_t* p, const float* p_scale,

@@ -151,17 +151,20 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       const float* sa = (const float*)(base + A_BYTES + B_BYTES);
       const float2 sbw = *(const float2*)(base + A_BYTES + B_BYTES + SA_BYTES + wave * 8);
       const float sb_lo = sbw.x, sb_hi = sbw.y;
+      // One B block at a time against the four A blocks (register budget:
+      // two waves share a SIMD, 256 registers each), read one block ahead.
+      // Reads in use order (first B block, A blocks, then the scales), so
+      // the first MFMA waits for two of them rather than for all.
+      v8i bcur = frag(tb, wn * 128 + (lane & 15), lane);
       v8i af[4];
       float s4[4][4];
 #pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = frag(ta, wm * 64 + i * 16 + (lane & 15), lane);
+#pragma unroll
       for (int i = 0; i < 4; ++i) {
-        af[i] = frag(ta, wm * 64 + i * 16 + (lane & 15), lane);
         float4 v = *(const float4*)&sa[wm * 64 + i * 16 + 4 * (lane >> 4)];
         s4[i][0] = v.x; s4[i][1] = v.y; s4[i][2] = v.z; s4[i][3] = v.w;
       }
-      // One B block at a time against the four A blocks (register budget:
-      // two waves share a SIMD, 256 registers each), read one block ahead.
-      v8i bcur = frag(tb, wn * 128 + (lane & 15), lane);
       float sc[4][4];
 #pragma unroll
       for (int jb = 0; jb < 8; ++jb) {

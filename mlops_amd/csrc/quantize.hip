@@ -219,7 +219,8 @@ constexpr int kSwUnits = 4;
 __global__ void __launch_bounds__(256) swiglu_quantize_kernel(const uint16_t* __restrict__ h,
                                                               int rows, int width, float limit,
                                                               uint8_t* __restrict__ q,
-                                                              float* __restrict__ scales) {
+                                                              float* __restrict__ scales,
+                                                              uint16_t* __restrict__ act_out) {
   const int groups = width / 128;
   const long long units = (long long)rows * groups;
   const int lane16 = threadIdx.x & 15;
@@ -262,6 +263,14 @@ __global__ void __launch_bounds__(256) swiglu_quantize_kernel(const uint16_t* __
     const float sc = fmaxf(amax * kInv448, kMinScale);
     *(uint2*)(q + r * width + j) = quant8(act, sc);
     if (lane16 == 0) scales[(size_t)grp * rows + r] = sc;
+    if (act_out != nullptr) {
+      uint4 o;
+      o.x = pack_bf16x2(act[0], act[1]);
+      o.y = pack_bf16x2(act[2], act[3]);
+      o.z = pack_bf16x2(act[4], act[5]);
+      o.w = pack_bf16x2(act[6], act[7]);
+      *(uint4*)(act_out + r * width + j) = o;
+    }
   }
 }
 
@@ -659,13 +668,14 @@ extern "C" int mi355x_quantize_rows_fp8(const void* x, int rows, int width, int6
 }
 
 extern "C" int mi355x_swiglu_quantize_fp8(const void* h, int rows, int width, float limit,
-                                          uint8_t* q, float* scales, void* stream) {
+                                          uint8_t* q, float* scales, void* act, void* stream) {
   MI355X_REQUIRE(width > 0 && width % 128 == 0, "swiglu_quantize: I must be a multiple of 128");
   if (rows == 0) return MI355X_OK;
   const long long units = (long long)rows * (width / 128);
   const long long blocks = (units + 16 * kSwUnits - 1) / (16 * kSwUnits);
   hipLaunchKernelGGL(swiglu_quantize_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     (hipStream_t)stream, (const uint16_t*)h, rows, width, limit, q, scales);
+                     (hipStream_t)stream, (const uint16_t*)h, rows, width, limit, q, scales,
+                     (uint16_t*)act);
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
 }

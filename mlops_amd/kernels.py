@@ -255,18 +255,22 @@ def quantize_rows(x: torch.Tensor, *, gate_up: bool = False):
     return q, scales
 
 
-def swiglu_quantize(h: torch.Tensor, limit: float | None = None):
-    """``silu(gate) * up`` of interleaved ``h [R, 2I]`` as ``(e4m3 [R,I], scales [I/128, R])``."""
+def swiglu_quantize(h: torch.Tensor, limit: float | None = None, *, activation: bool = False):
+    """``silu(gate) * up`` of interleaved ``h [R, 2I]`` as ``(e4m3 [R,I], scales [I/128, R])``,
+    followed by the bf16 activation ``[R, I]`` itself when ``activation``."""
     if h.dtype != torch.bfloat16 or h.ndim != 2 or h.shape[1] % 2:
         raise ValueError("swiglu_quantize takes bf16 [rows, 2I]")
     rows, width = h.shape[0], h.shape[1] // 2
     device = _on_gpu(h)
     q = torch.empty((rows, width), dtype=FP8, device=device)
     scales = torch.empty((width // 128, rows), dtype=torch.float32, device=device)
+    act = torch.empty((rows, width), dtype=torch.bfloat16, device=device) if activation else None
     nbytes = 4 * rows * width + rows * width + 4 * rows * (width // 128)
+    if activation:
+        nbytes += 2 * rows * width
     _timed("swiglu_quantize_fp8", device, 0, nbytes, "mi355x_swiglu_quantize_fp8", _ptr(h), rows,
-           width, _limit(limit), _ptr(q), _ptr(scales), _stream(device))
-    return q, scales
+           width, _limit(limit), _ptr(q), _ptr(scales), _ptr(act), _stream(device))
+    return (q, scales, act) if activation else (q, scales)
 
 
 def quantize_weight_blocks(w: torch.Tensor, *, transposed: bool = False):

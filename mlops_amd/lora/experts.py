@@ -1,0 +1,317 @@
+"""Expert LoRA on the MI355X block-FP8 MoE path.
+
+``expert_lora`` (reference: ``src/mlops/lora/experts.py:53-167``) is the
+routed MoE layer with a rank-r correction on both projections of every
+expert, ``W -> W + scale * B[e] @ A[e]``:
+
+    h13 = x @ W13[e]^T + scale * (x @ A13[e]^T) @ B13[e]^T
+    y   = a @ W2[e]^T  + scale * (a @ A2[e]^T) @ B2[e]^T,   a = SwiGLU(h13)
+
+The base weights are block-FP8 (``BlockFP8Weight`` containers, or plain
+masters quantized per call with ``compute_precision="fp8_block"``) and run on
+the MI355X grouped GEMMs. The low-rank terms enter those GEMMs through their
+bf16 ``addend`` operand, the form of the reference's SonicMoE composition
+(``providers/sonicmoe/lora.py:1-45``: the LoRA term joins the base GEMM's C
+input before SwiGLU, and the row gradient in place), so no LoRA term is added
+by a separate pass over ``[rows, 2I]``. The scale is folded into the small
+``B`` factors, which for the up projection are taken with their gate/up rows
+interleaved, the order of ``h13``.
+
+Rank projections of token rows (``x @ A13^T`` forward, ``dy @ B2`` backward)
+are formed once per token for all experts, as one dense ``[T, E*r]`` GEMM,
+and gathered to the routed rows; the rest are per-expert GEMMs over each
+expert's rows. These rank-r products and the factor gradients are plain
+library GEMMs (hipBLASLt through torch), bf16 operands with fp32 sums; the
+factor gradients come back at the factors' dtype (fp32 sums throughout).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import kernels, router
+from ..block_fp8 import BlockFP8Weight
+from ..dispatch.context import weight_gradient_dtype
+from ..providers.mi355x import moe as provider
+from ..routing import current_route_weight_precision, next_override
+
+IMPLEMENTATIONS = ("auto", "mi355x")
+
+
+def interleaved_rows(b: torch.Tensor) -> torch.Tensor:
+    """``[E, 2I, r]`` gate rows then up rows -> gate/up rows alternating
+    (reference ``providers/sonicmoe/lora.py:81-84``)."""
+    experts, packed, rank = b.shape
+    return b.view(experts, 2, packed // 2, rank).transpose(1, 2).reshape(b.shape)
+
+
+def gate_up_rows(b: torch.Tensor) -> torch.Tensor:
+    """Inverse of :func:`interleaved_rows`."""
+    experts, packed, rank = b.shape
+    return b.view(experts, packed // 2, 2, rank).transpose(1, 2).reshape(b.shape)
+
+
+def _segments(offsets: torch.Tensor):
+    """``[(expert, start, stop)]`` of the experts that have rows."""
+    bounds = offsets.tolist()
+    return [(e, bounds[e], bounds[e + 1]) for e in range(len(bounds) - 1)
+            if bounds[e + 1] > bounds[e]]
+
+
+def _per_expert(rows: torch.Tensor, factors: torch.Tensor, segments, out_cols: int,
+                *, transpose: bool) -> torch.Tensor:
+    """``rows[s:t] @ factors[e]^T`` (``transpose``) or ``rows[s:t] @ factors[e]``
+    for every expert segment, bf16 out (fp32 sums)."""
+    out = torch.zeros((rows.shape[0], out_cols), dtype=torch.bfloat16, device=rows.device)
+    for e, start, stop in segments:
+        f = factors[e].t() if transpose else factors[e]
+        torch.mm(rows[start:stop], f, out=out[start:stop])
+    return out
+
+
+def _token_projection(x_tok: torch.Tensor, factors_flat: torch.Tensor, experts: int,
+                      tokens_of_row: torch.Tensor, experts_of_row: torch.Tensor) -> torch.Tensor:
+    """Per routed row j: ``x_tok[token_j] @ F[e_j]`` with ``factors_flat``
+    ``[D, E*r]`` holding every expert's ``F[e]`` side by side: one dense GEMM
+    over the tokens, then the gather."""
+    projected = x_tok @ factors_flat
+    rank = factors_flat.shape[1] // experts
+    return projected.view(x_tok.shape[0], experts, rank)[tokens_of_row, experts_of_row]
+
+
+def _scatter_tokens(rows: torch.Tensor, tokens: int, experts: int,
+                    tokens_of_row: torch.Tensor, experts_of_row: torch.Tensor) -> torch.Tensor:
+    """``Z[t, e*r:(e+1)*r] = rows[j]`` for the row j of pair (t, e) (fp32,
+    zeros elsewhere): the token-side form of a per-row factor gradient."""
+    out = torch.zeros((tokens, experts, rows.shape[1]), dtype=torch.float32, device=rows.device)
+    out[tokens_of_row, experts_of_row] = rows.float()
+    return out.view(tokens, experts * rows.shape[1])
+
+
+def _weight_parts(weight):
+    """``(data, scale, data_t | None)`` of a block-FP8 container."""
+    data, scale = weight.components()
+    return data, scale, getattr(weight, "_transposed", None)
+
+
+class _ExpertLoRA(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, hidden, residual, router_weight, w13, w2, a13, b13, a2, b2, opts):
+        ctx.set_materialize_grads(False)
+        top_k, mode, scale, limit = opts["top_k"], opts["routing_mode"], opts["scale"], opts["limit"]
+        width = hidden.shape[-1]
+        tokens = hidden.numel() // width
+        experts = router_weight.shape[0]
+        w13_data, w13_scale, w13_t = _weight_parts(w13)
+        w2_data, w2_scale, w2_t = _weight_parts(w2)
+        inter = w2_data.shape[2]
+        with torch.no_grad():
+            x = hidden.reshape(tokens, width).contiguous()
+            base = residual.reshape(tokens, width).contiguous()
+            logits = router.router_logits(x, router_weight)
+            forced = next_override(tokens, experts, top_k, x.device)
+            bias = opts["router_bias"]
+            weights, ids = kernels.router_topk(
+                logits, top_k, mode, bias=bias, n_group=opts["n_group"],
+                topk_group=opts["topk_group"], routed_scaling=opts["routed_scaling"],
+                forced_ids=forced,
+            )
+            counts, offsets, order, slots = kernels.permute_plan(ids, experts)
+            order_l = order.long()
+            rows_token = order_l // top_k
+            rows_expert = ids.reshape(-1).long()[order_l]
+            segments = _segments(offsets)
+            # Factors at the activations' dtype, the scale folded into B.
+            a13b = a13.detach().to(torch.bfloat16)
+            b13b = interleaved_rows((b13.detach().float() * scale).to(torch.bfloat16))
+            a2b = a2.detach().to(torch.bfloat16)
+            b2b = (b2.detach().float() * scale).to(torch.bfloat16)
+            rank13, rank2 = a13b.shape[1], a2b.shape[1]
+            # Up projection: z13 = x @ A13^T per routed row; its B-term is the
+            # GEMM's addend.
+            z13 = _token_projection(x, a13b.reshape(experts * rank13, width).t(), experts,
+                                    rows_token, rows_expert)
+            c13 = _per_expert(z13, b13b, segments, 2 * inter, transpose=True)
+            xq, xs = kernels.permute_quantize(x, slots)
+            h13 = kernels.gemm(xq, xs, w13_data, w13_scale, offsets, interleave=True, addend=c13)
+            del c13
+            aq, as_, act = kernels.swiglu_quantize(h13, limit, activation=True)
+            # Down projection: z2 = a @ A2^T per routed row.
+            z2 = _per_expert(act, a2b, segments, rank2, transpose=True)
+            del act
+            c2 = _per_expert(z2, b2b, segments, width, transpose=True)
+            y = kernels.gemm(aq, as_, w2_data, w2_scale, offsets, addend=c2)
+            del c2
+            output = kernels.combine(y, slots, weights, base)
+            aux, probability_sum, _, _ = kernels.router_stats(logits, ids, top_k, mode,
+                                                              opts["lengths"])
+        ctx.opts = opts
+        ctx.segments = segments
+        ctx.w13_parts = (w13_data, w13_scale, w13_t)
+        ctx.w2_parts = (w2_data, w2_scale, w2_t)
+        ctx.factor_dtypes = (a13.dtype, b13.dtype, a2.dtype, b2.dtype)
+        ctx.save_for_backward(hidden, router_weight, logits, weights, ids, order, offsets, slots,
+                              h13, z13, z2, rows_token, rows_expert, a13b, b13b, a2b, b2b)
+        ctx.mark_non_differentiable(counts)
+        return output.reshape(hidden.shape), aux, counts, probability_sum
+
+    @staticmethod
+    def backward(ctx, grad_output, grad_aux, _grad_counts, grad_probability_sum):
+        (hidden, router_weight, logits, weights, ids, order, offsets, slots, h13, z13, z2,
+         rows_token, rows_expert, a13b, b13b, a2b, b2b) = ctx.saved_tensors
+        opts, segments = ctx.opts, ctx.segments
+        top_k, mode, scale, limit = opts["top_k"], opts["routing_mode"], opts["scale"], opts["limit"]
+        need = ctx.needs_input_grad
+        width = hidden.shape[-1]
+        tokens = hidden.numel() // width
+        experts = router_weight.shape[0]
+        assignments = order.numel()
+        w13_data, w13_scale, w13_t = ctx.w13_parts
+        w2_data, w2_scale, w2_t = ctx.w2_parts
+        inter = w2_data.shape[2]
+        rank13, rank2 = a13b.shape[1], a2b.shape[1]
+        grad_dtype = weight_gradient_dtype()
+        with torch.no_grad():
+            x = hidden.reshape(tokens, width).contiguous()
+            if grad_output is None:
+                dy = torch.zeros((tokens, width), dtype=torch.bfloat16, device=x.device)
+            else:
+                dy = grad_output.reshape(tokens, width).contiguous().to(torch.bfloat16)
+            # Row gradient of the activation, unscaled by the route weight:
+            # r = dy_j @ W2[e] + (dy_j @ (s B2[e])) @ A2[e].
+            u2 = _token_projection(dy, b2b.permute(1, 0, 2).reshape(width, experts * rank2),
+                                   experts, rows_token, rows_expert)
+            c_r = _per_expert(u2, a2b, segments, inter, transpose=False)
+            dyq, dys = kernels.permute_quantize(dy, slots)
+            w2_t = w2_t if w2_t is not None else kernels.transpose_fp8(w2_data)
+            r = kernels.gemm(dyq, dys, w2_t, w2_scale, offsets, transposed_scale=True, addend=c_r)
+            del c_r
+            dh, a_prime, dscore = kernels.routed_swiglu_backward(
+                r, h13, weights.reshape(-1), order, limit)
+            del r
+            # Input gradient: dx_j = dh_j @ W13[e] + (dh_j @ (s B13[e])) @ A13[e].
+            u13 = _per_expert(dh, b13b, segments, rank13, transpose=False)
+            c_x = _per_expert(u13, a13b, segments, width, transpose=False)
+            dhq, dhs = kernels.quantize_rows(dh, gate_up=True)
+            w13_t = w13_t if w13_t is not None else kernels.transpose_fp8(w13_data)
+            dx = kernels.gemm(dhq, dhs, w13_t, w13_scale, offsets, transposed_scale=True,
+                              addend=c_x)
+            del c_x, dhq, dhs
+            grad_hidden = kernels.unpermute_sum(dx, slots)
+            del dx
+            # Factor gradients (fp32 sums), scale applied once.
+            grads = [None, None, None, None]
+            if need[8]:    # B2: s * sum_j (score_j dy_j) z2_j^T
+                score = weights.reshape(-1)[order.long()]
+                zs = _scatter_tokens(z2.float() * score[:, None], tokens, experts,
+                                     rows_token, rows_expert)
+                g = (dy.float().t() @ zs) * scale
+                grads[3] = g.view(width, experts, rank2).permute(1, 0, 2).contiguous()
+            if need[7]:    # A2: sum_j u2_j a'_j^T, a' = score * a
+                g = torch.zeros((experts, rank2, inter), dtype=torch.float32, device=x.device)
+                for e, start, stop in segments:
+                    g[e] = u2[start:stop].float().t() @ a_prime[start:stop].float()
+                grads[2] = g
+            if need[6]:    # B13: s * sum_j dh_j z13_j^T (rows back to gate then up)
+                g = torch.zeros((experts, 2 * inter, rank13), dtype=torch.float32, device=x.device)
+                for e, start, stop in segments:
+                    g[e] = dh[start:stop].float().t() @ z13[start:stop].float()
+                grads[1] = gate_up_rows(g * scale)
+            if need[5]:    # A13: sum_j u13_j x_j^T, formed on the token side
+                zd = _scatter_tokens(u13, tokens, experts, rows_token, rows_expert)
+                grads[0] = (zd.t() @ x.float()).view(experts, rank13, width)
+            grads = [None if g is None else g.to(dtype)
+                     for g, dtype in zip(grads, ctx.factor_dtypes)]
+            # Base weight gradients, when the base is trained.
+            grad_w13 = grad_w2 = None
+            if need[3] or need[4]:
+                direct = grad_dtype if grad_dtype in (torch.bfloat16, torch.float32) else torch.float32
+                padded = kernels.wgrad_padded_rows(assignments, experts)
+                blocks = kernels.padded_row_blocks(offsets, padded)
+                common = dict(padded=padded, row_blocks=blocks)
+                if need[4]:
+                    dy_t, dy_ts, _ = kernels.quantize_transpose(
+                        dy, offsets, assignments, gather=order, gather_div=top_k, **common)
+                    ap_t, ap_ts, _ = kernels.quantize_transpose(a_prime, offsets, assignments,
+                                                                **common)
+                    grad_w2 = kernels.wgrad(dy_t, dy_ts, ap_t, ap_ts, offsets, out_dtype=direct,
+                                            rows=assignments)
+                if need[3]:
+                    dh_t, dh_ts, _ = kernels.quantize_transpose(dh, offsets, assignments,
+                                                                gate_up=True, **common)
+                    x_t, x_ts, _ = kernels.quantize_transpose(
+                        x, offsets, assignments, gather=order, gather_div=top_k, **common)
+                    grad_w13 = kernels.wgrad(dh_t, dh_ts, x_t, x_ts, offsets, out_dtype=direct,
+                                             rows=assignments)
+                logical = torch.bfloat16 if grad_dtype is None else grad_dtype
+                grad_w13 = None if grad_w13 is None else grad_w13.to(logical)
+                grad_w2 = None if grad_w2 is None else grad_w2.to(logical)
+            router_dtype = router_weight.dtype if grad_dtype is None else grad_dtype
+            grad_router = provider.routing_backward(
+                grad_hidden, x, router_weight, logits, weights, ids, dscore, slots, offsets,
+                grad_aux, grad_probability_sum, top_k=top_k, routing_mode=mode,
+                lengths=opts["lengths"], router_dtype=router_dtype, need_router=bool(need[2]),
+            )
+        grad_residual = None
+        if need[1] and grad_output is not None:
+            grad_residual = grad_output.clone()
+        return (grad_hidden.reshape(hidden.shape).to(hidden.dtype) if need[0] else None,
+                grad_residual, grad_router if need[2] else None, grad_w13, grad_w2,
+                *grads, None)
+
+
+def expert_lora(
+    hidden, residual, router_weight, gate_up, down, a13, b13, a2, b2, *, top_k, routing_mode,
+    scale, router_bias=None, n_group=1, topk_group=1, routed_scaling=1.0, lengths=None,
+    swiglu_limit=None, implementation="auto", compute_precision=None,
+):
+    """Routed MoE with per-expert LoRA factors: ``(output, aux, counts,
+    probability_sum)`` as ``mlops.lora.experts.expert_lora`` returns them.
+
+    Weights ``gate_up [E, 2I, D]`` (gate rows then up rows) and ``down
+    [E, D, I]``, factors ``a13 [E, r, D]``, ``b13 [E, 2I, r]``, ``a2 [E, r, I]``,
+    ``b2 [E, D, r]`` (any float dtype, computed in bf16), ``router_weight
+    [E, D]``. Routing options and ``swiglu_limit`` are `mlops.moe`'s.
+    ``implementation`` is ``"auto"`` or ``"mi355x"`` (this build has no other
+    composition); ``compute_precision`` is ``None`` for block-FP8 containers
+    or ``"fp8_block"`` (plain masters quantized per call). Gradients reach the
+    factors, the router, the hidden and residual rows, and base weights that
+    require them (plain masters; straight through the per-call quantizer).
+    """
+    if implementation not in IMPLEMENTATIONS:
+        raise ValueError(f"unknown expert LoRA implementation {implementation!r}; this build "
+                         f"serves {IMPLEMENTATIONS}")
+    if swiglu_limit is not None:
+        swiglu_limit = float(swiglu_limit)
+        if not swiglu_limit > 0:
+            raise ValueError("swiglu_limit must be positive")
+    rows = hidden.numel() // hidden.shape[-1]
+    lengths = (rows,) if lengths is None else tuple(int(x) for x in lengths)
+    support = provider.supports(
+        hidden, residual, router_weight, gate_up, down, surface="semantic", top_k=top_k,
+        routing_mode=routing_mode, router_bias=router_bias, n_group=n_group,
+        topk_group=topk_group, routed_scaling=routed_scaling, lengths=lengths,
+        compute_precision=compute_precision, swiglu_limit=swiglu_limit,
+    )
+    if not support:
+        raise ValueError(f"the MI355X expert LoRA path does not apply here: {support.reason}")
+    experts, inter, width = router_weight.shape[0], down.shape[2], hidden.shape[-1]
+    rank = a13.shape[1]
+    expected = {"a13": (experts, rank, width), "b13": (experts, 2 * inter, rank),
+                "a2": (experts, a2.shape[1], inter), "b2": (experts, width, a2.shape[1])}
+    for name, factor in zip(expected, (a13, b13, a2, b2)):
+        if tuple(factor.shape) != expected[name]:
+            raise ValueError(f"LoRA factor {name} must have shape {expected[name]}, "
+                             f"got {tuple(factor.shape)}")
+        if not factor.is_floating_point() or factor.device != hidden.device:
+            raise ValueError(f"LoRA factor {name} must be a floating tensor on {hidden.device}")
+    w13, w2 = provider._containers(gate_up, down)
+    bias = None if router_bias is None or router_bias.numel() == 0 else router_bias
+    opts = dict(top_k=int(top_k), routing_mode=str(routing_mode), scale=float(scale),
+                limit=swiglu_limit, router_bias=bias, n_group=int(n_group),
+                topk_group=int(topk_group), routed_scaling=float(routed_scaling),
+                lengths=lengths, weight_precision=current_route_weight_precision())
+    return _ExpertLoRA.apply(hidden, residual, router_weight, w13, w2, a13, b13, a2, b2, opts)
+
+
+__all__ = ["expert_lora", "gate_up_rows", "interleaved_rows"]

@@ -238,29 +238,43 @@ def backward_routed(
         else:
             grad_w13 = skipped_gradient(h2, weight_grad_dtype)
         grad_h2 = kernels.unpermute_sum(dx, slots)
-        # Routing: score gradient + aux / probability-sum cotangents -> logits.
-        seg_offsets = seg_counts = None
-        if routing_mode == "sigmoid_noaux_tc" and grad_aux is not None:
-            _, _, seg_counts, seg_offsets = kernels.router_stats(
-                logits, route_ids, int(top_k), routing_mode, lengths
-            )
-        grad_logits = kernels.router_backward(
-            logits, route_weights, route_ids, dscore, slots, routing_mode,
-            grad_aux=grad_aux, grad_prob_sum=grad_probability_sum, offsets=offsets,
-            seg_offsets=seg_offsets, seg_counts=seg_counts,
+        grad_router = routing_backward(
+            grad_h2, x, router_weight, logits, route_weights, route_ids, dscore, slots, offsets,
+            grad_aux, grad_probability_sum, top_k=top_k, routing_mode=routing_mode,
+            lengths=lengths, router_dtype=router_dtype, need_router=need_router,
         )
-        if need_router:
-            grad_router = router.router_weight_gradient(grad_logits, x, router_dtype)
-            if grad_router.stride() != router_weight.stride():
-                aligned = torch.empty_strided(grad_router.shape, router_weight.stride(),
-                                              dtype=grad_router.dtype, device=grad_router.device)
-                aligned.copy_(grad_router)
-                grad_router = aligned
-        else:
-            grad_router = skipped_gradient(router_weight, router_dtype)
-        router.add_router_input_gradient_(grad_h2, grad_logits, router_weight)
     return (grad_h2.reshape(h2.shape).to(h2.dtype), grad_output.clone(), grad_router, grad_w13,
             grad_w2)
+
+
+def routing_backward(grad_h2, x, router_weight, logits, route_weights, route_ids, dscore, slots,
+                     offsets, grad_aux, grad_probability_sum, *, top_k, routing_mode, lengths,
+                     router_dtype, need_router=True):
+    """Score gradient ``dscore`` (per sorted row) and the aux / probability-sum
+    cotangents through the router: returns the router weight's gradient (a
+    placeholder when not needed) and adds the router's input gradient to
+    ``grad_h2`` in place."""
+    seg_offsets = seg_counts = None
+    if routing_mode == "sigmoid_noaux_tc" and grad_aux is not None:
+        _, _, seg_counts, seg_offsets = kernels.router_stats(
+            logits, route_ids, int(top_k), routing_mode, lengths
+        )
+    grad_logits = kernels.router_backward(
+        logits, route_weights, route_ids, dscore, slots, routing_mode,
+        grad_aux=grad_aux, grad_prob_sum=grad_probability_sum, offsets=offsets,
+        seg_offsets=seg_offsets, seg_counts=seg_counts,
+    )
+    if need_router:
+        grad_router = router.router_weight_gradient(grad_logits, x, router_dtype)
+        if grad_router.stride() != router_weight.stride():
+            aligned = torch.empty_strided(grad_router.shape, router_weight.stride(),
+                                          dtype=grad_router.dtype, device=grad_router.device)
+            aligned.copy_(grad_router)
+            grad_router = aligned
+    else:
+        grad_router = skipped_gradient(router_weight, router_dtype)
+    router.add_router_input_gradient_(grad_h2, grad_logits, router_weight)
+    return grad_router
 
 
 # --------------------------------------------------------------------------
@@ -596,5 +610,6 @@ __all__ = [
     "backward_routed",
     "forward",
     "forward_routed",
+    "routing_backward",
     "supports",
 ]

@@ -363,13 +363,17 @@ def router_logits(x, router_weight):
 # -------------------------------------------------------------- full layer
 def native_moe(h2, residual, router_weight, w13, w2, *, top_k, routing_mode, router_bias=None,
                n_group=1, topk_group=1, routed_scaling=1.0, lengths=None, swiglu_limit=None,
-               compute_dtype=torch.float32):
+               compute_dtype=torch.float32, lora=None):
     """The reference's native oracle -- kernels/moe_reference.py:20-109: every
     expert runs on every row, masked by its route coefficient. Differentiable
     (plain autograd). Computed at ``compute_dtype`` (fp32 by default).
     ``w13``/``w2`` are ``[E, ...]`` tensors or lists of per-expert ``[...]``
     tensors (same values; per-expert leaves avoid autograd materializing a
-    full ``[E, ...]`` gradient for every expert's slice)."""
+    full ``[E, ...]`` gradient for every expert's slice).
+
+    ``lora = (a13, b13, a2, b2, scale)`` adds expert LoRA as
+    lora/experts.py:46-50 and :160-163 compose it: each projection
+    ``v @ W[e]^T`` becomes ``v @ W[e]^T + scale * (v @ A[e]^T) @ B[e]^T``."""
     shape = h2.shape
     x = h2.reshape(-1, shape[-1])
     res = residual.reshape_as(x)
@@ -389,11 +393,17 @@ def native_moe(h2, residual, router_weight, w13, w2, *, top_k, routing_mode, rou
     for e in range(experts):
         coef = (weights * (ids == e)).sum(-1)
         h13 = xc @ w13[e].to(compute_dtype).t()
+        if lora is not None:
+            a13, b13, scale = lora[0][e], lora[1][e], lora[4]
+            h13 = h13 + scale * (xc @ a13.to(compute_dtype).t()) @ b13.to(compute_dtype).t()
         g, u = h13[:, :width], h13[:, width:]
         if swiglu_limit is not None:
             g, u = g.clamp(max=swiglu_limit), u.clamp(-swiglu_limit, swiglu_limit)
         act = F.silu(g.float()).to(compute_dtype) * u
         y = act @ w2[e].to(compute_dtype).t()
+        if lora is not None:
+            a2, b2, scale = lora[2][e], lora[3][e], lora[4]
+            y = y + scale * (act @ a2.to(compute_dtype).t()) @ b2.to(compute_dtype).t()
         routed = routed + coef[:, None] * y.float()
     out = (res.float() + routed).to(h2.dtype)
     return out.reshape(shape), aux, counts, prob_sum

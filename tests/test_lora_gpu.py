@@ -1,0 +1,162 @@
+"""Expert LoRA (``mlops_amd.lora.expert_lora``) on the MI355X block-FP8 path.
+
+* Against the reference's native form on the dequantized base weights
+  (``oracle.native_moe(..., lora=...)``, fp32 autograd on the CPU), with the
+  reference's FP8 bounds for expert LoRA (tests/test_sonicmoe_lora.py:336-343:
+  8e-2 relative Frobenius), for a frozen FP8 base and for trained masters,
+  at aligned and unaligned ranks.
+* With zero B factors it is ``mlops_amd.moe`` (tests/test_sonicmoe_lora.py
+  :159-193): the forward bitwise, the gradients to summation order.
+"""
+
+import math
+
+import pytest
+import torch
+
+import mlops_amd
+from mlops_amd import BlockFP8Weight
+from mlops_amd.lora import expert_lora
+from oracle import moe_oracle as O
+from tests.conftest import frob_rel
+
+TOKENS, WIDTH, EXPERTS, INTER, TOP_K, SCALE = 256, 512, 8, 256, 2, 0.5
+BOUND = 8e-2
+
+
+def _inputs(device, rank, seed):
+    g = torch.Generator().manual_seed(seed)
+
+    def rnd(*shape, s=1.0, dtype=torch.float32):
+        return (torch.randn(*shape, generator=g) * s).to(dtype).to(device)
+
+    x, res = rnd(TOKENS, WIDTH, dtype=torch.bfloat16), rnd(TOKENS, WIDTH, dtype=torch.bfloat16)
+    wr = rnd(EXPERTS, WIDTH, s=WIDTH ** -0.5)
+    w13 = rnd(EXPERTS, 2 * INTER, WIDTH, s=WIDTH ** -0.5, dtype=torch.bfloat16)
+    w2 = rnd(EXPERTS, WIDTH, INTER, s=INTER ** -0.5, dtype=torch.bfloat16)
+    a13, b13 = rnd(EXPERTS, rank, WIDTH, s=WIDTH ** -0.5), rnd(EXPERTS, 2 * INTER, rank, s=rank ** -0.5)
+    a2, b2 = rnd(EXPERTS, rank, INTER, s=INTER ** -0.5), rnd(EXPERTS, WIDTH, rank, s=rank ** -0.5)
+    dy = rnd(TOKENS, WIDTH, dtype=torch.bfloat16)
+    return x, res, wr, w13, w2, a13, b13, a2, b2, dy
+
+
+def _leaf(t):
+    return t.detach().clone().requires_grad_(True)
+
+
+def _run_gpu(x, res, wr, w13, w2, a13, b13, a2, b2, dy, *, train_base, mode, limit=None):
+    x, wr = _leaf(x), _leaf(wr)
+    factors = [_leaf(t) for t in (a13, b13, a2, b2)]
+    if train_base:
+        w13, w2, precision = _leaf(w13), _leaf(w2), "fp8_block"
+    else:
+        w13, w2, precision = BlockFP8Weight.quantize(w13), BlockFP8Weight.quantize(w2), None
+    out, aux, counts, psum = expert_lora(
+        x, res, wr, w13, w2, *factors, top_k=TOP_K, routing_mode=mode, scale=SCALE,
+        swiglu_limit=limit, compute_precision=precision)
+    trainable = [x, wr, *factors] + ([w13, w2] if train_base else [])
+    grads = torch.autograd.grad((out.float() * dy.float()).sum() + 0.3 * aux, trainable)
+    return out.detach(), aux.detach(), counts, psum.detach(), grads
+
+
+def _run_oracle(x, res, wr, w13, w2, a13, b13, a2, b2, dy, *, train_base, mode, limit=None):
+    cpu = lambda t: t.detach().cpu()
+    # The base as the GPU path sees it: its block-FP8 values, dequantized.
+    w13d = O.dequantize_blocks(*O.quantize_blocks(cpu(w13).float()))
+    w2d = O.dequantize_blocks(*O.quantize_blocks(cpu(w2).float()))
+    xl, wrl = _leaf(cpu(x)), _leaf(cpu(wr))
+    w13l, w2l = _leaf(w13d), _leaf(w2d)
+    factors = [_leaf(cpu(t)) for t in (a13, b13, a2, b2)]
+    out, aux, counts, psum = O.native_moe(xl, cpu(res), wrl, w13l, w2l, top_k=TOP_K,
+                                          routing_mode=mode, swiglu_limit=limit,
+                                          lora=(*factors, SCALE))
+    trainable = [xl, wrl, *factors] + ([w13l, w2l] if train_base else [])
+    grads = torch.autograd.grad((out.float() * cpu(dy).float()).sum() + 0.3 * aux, trainable)
+    return out.detach(), aux.detach(), counts, psum.detach(), grads
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["topk_then_softmax", "softmax_then_topk", "sigmoid_noaux_tc"])
+@pytest.mark.parametrize("rank,train_base", [(16, False), (7, True), (1, False)])
+def test_expert_lora_matches_native_on_dequantized_weights(device, mode, rank, train_base):
+    case = _inputs(device, rank, seed=rank)
+    out, aux, counts, psum, grads = _run_gpu(*case, train_base=train_base, mode=mode)
+    r_out, r_aux, r_counts, r_psum, r_grads = _run_oracle(*case, train_base=train_base, mode=mode)
+    assert torch.equal(counts.cpu(), r_counts)
+    assert frob_rel(out.cpu().float(), r_out.float()) < 4e-2
+    assert abs(aux.item() - r_aux.item()) < 1e-4 * max(1.0, abs(r_aux.item()))
+    assert frob_rel(psum.cpu(), r_psum) < 1e-4
+    names = ["x", "router", "a13", "b13", "a2", "b2"] + (["w13", "w2"] if train_base else [])
+    for name, g, r in zip(names, grads, r_grads, strict=True):
+        assert g.shape == r.shape, name
+        err = frob_rel(g.cpu().float(), r.float())
+        assert err < BOUND, f"{name}: relative error {err:.3e}"
+    # Factor gradients come back at the factors' dtype, base ones at bf16.
+    assert all(g.dtype == torch.float32 for g in grads[2:6])
+    if train_base:
+        assert grads[6].dtype == grads[7].dtype == torch.bfloat16
+
+
+@pytest.mark.gpu
+def test_the_limit_reaches_the_lora_path(device):
+    """As tests/test_sonicmoe_lora.py:377-403 checks its FP8 base: FP8 moves
+    pre-activations by a few percent, enough to cross a limit inside the bulk
+    of them and move a gradient by whole elements, so parity with the native
+    form is taken at a limit far out (4.0, still clipping a few), and a tight
+    limit (0.75) must change the output and the hidden rows' gradient."""
+    case = _inputs(device, 16, seed=21)
+    got = _run_gpu(*case, train_base=False, mode="softmax_then_topk", limit=4.0)
+    ref = _run_oracle(*case, train_base=False, mode="softmax_then_topk", limit=4.0)
+    assert frob_rel(got[0].cpu().float(), ref[0].float()) < 4e-2
+    for g, r in zip(got[4], ref[4], strict=True):
+        assert frob_rel(g.cpu().float(), r.float()) < BOUND
+    clamped = _run_gpu(*case, train_base=False, mode="softmax_then_topk", limit=0.75)
+    plain = _run_gpu(*case, train_base=False, mode="softmax_then_topk")
+    assert frob_rel(clamped[0].float(), plain[0].float()) > 5e-2
+    assert frob_rel(clamped[4][0].float(), plain[4][0].float()) > 5e-2
+
+
+@pytest.mark.gpu
+def test_zero_b_factors_are_mlops_moe(device):
+    x, res, wr, w13, w2, a13, b13, a2, b2, dy = _inputs(device, 16, seed=5)
+    b13, b2 = torch.zeros_like(b13), torch.zeros_like(b2)
+    w13c, w2c = BlockFP8Weight.quantize(w13), BlockFP8Weight.quantize(w2)
+    options = dict(top_k=TOP_K, routing_mode="sigmoid_noaux_tc", n_group=2, topk_group=1,
+                   routed_scaling=1.5, lengths=(96, 160), swiglu_limit=2.75)
+
+    def run(lora):
+        xl, wrl = _leaf(x), _leaf(wr)
+        if lora:
+            outs = expert_lora(xl, res, wrl, w13c, w2c, a13, b13, a2, b2, scale=SCALE, **options)
+        else:
+            outs = mlops_amd.moe(xl, res, wrl, w13c, w2c, **options)
+        grads = torch.autograd.grad((outs[0].float() * dy.float()).sum() + 0.3 * outs[1],
+                                    [xl, wrl])
+        return [o.detach() for o in outs], grads
+
+    (outs, grads), (ref_outs, ref_grads) = run(True), run(False)
+    for a, b in zip(outs, ref_outs, strict=True):
+        assert torch.equal(a, b)
+    for a, b in zip(grads, ref_grads, strict=True):
+        assert frob_rel(a.float(), b.float()) < 1e-3
+
+
+def test_unknown_implementations_are_refused():
+    t = torch.zeros(1)
+    with pytest.raises(ValueError, match="unknown expert LoRA implementation"):
+        expert_lora(t, t, t, t, t, t, t, t, t, top_k=1, routing_mode="softmax_then_topk",
+                    scale=1.0, implementation="sonicmoe")
+    with pytest.raises(ValueError, match="swiglu_limit must be positive"):
+        expert_lora(t, t, t, t, t, t, t, t, t, top_k=1, routing_mode="softmax_then_topk",
+                    scale=1.0, swiglu_limit=0.0)
+
+
+def test_cpu_tensors_are_refused_with_the_reason():
+    x = torch.zeros(4, 128, dtype=torch.bfloat16)
+    wr = torch.zeros(2, 128)
+    w13, w2 = torch.zeros(2, 256, 128), torch.zeros(2, 128, 128)
+    a, b = torch.zeros(2, 4, 128), torch.zeros(2, 256, 4)
+    with pytest.raises(ValueError, match="does not apply here"):
+        expert_lora(x, x, wr, w13, w2, a, b, torch.zeros(2, 4, 128), torch.zeros(2, 128, 4),
+                    top_k=1, routing_mode="softmax_then_topk", scale=1.0,
+                    compute_precision="fp8_block")

@@ -385,3 +385,57 @@ def test_golden_cases():
         assert order.tolist() == case["order"], case["name"]
         assert offsets.tolist() == case["offsets"], case["name"]
         assert slots.reshape(-1).tolist() == case["slots"], case["name"]
+
+
+# --------------------------------------------------------------------------
+# Expert LoRA terms of the oracle (lora/experts.py:46-50, :160-163), pinned by
+# the LoRA identity W -> W + scale * B @ A, not by restating the formula.
+def _lora_case(seed=3, experts=4, width=24, inter=16, rank=5, tokens=20, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+
+    def rnd(*shape, s=1.0):
+        return (torch.randn(*shape, generator=g, dtype=torch.float64) * s).to(dtype)
+
+    x, res = rnd(tokens, width), rnd(tokens, width)
+    wr = rnd(experts, width, s=width ** -0.5)
+    w13, w2 = rnd(experts, 2 * inter, width, s=width ** -0.5), rnd(experts, width, inter, s=inter ** -0.5)
+    a13, b13 = rnd(experts, rank, width, s=width ** -0.5), rnd(experts, 2 * inter, rank, s=rank ** -0.5)
+    a2, b2 = rnd(experts, rank, inter, s=inter ** -0.5), rnd(experts, width, rank, s=rank ** -0.5)
+    return x, res, wr, w13, w2, a13, b13, a2, b2
+
+
+def test_oracle_lora_equals_the_merged_weights_forward_and_gradients():
+    """Expert LoRA is the layer with W' = W + s B@A: equal outputs, and the
+    factor gradients follow from the merged weight's by the chain rule
+    (dB = s dW' A^T, dA = s B^T dW'). A dropped scale, a transposed factor or
+    a gate/up mix-up in the LoRA terms fails this."""
+    x, res, wr, w13, w2, a13, b13, a2, b2 = _lora_case()
+    s = 0.7
+    opts = dict(top_k=2, routing_mode="softmax_then_topk", compute_dtype=torch.float64,
+                swiglu_limit=1.5)
+    leaves = [t.clone().requires_grad_(True) for t in (a13, b13, a2, b2)]
+    out, aux, _, _ = O.native_moe(x, res, wr, w13, w2, lora=(*leaves, s), **opts)
+    m13 = (w13 + s * b13 @ a13).requires_grad_(True)
+    m2 = (w2 + s * b2 @ a2).requires_grad_(True)
+    ref, ref_aux, _, _ = O.native_moe(x, res, wr, m13, m2, **opts)
+    assert torch.allclose(out, ref, rtol=1e-12, atol=1e-12)
+    upstream = torch.randn(out.shape, generator=torch.Generator().manual_seed(9), dtype=out.dtype)
+    ga13, gb13, ga2, gb2 = torch.autograd.grad((out * upstream).sum() + 0.3 * aux, leaves)
+    gm13, gm2 = torch.autograd.grad((ref * upstream).sum() + 0.3 * ref_aux, (m13, m2))
+    assert torch.allclose(gb13, s * gm13 @ a13.transpose(1, 2), rtol=1e-10, atol=1e-12)
+    assert torch.allclose(ga13, s * b13.transpose(1, 2) @ gm13, rtol=1e-10, atol=1e-12)
+    assert torch.allclose(gb2, s * gm2 @ a2.transpose(1, 2), rtol=1e-10, atol=1e-12)
+    assert torch.allclose(ga2, s * b2.transpose(1, 2) @ gm2, rtol=1e-10, atol=1e-12)
+
+
+def test_oracle_lora_with_zero_b_factors_is_the_plain_layer():
+    """lora/experts.py resets B to zero (:39-43): the layer is then mlops.moe's
+    (the reference's test_zero_factors_are_mlops_moe)."""
+    x, res, wr, w13, w2, a13, b13, a2, b2 = _lora_case(dtype=torch.float32)
+    opts = dict(top_k=2, routing_mode="sigmoid_noaux_tc", n_group=2, topk_group=1,
+                routed_scaling=1.5)
+    zero = (a13, torch.zeros_like(b13), a2, torch.zeros_like(b2), 0.5)
+    got = O.native_moe(x, res, wr, w13, w2, lora=zero, **opts)
+    ref = O.native_moe(x, res, wr, w13, w2, **opts)
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
