@@ -37,6 +37,11 @@ CONFIGS = {
     "qwen3_30b_a3b": dict(tokens=16384, hidden=2048, inter=768, experts=128, top_k=8),
     "deepseek_v3_shard": dict(tokens=4096, hidden=7168, inter=2048, experts=32, top_k=8),
     "mixtral_8x7b": dict(tokens=8192, hidden=4096, inter=14336, experts=8, top_k=2),
+    # Expert LoRA on a frozen block-FP8 base: rank-16 bf16 factors, logits
+    # N(0,1) + 2 on expert 0; gradients reach the factors, the router and the
+    # hidden rows only.
+    "mixtral_8x7b_lora": dict(tokens=8192, hidden=4096, inter=14336, experts=8, top_k=2,
+                              lora_rank=16),
     "config1": dict(tokens=256, hidden=512, inter=1024, experts=8, top_k=2),
 }
 
@@ -51,6 +56,41 @@ def make_inputs(cfg, device, seed=0):
     w2 = (torch.randn(e, h, i, generator=g, device=device) * 0.02).to(torch.bfloat16)
     dy = torch.randn(t, h, generator=g, device=device).to(torch.bfloat16)
     return x, res, wr, w13, w2, dy
+
+
+def make_lora_inputs(cfg, device, seed=0):
+    """The LoRA workload: the layer's inputs with a frozen block-FP8 base, a
+    +2 logit on expert 0 (a constant hidden feature the router reads) and
+    factors A ~ N(0, 0.01), B = 0.1 N(0, 1) in bf16."""
+    from mlops_amd import BlockFP8Weight
+
+    x, res, wr, w13, w2, dy = make_inputs(cfg, device, seed)
+    x[:, 0] = 1.0
+    wr[:, 0] = 0.0
+    wr[0, 0] = 2.0
+    g = torch.Generator(device=device).manual_seed(seed + 1)
+    e, r, h, i = cfg["experts"], cfg["lora_rank"], cfg["hidden"], cfg["inter"]
+
+    def factor(*shape, std):
+        return (torch.randn(*shape, generator=g, device=device) * std).to(torch.bfloat16)
+
+    factors = [factor(e, r, h, std=0.01), factor(e, 2 * i, r, std=0.1),
+               factor(e, r, i, std=0.01), factor(e, h, r, std=0.1)]
+    for t in factors:
+        t.requires_grad_(True)
+    w13c, w2c = BlockFP8Weight.quantize(w13), BlockFP8Weight.quantize(w2)
+    return x, res, wr, w13c, w2c, factors, dy
+
+
+def lora_step(args, cfg):
+    from mlops_amd.lora import expert_lora
+
+    x, res, wr, w13c, w2c, factors, dy = args
+    for t in (x, wr, *factors):
+        t.grad = None
+    out, aux, counts, psum = expert_lora(x, res, wr, w13c, w2c, *factors, top_k=cfg["top_k"],
+                                         routing_mode="topk_then_softmax", scale=2.0)
+    torch.autograd.backward([out, aux], [dy, torch.full_like(aux, 0.01)])
 
 
 def gpu_step(moe, args, cfg):
@@ -79,15 +119,25 @@ def cpu_baseline(cfg_name, sample_tokens=128, budget_s=20.0, max_iters=10):
     x, res, wr, w13, w2, dy = make_inputs(cfg, torch.device("cpu"))
     x.requires_grad_(True)
     wr.requires_grad_(True)
-    # Per-expert leaf weights (same values): the gradients are the same, without
-    # autograd materializing a full [E, ...] gradient for every expert's slice.
-    w13 = [w.clone().requires_grad_(True) for w in w13]
-    w2 = [w.clone().requires_grad_(True) for w in w2]
+    lora = None
+    if "lora_rank" in cfg:
+        # Frozen base, trainable factors (the LoRA workload's gradients).
+        e, r, h, i = cfg["experts"], cfg["lora_rank"], cfg["hidden"], cfg["inter"]
+        g = torch.Generator().manual_seed(1)
+        lora = (*[(torch.randn(*shape, generator=g) * std).requires_grad_(True)
+                  for shape, std in (((e, r, h), 0.01), ((e, 2 * i, r), 0.1),
+                                     ((e, r, i), 0.01), ((e, h, r), 0.1))], 2.0)
+        w13, w2 = list(w13), list(w2)
+    else:
+        # Per-expert leaf weights (same values): the gradients are the same, without
+        # autograd materializing a full [E, ...] gradient for every expert's slice.
+        w13 = [w.clone().requires_grad_(True) for w in w13]
+        w2 = [w.clone().requires_grad_(True) for w in w2]
 
     def step():
         out, aux, counts, psum = O.native_moe(x, res, wr, w13, w2, top_k=cfg["top_k"],
                                               routing_mode="topk_then_softmax",
-                                              compute_dtype=torch.float32)
+                                              compute_dtype=torch.float32, lora=lora)
         torch.autograd.backward([out, aux], [dy, torch.full_like(aux, 0.01)])
 
     for _ in range(2):
@@ -105,7 +155,8 @@ def cpu_baseline(cfg_name, sample_tokens=128, budget_s=20.0, max_iters=10):
         "cores": threads,
         "kind": "port",
         "sample": (f"{cfg_name} layer shape (H={cfg['hidden']}, I={cfg['inter']}, E={cfg['experts']}, "
-                   f"k={cfg['top_k']}) with {cfg['tokens']} tokens: reference native path (dense "
+                   f"k={cfg['top_k']}{', LoRA r=' + str(cfg['lora_rank']) + ' on a frozen base' if lora else ''}) "
+                   f"with {cfg['tokens']} tokens: reference native path (dense "
                    f"per-expert loop, masked, per-expert weight leaves) fwd+bwd in fp32 via torch autograd, median of "
                    f"{len(times)} runs after 2 warmups"),
         "ms_per_step": median * 1e3,
@@ -143,13 +194,21 @@ def main():
 
     cfg = CONFIGS[args.config]
     device = torch.device("cuda", 0)
-    inputs = make_inputs(cfg, device)
-    _, _, wr, w13, w2, _ = inputs
-    for t in (wr, w13, w2):
-        t.requires_grad_(True)
+    lora = "lora_rank" in cfg
+    if lora:
+        inputs = make_lora_inputs(cfg, device)
+        inputs[0].requires_grad_(True)
+        inputs[2].requires_grad_(True)
+        step = lambda: lora_step(inputs, cfg)
+    else:
+        inputs = make_inputs(cfg, device)
+        _, _, wr, w13, w2, _ = inputs
+        for t in (wr, w13, w2):
+            t.requires_grad_(True)
+        step = lambda: gpu_step(mlops_amd.moe, inputs, cfg)
 
     for _ in range(args.warmup):
-        gpu_step(mlops_amd.moe, inputs, cfg)
+        step()
     torch.cuda.synchronize()
 
     timer = kernels.LaunchTimer()
@@ -157,7 +216,7 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        gpu_step(mlops_amd.moe, inputs, cfg)
+        step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     kernels.set_launch_timer(None)
@@ -166,7 +225,9 @@ def main():
     ms_per_step = elapsed / args.steps * 1e3
     tokens_per_s = cfg["tokens"] * args.steps / elapsed
     a = cfg["tokens"] * cfg["top_k"]
-    layer_flops = 18 * a * cfg["hidden"] * cfg["inter"]
+    # fwd + input gradients + weight gradients; a frozen base has no weight
+    # gradients (the rank-r LoRA products add under 1%, not counted).
+    layer_flops = (12 if lora else 18) * a * cfg["hidden"] * cfg["inter"]
 
     gemm = summary.get("gemm_fp8_block", {})
     achieved = gemm["flops"] / (gemm["ms_total"] * 1e-3) / 1e12 if gemm else None
@@ -201,7 +262,9 @@ def main():
             "workload": f"{args.config} MoE layer fwd+bwd, block-FP8",
             **cfg,
             "routing_mode": "topk_then_softmax",
-            "weights": "bf16 masters quantized per call (128x128 blocks)",
+            "weights": ("frozen block-FP8 base (128x128 blocks), rank-16 bf16 LoRA factors, "
+                        "logits +2 on expert 0" if lora else
+                        "bf16 masters quantized per call (128x128 blocks)"),
         },
         "layer_tflops": layer_flops * args.steps / elapsed / 1e12,
         "gemm_tflops_all": all_gemm_flops / (all_gemm_ms * 1e-3) / 1e12 if all_gemm_ms else None,

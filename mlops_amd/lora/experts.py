@@ -61,11 +61,21 @@ def _segments(offsets: torch.Tensor):
 def _per_expert(rows: torch.Tensor, factors: torch.Tensor, segments, out_cols: int,
                 *, transpose: bool) -> torch.Tensor:
     """``rows[s:t] @ factors[e]^T`` (``transpose``) or ``rows[s:t] @ factors[e]``
-    for every expert segment, bf16 out (fp32 sums)."""
-    out = torch.zeros((rows.shape[0], out_cols), dtype=torch.bfloat16, device=rows.device)
+    for every expert segment, bf16 out (fp32 sums). The segments cover every
+    row."""
+    out = torch.empty((rows.shape[0], out_cols), dtype=torch.bfloat16, device=rows.device)
     for e, start, stop in segments:
         f = factors[e].t() if transpose else factors[e]
         torch.mm(rows[start:stop], f, out=out[start:stop])
+    return out
+
+
+def _factor_grad(left: torch.Tensor, right: torch.Tensor, segments, shape) -> torch.Tensor:
+    """``sum over each expert's rows of left_j right_j^T`` -> fp32 ``[E, *shape]``:
+    ``left[s:t]^T @ right[s:t]`` from bf16 operands with fp32 sums and output."""
+    out = torch.zeros(shape, dtype=torch.float32, device=left.device)
+    for e, start, stop in segments:
+        torch.mm(left[start:stop].t(), right[start:stop], out_dtype=torch.float32, out=out[e])
     return out
 
 
@@ -88,12 +98,6 @@ def _scatter_tokens(rows: torch.Tensor, tokens: int, experts: int,
     return out.view(tokens, experts * rows.shape[1])
 
 
-def _weight_parts(weight):
-    """``(data, scale, data_t | None)`` of a block-FP8 container."""
-    data, scale = weight.components()
-    return data, scale, getattr(weight, "_transposed", None)
-
-
 class _ExpertLoRA(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, residual, router_weight, w13, w2, a13, b13, a2, b2, opts):
@@ -102,8 +106,8 @@ class _ExpertLoRA(torch.autograd.Function):
         width = hidden.shape[-1]
         tokens = hidden.numel() // width
         experts = router_weight.shape[0]
-        w13_data, w13_scale, w13_t = _weight_parts(w13)
-        w2_data, w2_scale, w2_t = _weight_parts(w2)
+        w13_data, w13_scale = w13.components()
+        w2_data, w2_scale = w2.components()
         inter = w2_data.shape[2]
         with torch.no_grad():
             x = hidden.reshape(tokens, width).contiguous()
@@ -147,8 +151,7 @@ class _ExpertLoRA(torch.autograd.Function):
                                                               opts["lengths"])
         ctx.opts = opts
         ctx.segments = segments
-        ctx.w13_parts = (w13_data, w13_scale, w13_t)
-        ctx.w2_parts = (w2_data, w2_scale, w2_t)
+        ctx.w13, ctx.w2 = w13, w2
         ctx.factor_dtypes = (a13.dtype, b13.dtype, a2.dtype, b2.dtype)
         ctx.save_for_backward(hidden, router_weight, logits, weights, ids, order, offsets, slots,
                               h13, z13, z2, rows_token, rows_expert, a13b, b13b, a2b, b2b)
@@ -166,8 +169,8 @@ class _ExpertLoRA(torch.autograd.Function):
         tokens = hidden.numel() // width
         experts = router_weight.shape[0]
         assignments = order.numel()
-        w13_data, w13_scale, w13_t = ctx.w13_parts
-        w2_data, w2_scale, w2_t = ctx.w2_parts
+        w13_data, w13_scale = ctx.w13.components()
+        w2_data, w2_scale = ctx.w2.components()
         inter = w2_data.shape[2]
         rank13, rank2 = a13b.shape[1], a2b.shape[1]
         grad_dtype = weight_gradient_dtype()
@@ -183,7 +186,7 @@ class _ExpertLoRA(torch.autograd.Function):
                                    experts, rows_token, rows_expert)
             c_r = _per_expert(u2, a2b, segments, inter, transpose=False)
             dyq, dys = kernels.permute_quantize(dy, slots)
-            w2_t = w2_t if w2_t is not None else kernels.transpose_fp8(w2_data)
+            w2_t = provider.transposed_data(ctx.w2)
             r = kernels.gemm(dyq, dys, w2_t, w2_scale, offsets, transposed_scale=True, addend=c_r)
             del c_r
             dh, a_prime, dscore = kernels.routed_swiglu_backward(
@@ -193,7 +196,7 @@ class _ExpertLoRA(torch.autograd.Function):
             u13 = _per_expert(dh, b13b, segments, rank13, transpose=False)
             c_x = _per_expert(u13, a13b, segments, width, transpose=False)
             dhq, dhs = kernels.quantize_rows(dh, gate_up=True)
-            w13_t = w13_t if w13_t is not None else kernels.transpose_fp8(w13_data)
+            w13_t = provider.transposed_data(ctx.w13)
             dx = kernels.gemm(dhq, dhs, w13_t, w13_scale, offsets, transposed_scale=True,
                               addend=c_x)
             del c_x, dhq, dhs
@@ -201,25 +204,21 @@ class _ExpertLoRA(torch.autograd.Function):
             del dx
             # Factor gradients (fp32 sums), scale applied once.
             grads = [None, None, None, None]
-            if need[8]:    # B2: s * sum_j (score_j dy_j) z2_j^T
+            if need[8]:    # B2: s * sum_j (score_j dy_j) z2_j^T, on the token side
                 score = weights.reshape(-1)[order.long()]
-                zs = _scatter_tokens(z2.float() * score[:, None], tokens, experts,
+                zs = _scatter_tokens(z2.float() * (score[:, None] * scale), tokens, experts,
                                      rows_token, rows_expert)
-                g = (dy.float().t() @ zs) * scale
+                g = dy.float().t() @ zs
                 grads[3] = g.view(width, experts, rank2).permute(1, 0, 2).contiguous()
             if need[7]:    # A2: sum_j u2_j a'_j^T, a' = score * a
-                g = torch.zeros((experts, rank2, inter), dtype=torch.float32, device=x.device)
-                for e, start, stop in segments:
-                    g[e] = u2[start:stop].float().t() @ a_prime[start:stop].float()
-                grads[2] = g
+                grads[2] = _factor_grad(u2, a_prime, segments, (experts, rank2, inter))
             if need[6]:    # B13: s * sum_j dh_j z13_j^T (rows back to gate then up)
-                g = torch.zeros((experts, 2 * inter, rank13), dtype=torch.float32, device=x.device)
-                for e, start, stop in segments:
-                    g[e] = dh[start:stop].float().t() @ z13[start:stop].float()
-                grads[1] = gate_up_rows(g * scale)
+                g = _factor_grad(dh, z13, segments, (experts, 2 * inter, rank13))
+                grads[1] = gate_up_rows(g.mul_(scale))
             if need[5]:    # A13: sum_j u13_j x_j^T, formed on the token side
                 zd = _scatter_tokens(u13, tokens, experts, rows_token, rows_expert)
-                grads[0] = (zd.t() @ x.float()).view(experts, rank13, width)
+                grads[0] = torch.mm(zd.t().to(torch.bfloat16), x, out_dtype=torch.float32
+                                    ).view(experts, rank13, width)
             grads = [None if g is None else g.to(dtype)
                      for g, dtype in zip(grads, ctx.factor_dtypes)]
             # Base weight gradients, when the base is trained.

@@ -301,6 +301,26 @@ def _transposed(weight, data):
     return weight[2] if len(weight) == 3 else kernels.transpose_fp8(data)
 
 
+def transposed_data(container: BlockFP8Weight) -> torch.Tensor:
+    """The container's e4m3 data transposed per expert (``[E, in, out]``), the
+    operand layout of the input-gradient GEMMs. A per-call quantized weight
+    carries it from the quantizer's own pass; otherwise it is made once and
+    kept on the container for as long as the data's version counter (bumped
+    by every in-place write through torch) is unchanged, so a frozen base is
+    transposed once, not at every backward. It occupies as much memory as
+    the data."""
+    carried = getattr(container, "_transposed", None)
+    if carried is not None:
+        return carried
+    data = container._data
+    cached = getattr(container, "_transposed_cache", None)
+    if cached is not None and cached[0] == data._version and cached[1] is data:
+        return cached[2]
+    result = kernels.transpose_fp8(data)
+    container._transposed_cache = (data._version, data, result)
+    return result
+
+
 @torch.library.custom_op("mlops_mi355x::moe_mi355x_block_fp8_fwd", mutates_args=())
 def _forward_op(
     h2: torch.Tensor, residual: torch.Tensor, router_weight: torch.Tensor,
@@ -401,11 +421,14 @@ def _container_rule(cls, func, types, args, kwargs):
     args = list(args)
     components = list(args[-1])
     transposed = []
+    backward = func is torch.ops.mlops_mi355x.moe_mi355x_block_fp8_bwd.default
     for index, value in enumerate(args):
         if isinstance(value, BlockFP8Weight):
             args[index] = value._data
             components.append(value._scale)
-            transposed.append(getattr(value, "_transposed", None))
+            # The input-gradient GEMMs read the transposed copies.
+            transposed.append(transposed_data(value) if backward
+                              else getattr(value, "_transposed", None))
     if len(transposed) == 2 and all(t is not None for t in transposed):
         components.extend(transposed)
     args[-1] = components
@@ -612,4 +635,5 @@ __all__ = [
     "forward_routed",
     "routing_backward",
     "supports",
+    "transposed_data",
 ]
