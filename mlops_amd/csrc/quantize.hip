@@ -280,6 +280,83 @@ __global__ void __launch_bounds__(256) swiglu_quantize_kernel(const uint16_t* __
 // Block = (padded 128-row block, 128 source columns).
 constexpr int kQtPitch = 128 + 8;  // bf16 per LDS row: 272 B keeps 16-byte row alignment
 
+// Every thread of the block calls this (it holds barriers); `active` ones
+// (t in [0, 256)) do the work. The bf16 tile [128 rows][128 columns] becomes
+// 128 feature rows of the weight-gradient layout: thread (4 columns fg, 16
+// rows rb) takes its values and column maxima (combined over the 8 row
+// groups through pmax), quantizes with power-of-two scales and stages the
+// bytes in LDS as [column][row] over the tile's own memory (every read of
+// the tile is behind the first barrier); then 8 lanes per column write its
+// 128 rows as one whole 128-byte line. Column lc is feature feat0 + lc, or,
+// with gate_half > 0 (an interleaved gate/up source), source column c0 + lc
+// -> gate (even) or up (odd) feature.
+constexpr int kQtLine = 128 + 16;  // LDS bytes per staged feature row
+
+__device__ __forceinline__ int tile_feature(int lc, int feat0, int c0, int gate_half) {
+  if (gate_half == 0) return feat0 + lc;
+  const int src = c0 + lc;
+  return (src & 1) ? gate_half + (src >> 1) : (src >> 1);
+}
+
+__device__ __forceinline__ void transpose_tile_pow2(bool active, uint16_t* tile,
+                                                    float (*pmax)[128], int t, uint8_t* qt,
+                                                    float* scales, int feat0, int c0,
+                                                    int gate_half, int width_f, int padded,
+                                                    int pb) {
+  const int fg = t & 31, rb = t >> 5;
+  float v[16][4];
+  float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint2 d = *(const uint2*)&tile[(rb * 16 + i) * kQtPitch + 4 * fg];
+      v[i][0] = bf16_to_f32(d.x & 0xffff);
+      v[i][1] = bf16_to_f32(d.x >> 16);
+      v[i][2] = bf16_to_f32(d.y & 0xffff);
+      v[i][3] = bf16_to_f32(d.y >> 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) m[j] = fmaxf(m[j], fabsf(v[i][j]));
+    }
+    *(float4*)&pmax[rb][4 * fg] = make_float4(m[0], m[1], m[2], m[3]);
+  }
+  __syncthreads();
+  uint8_t* staged = reinterpret_cast<uint8_t*>(tile);
+  if (active) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const float4 q = *(const float4*)&pmax[r][4 * fg];
+      m[0] = fmaxf(m[0], q.x);
+      m[1] = fmaxf(m[1], q.y);
+      m[2] = fmaxf(m[2], q.z);
+      m[3] = fmaxf(m[3], q.w);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float sc = pow2_ceil(fmaxf(m[j] * kInv448, kMinScale));
+      const float inv = 1.0f / sc;  // exact: sc is a power of two
+      auto q = [&](int i) { return fminf(fmaxf(v[i][j] * inv, -kE4M3Max), kE4M3Max); };
+      uint4 w;
+      w.x = f32x4_to_e4m3(q(0), q(1), q(2), q(3));
+      w.y = f32x4_to_e4m3(q(4), q(5), q(6), q(7));
+      w.z = f32x4_to_e4m3(q(8), q(9), q(10), q(11));
+      w.w = f32x4_to_e4m3(q(12), q(13), q(14), q(15));
+      *(uint4*)&staged[(4 * fg + j) * kQtLine + rb * 16] = w;
+      if (rb == 0)
+        scales[(size_t)pb * width_f + tile_feature(4 * fg + j, feat0, c0, gate_half)] = sc;
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int lc = pass * 32 + (t >> 3), part = t & 7;
+    const int feat = tile_feature(lc, feat0, c0, gate_half);
+    *(uint4*)(qt + (size_t)feat * padded + (size_t)pb * 128 + part * 16) =
+        *(const uint4*)&staged[lc * kQtLine + part * 16];
+  }
+}
+
+
 __global__ void __launch_bounds__(256) quantize_transpose_kernel(
     const uint16_t* __restrict__ x, int64_t pitch, int width, const int32_t* __restrict__ gather,
     int gather_div, int gate_up, const int32_t* __restrict__ row_blocks, int padded,
@@ -306,45 +383,8 @@ __global__ void __launch_bounds__(256) quantize_transpose_kernel(
     }
   }
   __syncthreads();
-  // Thread: 4 columns (fg) x 16 rows (rb); column amax over the 8 row blocks.
-  const int fg = tid & 31, rb = tid >> 5;
-  float v[16][4];
-  float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const uint2 d = *(const uint2*)&tile[(rb * 16 + i) * kQtPitch + 4 * fg];
-    v[i][0] = bf16_to_f32(d.x & 0xffff);
-    v[i][1] = bf16_to_f32(d.x >> 16);
-    v[i][2] = bf16_to_f32(d.y & 0xffff);
-    v[i][3] = bf16_to_f32(d.y >> 16);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) m[j] = fmaxf(m[j], fabsf(v[i][j]));
-  }
-  *(float4*)&pmax[rb][4 * fg] = make_float4(m[0], m[1], m[2], m[3]);
-  __syncthreads();
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const float4 q = *(const float4*)&pmax[r][4 * fg];
-    m[0] = fmaxf(m[0], q.x);
-    m[1] = fmaxf(m[1], q.y);
-    m[2] = fmaxf(m[2], q.z);
-    m[3] = fmaxf(m[3], q.w);
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int src_col = c0 + 4 * fg + j;
-    const int feat = gate_up ? ((src_col & 1) ? width / 2 + (src_col >> 1) : (src_col >> 1)) : src_col;
-    const float sc = pow2_ceil(fmaxf(m[j] * kInv448, kMinScale));
-    const float inv = 1.0f / sc;  // exact: sc is a power of two
-    auto q = [&](int i) { return fminf(fmaxf(v[i][j] * inv, -kE4M3Max), kE4M3Max); };
-    uint4 w;
-    w.x = f32x4_to_e4m3(q(0), q(1), q(2), q(3));
-    w.y = f32x4_to_e4m3(q(4), q(5), q(6), q(7));
-    w.z = f32x4_to_e4m3(q(8), q(9), q(10), q(11));
-    w.w = f32x4_to_e4m3(q(12), q(13), q(14), q(15));
-    *(uint4*)(qt + (size_t)feat * padded + (size_t)pb * 128 + rb * 16) = w;
-    if (rb == 0) scales[(size_t)pb * width + feat] = sc;
-  }
+  transpose_tile_pow2(true, tile, pmax, tid, qt, scales, c0, c0, gate_up ? width / 2 : 0, width,
+                      padded, pb);
 }
 
 // ---------------------------------------------------------------------------
@@ -420,54 +460,6 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
 //     features cb*128 + j and I + cb*128 + j, a' features cb*128 + j) with
 //     power-of-two scales, as quantize_transpose_kernel does.
 constexpr int kSbThreads = 512;
-
-// Every thread of the block calls this (it holds a barrier); `active` ones
-// (t in [0, 256): 4 features fg x 16 rows rb) do the work.
-__device__ __forceinline__ void transpose_tile_pow2(bool active, const uint16_t* tile,
-                                                    float (*pmax)[128], int t, uint8_t* qt,
-                                                    float* scales, int feat0, int width_f,
-                                                    int padded, int pb) {
-  const int fg = t & 31, rb = t >> 5;
-  float v[16][4];
-  float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (active) {
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const uint2 d = *(const uint2*)&tile[(rb * 16 + i) * kQtPitch + 4 * fg];
-    v[i][0] = bf16_to_f32(d.x & 0xffff);
-    v[i][1] = bf16_to_f32(d.x >> 16);
-    v[i][2] = bf16_to_f32(d.y & 0xffff);
-    v[i][3] = bf16_to_f32(d.y >> 16);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) m[j] = fmaxf(m[j], fabsf(v[i][j]));
-  }
-  *(float4*)&pmax[rb][4 * fg] = make_float4(m[0], m[1], m[2], m[3]);
-  }
-  __syncthreads();
-  if (!active) return;
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const float4 q = *(const float4*)&pmax[r][4 * fg];
-    m[0] = fmaxf(m[0], q.x);
-    m[1] = fmaxf(m[1], q.y);
-    m[2] = fmaxf(m[2], q.z);
-    m[3] = fmaxf(m[3], q.w);
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int feat = feat0 + 4 * fg + j;
-    const float sc = pow2_ceil(fmaxf(m[j] * kInv448, kMinScale));
-    const float inv = 1.0f / sc;
-    auto q = [&](int i) { return fminf(fmaxf(v[i][j] * inv, -kE4M3Max), kE4M3Max); };
-    uint4 w;
-    w.x = f32x4_to_e4m3(q(0), q(1), q(2), q(3));
-    w.y = f32x4_to_e4m3(q(4), q(5), q(6), q(7));
-    w.z = f32x4_to_e4m3(q(8), q(9), q(10), q(11));
-    w.w = f32x4_to_e4m3(q(12), q(13), q(14), q(15));
-    *(uint4*)(qt + (size_t)feat * padded + (size_t)pb * 128 + rb * 16) = w;
-    if (rb == 0) scales[(size_t)pb * width_f + feat] = sc;
-  }
-}
 
 __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
     const uint16_t* __restrict__ rmat, const uint16_t* __restrict__ h,
@@ -576,14 +568,15 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
   const int half = tid >> 8, t = tid & 255;
   if (dht != nullptr)
     transpose_tile_pow2(true, tiles[half], pmax[half], t, dht, dhts, half * width + cb * 128,
-                        2 * width, padded, pb);
+                        0, 0, 2 * width, padded, pb);
   if (apt != nullptr) {
     __syncthreads();  // tile 0 and pmax[0] reuse
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass)
       *(uint4*)&tiles[0][(pass * 32 + rsub) * kQtPitch + jl] = apk[pass];
     __syncthreads();
-    transpose_tile_pow2(half == 0, tiles[0], pmax[0], t, apt, apts, cb * 128, width, padded, pb);
+    transpose_tile_pow2(half == 0, tiles[0], pmax[0], t, apt, apts, cb * 128, 0, 0, width,
+                        padded, pb);
   }
 }
 
