@@ -195,7 +195,13 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     uint16_t* obase = out + (size_t)(ct.row0 + wm * 64) * N + ct.nt * BN + wn * 128;
     const uint16_t* cbase = addend == nullptr ? nullptr
         : addend + (size_t)(ct.row0 + wm * 64) * N + ct.nt * BN + wn * 128;
-    const uint32_t lane_col = (lane & 15) * 8;
+    // The lane id passes through an empty asm here, so the per-row store
+    // addresses are computed where they are used. Hoisted above the K loop
+    // (they depend only on the tile and the lane) they would be live across
+    // it and spill, and every store would wait on a scratch reload.
+    uint32_t elane = lane;
+    asm volatile("" : "+v"(elane));
+    const uint32_t lane_col = (elane & 15) * 8;
     // SwiGLU fused into the up projection (gate/up mode with act_q): the
     // activation of the stored bf16 gate/up pairs, quantized 1x128 as
     // swiglu_quantize_kernel does. A lane holds 4 of a row's 64 act columns
@@ -212,7 +218,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
         const int i = half * 2 + ii;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int lrow = i * 16 + 4 * (lane >> 4) + r;  // row within the wave's 64
+          const int lrow = i * 16 + 4 * (elane >> 4) + r;  // row within the wave's 64
           float v[8];
           if (interleave) {
 #pragma unroll
