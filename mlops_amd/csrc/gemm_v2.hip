@@ -48,7 +48,7 @@ __device__ __forceinline__ int weight_row(int tr, int nt, int interleave, int ha
   return jb < 4 ? j : half_n + j;
 }
 
-template <bool kAct>
+template <bool kAct, bool kAdd>
 __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ a_scale, int rows,
     const uint8_t* __restrict__ w, const float* __restrict__ w_scale, int w_scale_t, int experts,
@@ -193,7 +193,9 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     // columns) -> one 16-byte store per row, rounding to bf16 once. Wave
     // base pointer + 32-bit per-lane offsets.
     uint16_t* obase = out + (size_t)(ct.row0 + wm * 64) * N + ct.nt * BN + wn * 128;
-    const uint16_t* cbase = addend == nullptr ? nullptr
+    // kAdd: a bf16 addend is given (a separate instantiation, so the plain
+    // kernel carries none of its registers).
+    const uint16_t* cbase = !kAdd ? nullptr
         : addend + (size_t)(ct.row0 + wm * 64) * N + ct.nt * BN + wn * 128;
     // The lane id passes through an empty asm here, so the per-row store
     // addresses are computed where they are used. Hoisted above the K loop
@@ -213,6 +215,21 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       float act[2][4][4];
+      // The addend's 8 rows of this half, loaded before its first store:
+      // loads and stores share one completion counter, so a load issued
+      // after a store would wait for that store too.
+      uint4 cadd[2][4];
+      if (kAdd) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int lrow = (half * 2 + ii) * 16 + 4 * (elane >> 4) + r;
+            cadd[ii][r] = make_uint4(0, 0, 0, 0);
+            if (wm * 64 + lrow < ct.nvalid)
+              cadd[ii][r] = *(const uint4*)(cbase + (uint32_t)lrow * (uint32_t)N + lane_col);
+          }
+      }
 #pragma unroll
       for (int ii = 0; ii < 2; ++ii) {
         const int i = half * 2 + ii;
@@ -232,8 +249,8 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
           }
           if (wm * 64 + lrow < ct.nvalid) {
             const uint32_t off = (uint32_t)lrow * (uint32_t)N + lane_col;
-            if (cbase != nullptr) {
-              uint4 c = *(const uint4*)(cbase + off);
+            if (kAdd) {
+              const uint4 c = cadd[ii][r];
               uint32_t w4[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
               for (int m = 0; m < 4; ++m) {
@@ -317,16 +334,17 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
   if (n % BN != 0 || experts > kMaxExperts || (interleave && (n / 2) % 128 != 0)) return 1;
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   const int grid = upper < cu_count() ? upper : cu_count();
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream, a, a_scale,
+                       rows, w, w_scale, w_scale_t, experts, n, k, offsets, interleave,
+                       (const uint16_t*)addend, (uint16_t*)out, act_q, act_scales, limit);
+  };
   if (act_q != nullptr)
-    hipLaunchKernelGGL(grouped_gemm_v2_kernel<true>, dim3(grid), dim3(kThreads), 0,
-                       (hipStream_t)stream, a, a_scale, rows, w, w_scale, w_scale_t, experts, n, k,
-                       offsets, interleave, (const uint16_t*)addend, (uint16_t*)out, act_q,
-                       act_scales, limit);
+    addend != nullptr ? launch(grouped_gemm_v2_kernel<true, true>)
+                      : launch(grouped_gemm_v2_kernel<true, false>);
   else
-    hipLaunchKernelGGL(grouped_gemm_v2_kernel<false>, dim3(grid), dim3(kThreads), 0,
-                       (hipStream_t)stream, a, a_scale, rows, w, w_scale, w_scale_t, experts, n, k,
-                       offsets, interleave, (const uint16_t*)addend, (uint16_t*)out, nullptr,
-                       nullptr, 0.0f);
+    addend != nullptr ? launch(grouped_gemm_v2_kernel<false, true>)
+                      : launch(grouped_gemm_v2_kernel<false, false>);
   MI355X_LAUNCH_CHECK();
   return 0;
 }
