@@ -53,10 +53,13 @@ def router_weight_gradient(grad_logits, hidden, dtype) -> torch.Tensor:
     if operands is torch.float32:
         return (grad_logits.float().t() @ hidden.float()).to(dtype)
     rows = hidden.to(operands)
+    experts = grad_logits.shape[1]
     high = grad_logits.to(operands)
-    gradient = _product_fp32(high.t().contiguous(), rows)
     residue = (grad_logits.float() - high.float()).to(operands)
-    gradient.add_(_product_fp32(residue.t().contiguous(), rows))
+    # Both pieces in one GEMM, stacked along its output rows ([hi | mid]^T @
+    # rows, M = 2E): measured 1.4x faster than two M = E GEMMs on MI355X.
+    both = _product_fp32(torch.cat([high, residue], 1).t().contiguous(), rows)
+    gradient = both[:experts].add_(both[experts:])
     return gradient.to(dtype)
 
 
