@@ -295,3 +295,45 @@ def test_large_shapes_match_native_on_gpu(device, shape):
     assert frob_rel(r["g13"].float(), torch.stack([w.grad for w in w13d])) < 8e-2
     assert frob_rel(r["g2"].float(), torch.stack([w.grad for w in w2d])) < 8e-2
     assert frob_rel(r["gr"].float(), wrr.grad) < 8e-2
+
+
+@pytest.mark.parametrize("tokens,experts,top_k", [
+    (333, 16, 2),    # an odd token count; half the experts get no rows
+    (1, 8, 2),       # one token
+    (64, 64, 32),    # the largest top_k
+    (96, 512, 4),    # the largest expert count, most experts empty
+])
+def test_layer_edge_shapes_match_fp8_oracle(device, tokens, experts, top_k):
+    """Ragged and empty inputs at the layer: the upper half of the experts
+    never wins (a constant hidden feature with a strongly negative router
+    weight), so their weight gradients must be exactly zero; everything else
+    matches the fp8 oracle as in test_layer_matches_fp8_oracle."""
+    x, res, wr, w13, w2, dy = _inputs(device, tokens=tokens, hidden=256, experts=experts,
+                                      inter=256, seed=11)
+    x[:, 0] = 1.0
+    wr[:, 0] = 0.0
+    if top_k <= experts // 2:
+        wr[experts // 2:, 0] = -30.0
+    mode = "softmax_then_topk"
+    r = _run(x, res, wr, w13, w2, dy, top_k=top_k, routing_mode=mode)
+    w13q, w13s = r["w13c"].components()
+    w2q, w2s = r["w2c"].components()
+    cpu = lambda t: t.detach().cpu()
+    from mlops_amd import router
+    logits = router.router_logits(x, wr).cpu()
+    fwd = O.fp8_moe_forward(cpu(x), cpu(res), cpu(wr), cpu(w13q), cpu(w13s), cpu(w2q), cpu(w2s),
+                            top_k=top_k, routing_mode=mode, logits=logits)
+    assert torch.equal(r["counts"].cpu(), fwd["counts"])
+    assert frob_rel(r["out"].cpu().float(), fwd["out"].float()) < 1e-2
+    bwd = O.fp8_moe_backward(fwd, cpu(x), cpu(dy), cpu(wr), cpu(w13q), cpu(w13s), cpu(w2q),
+                             cpu(w2s), top_k=top_k, routing_mode=mode,
+                             grad_aux=torch.tensor(0.1), grad_prob_sum=None)
+    assert frob_rel(r["gx"].cpu().float(), bwd["grad_x"].float()) < 1e-2
+    assert frob_rel(r["gr"].cpu().float(), bwd["grad_router"]) < 1e-2
+    used = r["counts"].cpu() > 0
+    assert frob_rel(r["g13"].cpu().float()[used], bwd["dw13"][used]) < 1e-2
+    assert frob_rel(r["g2"].cpu().float()[used], bwd["dw2"][used]) < 1e-2
+    if top_k <= experts // 2:
+        assert not bool(used[experts // 2:].any())
+        assert bool((r["g13"][~used.to(device)] == 0).all())
+        assert bool((r["g2"][~used.to(device)] == 0).all())
