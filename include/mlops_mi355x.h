@@ -219,6 +219,23 @@ int mi355x_gemm_fp8_block(const uint8_t* a, const float* a_scale, int rows, cons
                           const int32_t* offsets, int interleave, const void* addend, void* out,
                           void* stream);
 
+/* mi355x_gemm_fp8_block with a rank-r term in place of the addend:
+ *   out[r, n] = (block-FP8 product as above) + sum_j lora_z[r, j] * lora_b[e][n', j]
+ * for rows r of expert e, where n' is the weight row feeding output column n
+ * (the same row the product reads: n itself, or in gate/up mode the
+ * gate-first row of the interleaved column). The rank term is a bf16 MFMA
+ * with fp32 sums that initialises the accumulators, so no [rows, N] addend
+ * is materialized. lora_z: bf16 [rows, R]; lora_b: bf16 [E, N, R]; R (the
+ * rank padded with zero columns) a multiple of 16 up to 256. N must be a
+ * multiple of 256. Replaces the LoRA C input of the expert-LoRA up and down
+ * GEMMs and the in-place LoRA branch of their row gradients
+ * (providers/sonicmoe/lora.py:1-45, _up_forward :189, _down_forward :540;
+ * block_fp8_gemm(c=) at kernels/quack_moe/block_fp8_gemm.py:1458). */
+int mi355x_gemm_fp8_block_lora(const uint8_t* a, const float* a_scale, int rows, const uint8_t* w,
+                               const float* w_scale, int w_scale_t, int experts, int n, int k,
+                               const int32_t* offsets, int interleave, const void* lora_z,
+                               const void* lora_b, int lora_rank, void* out, void* stream);
+
 /* The up projection with SwiGLU fused: mi355x_gemm_fp8_block in gate/up mode
  * (w13 [E, 2I, K], interleave = 1) writing h [rows, 2I] bf16 interleaved, and
  * from the same bf16 values act = silu(min(g, L)) * clamp(u, +-L) (limit <=

@@ -401,7 +401,8 @@ int persistent_grid(int tiles) {
 int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, const uint8_t* w,
                           const float* w_scale, int w_scale_t, int experts, int n, int k,
                           const int32_t* offsets, int interleave, const void* addend, void* out,
-                          uint8_t* act_q, float* act_scales, float limit, void* stream);
+                          uint8_t* act_q, float* act_scales, float limit, const void* lora_z,
+                          const void* lora_b, int lora_rank, void* stream);
 
 int mi355x_wgrad_v2_launch(const uint8_t* p, const float* p_scale, int m_features,
                            const uint8_t* q, const float* q_scale, int n_features, int padded,
@@ -423,13 +424,37 @@ extern "C" int mi355x_gemm_fp8_block(const uint8_t* a, const float* a_scale, int
   if (rows == 0) return MI355X_OK;
   const int v2 = mi355x_gemm_v2_launch(a, a_scale, rows, w, w_scale, w_scale_t, experts, n, k,
                                        offsets, interleave, addend, out, nullptr, nullptr, 0.0f,
-                                       stream);
+                                       nullptr, nullptr, 0, stream);
   if (v2 <= 0) return v2;
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   hipLaunchKernelGGL(grouped_gemm_kernel, dim3(persistent_grid(upper)), dim3(kThreads), 0,
                      (hipStream_t)stream, a, a_scale, rows, w, w_scale, w_scale_t, experts, n, k,
                      offsets, interleave, (const uint16_t*)addend, (uint16_t*)out);
   MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_gemm_fp8_block_lora(const uint8_t* a, const float* a_scale, int rows,
+                                          const uint8_t* w, const float* w_scale, int w_scale_t,
+                                          int experts, int n, int k, const int32_t* offsets,
+                                          int interleave, const void* lora_z, const void* lora_b,
+                                          int lora_rank, void* out, void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= kMaxExperts, "gemm_lora: experts must be in [1, %d]",
+                 kMaxExperts);
+  MI355X_REQUIRE(n > 0 && n % 256 == 0 && (!interleave || (n / 2) % 128 == 0),
+                 "gemm_lora: N must be a multiple of 256 (2I of 128), got %d", n);
+  MI355X_REQUIRE(k > 0 && k % BK == 0, "gemm_lora: K must be a multiple of %d, got %d", BK, k);
+  MI355X_REQUIRE(lora_rank > 0 && lora_rank % 16 == 0 && lora_rank <= 256,
+                 "gemm_lora: the (padded) rank must be a multiple of 16 in [16, 256], got %d",
+                 lora_rank);
+  MI355X_REQUIRE(lora_z != nullptr && lora_b != nullptr, "gemm_lora: z and b are required");
+  MI355X_REQUIRE(rows >= 0, "gemm_lora: negative rows");
+  if (rows == 0) return MI355X_OK;
+  const int v2 = mi355x_gemm_v2_launch(a, a_scale, rows, w, w_scale, w_scale_t, experts, n, k,
+                                       offsets, interleave, nullptr, out, nullptr, nullptr, 0.0f,
+                                       lora_z, lora_b, lora_rank, stream);
+  if (v2 < 0) return v2;
+  MI355X_REQUIRE(v2 == 0, "gemm_lora: shape outside the pipelined kernel");
   return MI355X_OK;
 }
 
@@ -446,7 +471,8 @@ extern "C" int mi355x_gemm_fp8_block_swiglu(const uint8_t* a, const float* a_sca
   MI355X_REQUIRE(rows >= 0, "gemm_swiglu: negative rows");
   if (rows == 0) return MI355X_OK;
   const int v2 = mi355x_gemm_v2_launch(a, a_scale, rows, w, w_scale, 0, experts, n, k, offsets, 1,
-                                       addend, h, act_q, act_scales, limit, stream);
+                                       addend, h, act_q, act_scales, limit, nullptr, nullptr, 0,
+                                       stream);
   if (v2 <= 0) return v2;
   // Shapes outside the pipelined kernel: the GEMM, then the SwiGLU pass.
   const int rc = mi355x_gemm_fp8_block(a, a_scale, rows, w, w_scale, 0, experts, n, k, offsets, 1,

@@ -48,13 +48,16 @@ __device__ __forceinline__ int weight_row(int tr, int nt, int interleave, int ha
   return jb < 4 ? j : half_n + j;
 }
 
-template <bool kAct, bool kAdd>
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+template <bool kAct, bool kAdd, bool kLora>
 __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ a_scale, int rows,
     const uint8_t* __restrict__ w, const float* __restrict__ w_scale, int w_scale_t, int experts,
     int N, int K, const int32_t* __restrict__ offsets, int interleave,
     const uint16_t* __restrict__ addend, uint16_t* __restrict__ out,
-    uint8_t* __restrict__ act_q, float* __restrict__ act_scales, float limit) {
+    uint8_t* __restrict__ act_q, float* __restrict__ act_scales, float limit,
+    const uint16_t* __restrict__ lora_z, const uint16_t* __restrict__ lora_b, int lora_rank) {
   __shared__ __align__(1024) uint8_t smem[kStages * STAGE_BYTES];
   __shared__ float act_amax[2][BM];  // per-row amax of each wave column's 64 act columns
   __shared__ int prefix[kMaxExperts + 1];
@@ -134,6 +137,33 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[i][j] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (kLora) {
+      // The accumulators start from the rank-r product z[row] . b[e][col]
+      // (bf16 MFMA, fp32 sums, 16 of the rank at a time): the low-rank term
+      // of out = A W^T + z B^T joins before the block products, with no
+      // [rows, N] addend in memory. A lane's z fragment is 4 consecutive
+      // rank entries of its A row (16x16x16 operand layout), its b fragment
+      // 4 of the weight row feeding its B column, the same rows the
+      // operand copies use; the result lands in the accumulator layout of
+      // the fp8 MFMA.
+      const int zl = lane & 15, kq = 4 * (lane >> 4);
+      for (int kc = 0; kc < lora_rank; kc += 16) {
+        v4s zf[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = min(ct.row0 + wm * 64 + i * 16 + zl, rows - 1);
+          zf[i] = *(const v4s*)(lora_z + (size_t)row * lora_rank + kc + kq);
+        }
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb) {
+          const int wrow = weight_row(wn * 128 + jb * 16 + zl, ct.nt, interleave, half_n);
+          const v4s bf = *(const v4s*)(lora_b + ((size_t)ct.e * N + wrow) * lora_rank + kc + kq);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc[i][jb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(zf[i], bf, acc[i][jb], 0, 0, 0);
+        }
+      }
+    }
 
     for (int kb = 0; kb < nk; ++kb) {
       wait_and_sync<0>();  // two stages: the only loads in flight are this step's
@@ -330,21 +360,27 @@ int cu_count() {
 int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, const uint8_t* w,
                           const float* w_scale, int w_scale_t, int experts, int n, int k,
                           const int32_t* offsets, int interleave, const void* addend, void* out,
-                          uint8_t* act_q, float* act_scales, float limit, void* stream) {
+                          uint8_t* act_q, float* act_scales, float limit, const void* lora_z,
+                          const void* lora_b, int lora_rank, void* stream) {
   if (n % BN != 0 || experts > kMaxExperts || (interleave && (n / 2) % 128 != 0)) return 1;
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   const int grid = upper < cu_count() ? upper : cu_count();
   auto launch = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream, a, a_scale,
                        rows, w, w_scale, w_scale_t, experts, n, k, offsets, interleave,
-                       (const uint16_t*)addend, (uint16_t*)out, act_q, act_scales, limit);
+                       (const uint16_t*)addend, (uint16_t*)out, act_q, act_scales, limit,
+                       (const uint16_t*)lora_z, (const uint16_t*)lora_b, lora_rank);
   };
-  if (act_q != nullptr)
-    addend != nullptr ? launch(grouped_gemm_v2_kernel<true, true>)
-                      : launch(grouped_gemm_v2_kernel<true, false>);
-  else
-    addend != nullptr ? launch(grouped_gemm_v2_kernel<false, true>)
-                      : launch(grouped_gemm_v2_kernel<false, false>);
+  if (lora_z != nullptr) {
+    if (act_q != nullptr || addend != nullptr) return 1;  // not a form of this kernel
+    launch(grouped_gemm_v2_kernel<false, false, true>);
+  } else if (act_q != nullptr) {
+    addend != nullptr ? launch(grouped_gemm_v2_kernel<true, true, false>)
+                      : launch(grouped_gemm_v2_kernel<true, false, false>);
+  } else {
+    addend != nullptr ? launch(grouped_gemm_v2_kernel<false, true, false>)
+                      : launch(grouped_gemm_v2_kernel<false, false, false>);
+  }
   MI355X_LAUNCH_CHECK();
   return 0;
 }

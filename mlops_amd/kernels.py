@@ -421,8 +421,12 @@ def swiglu_bwd_quantize(r, h, weights, order, offsets, *, padded=None, limit=Non
 
 # ------------------------------------------------------------------- GEMMs
 def gemm(a, a_scale, w, w_scale, offsets, *, transposed_scale=False, interleave=False,
-         addend=None):
-    """Grouped block-FP8 GEMM: bf16 ``[A, N]`` (see the C header for the math)."""
+         addend=None, lora=None):
+    """Grouped block-FP8 GEMM: bf16 ``[A, N]`` (see the C header for the math).
+    ``lora = (z bf16 [A, R], b bf16 [E, N, R])``, R a multiple of 16: the
+    rank-R term ``z b[e]^T`` joins the accumulators (``mi355x_gemm_fp8_block_lora``)."""
+    if lora is not None:
+        return _gemm_lora(a, a_scale, w, w_scale, offsets, transposed_scale, interleave, *lora)
     rows, k = a.shape
     experts, n, wk = w.shape
     if a.dtype != FP8 or w.dtype != FP8 or wk != k:
@@ -440,6 +444,29 @@ def gemm(a, a_scale, w, w_scale, offsets, *, transposed_scale=False, interleave=
         "mi355x_gemm_fp8_block", _ptr(a), _ptr(a_scale), rows, _ptr(w), _ptr(w_scale),
         int(transposed_scale), experts, n, k, _ptr(offsets), int(interleave), _ptr(addend),
         _ptr(out), _stream(device),
+    )
+    return out
+
+
+def _gemm_lora(a, a_scale, w, w_scale, offsets, transposed_scale, interleave, z, b):
+    rows, k = a.shape
+    experts, n, wk = w.shape
+    if a.dtype != FP8 or w.dtype != FP8 or wk != k:
+        raise ValueError("gemm takes e4m3 rows [A,K] and e4m3 weights [E,N,K]")
+    _check(a_scale, (k // 128, rows), torch.float32, "row scales")
+    expected = (experts, k // 128, n // 128) if transposed_scale else (experts, n // 128, k // 128)
+    _check(w_scale, expected, torch.float32, "weight scales")
+    _check(offsets, (experts + 1,), torch.int32, "offsets")
+    rank = z.shape[1] if z.ndim == 2 else -1
+    _check(z, (rows, rank), torch.bfloat16, "LoRA z")
+    _check(b, (experts, n, rank), torch.bfloat16, "LoRA b")
+    device = _on_gpu(a, a_scale, w, w_scale, offsets, z, b)
+    out = torch.empty((rows, n), dtype=torch.bfloat16, device=device)
+    _timed(
+        "gemm_fp8_block", device, 2 * rows * n * k, rows * k + experts * n * k + 2 * rows * n,
+        "mi355x_gemm_fp8_block_lora", _ptr(a), _ptr(a_scale), rows, _ptr(w), _ptr(w_scale),
+        int(transposed_scale), experts, n, k, _ptr(offsets), int(interleave), _ptr(z), _ptr(b),
+        rank, _ptr(out), _stream(device),
     )
     return out
 

@@ -9,13 +9,13 @@ expert, ``W -> W + scale * B[e] @ A[e]``:
 
 The base weights are block-FP8 (``BlockFP8Weight`` containers, or plain
 masters quantized per call with ``compute_precision="fp8_block"``) and run on
-the MI355X grouped GEMMs. The low-rank terms enter those GEMMs through their
-bf16 ``addend`` operand, the form of the reference's SonicMoE composition
-(``providers/sonicmoe/lora.py:1-45``: the LoRA term joins the base GEMM's C
-input before SwiGLU, and the row gradient in place), so no LoRA term is added
-by a separate pass over ``[rows, 2I]``. The scale is folded into the small
-``B`` factors, which for the up projection are taken with their gate/up rows
-interleaved, the order of ``h13``.
+the MI355X grouped GEMMs. Each low-rank term ``z @ F^T`` starts the GEMM's
+fp32 accumulators (``mi355x_gemm_fp8_block_lora``: a rank-16-at-a-time bf16
+MFMA per output tile), where the reference's SonicMoE composition passes it
+as the GEMM's C input (``providers/sonicmoe/lora.py:1-45``): no LoRA term is
+materialized as ``[rows, N]`` or added by a separate pass. The scale is
+folded into the small ``B`` factors; ranks are padded with zero columns to a
+multiple of 16.
 
 Rank projections of token rows (``x @ A13^T`` forward, ``dy @ B2`` backward)
 are formed once per token for all experts, as one dense ``[T, E*r]`` GEMM,
@@ -49,6 +49,16 @@ def gate_up_rows(b: torch.Tensor) -> torch.Tensor:
     """Inverse of :func:`interleaved_rows`."""
     experts, packed, rank = b.shape
     return b.view(experts, packed // 2, 2, rank).transpose(1, 2).reshape(b.shape)
+
+
+def _padded(t: torch.Tensor, rank: int) -> torch.Tensor:
+    """``t [..., r]`` with zero columns up to ``rank``, contiguous."""
+    extra = rank - t.shape[-1]
+    return torch.nn.functional.pad(t, (0, extra)).contiguous() if extra else t.contiguous()
+
+
+def _rank16(r: int) -> int:
+    return -(-r // 16) * 16
 
 
 def _segments(offsets: torch.Tensor):
@@ -127,25 +137,26 @@ class _ExpertLoRA(torch.autograd.Function):
             segments = _segments(offsets)
             # Factors at the activations' dtype, the scale folded into B.
             a13b = a13.detach().to(torch.bfloat16)
-            b13b = interleaved_rows((b13.detach().float() * scale).to(torch.bfloat16))
+            b13s = (b13.detach().float() * scale).to(torch.bfloat16)
+            b13b = interleaved_rows(b13s)
             a2b = a2.detach().to(torch.bfloat16)
             b2b = (b2.detach().float() * scale).to(torch.bfloat16)
             rank13, rank2 = a13b.shape[1], a2b.shape[1]
-            # Up projection: z13 = x @ A13^T per routed row; its B-term is the
-            # GEMM's addend.
+            r13, r2 = _rank16(rank13), _rank16(rank2)
+            # Up projection: z13 = x @ A13^T per routed row; z13 (s B13)^T
+            # starts the GEMM's accumulators (B13 in its gate-first row order,
+            # the order of the weight rows the GEMM reads).
             z13 = _token_projection(x, a13b.reshape(experts * rank13, width).t(), experts,
                                     rows_token, rows_expert)
-            c13 = _per_expert(z13, b13b, segments, 2 * inter, transpose=True)
             xq, xs = kernels.permute_quantize(x, slots)
-            h13 = kernels.gemm(xq, xs, w13_data, w13_scale, offsets, interleave=True, addend=c13)
-            del c13
+            h13 = kernels.gemm(xq, xs, w13_data, w13_scale, offsets, interleave=True,
+                               lora=(_padded(z13, r13), _padded(b13s, r13)))
             aq, as_, act = kernels.swiglu_quantize(h13, limit, activation=True)
             # Down projection: z2 = a @ A2^T per routed row.
             z2 = _per_expert(act, a2b, segments, rank2, transpose=True)
             del act
-            c2 = _per_expert(z2, b2b, segments, width, transpose=True)
-            y = kernels.gemm(aq, as_, w2_data, w2_scale, offsets, addend=c2)
-            del c2
+            y = kernels.gemm(aq, as_, w2_data, w2_scale, offsets,
+                             lora=(_padded(z2, r2), _padded(b2b, r2)))
             output = kernels.combine(y, slots, weights, base)
             aux, probability_sum, _, _ = kernels.router_stats(logits, ids, top_k, mode,
                                                               opts["lengths"])
@@ -184,22 +195,22 @@ class _ExpertLoRA(torch.autograd.Function):
             # r = dy_j @ W2[e] + (dy_j @ (s B2[e])) @ A2[e].
             u2 = _token_projection(dy, b2b.permute(1, 0, 2).reshape(width, experts * rank2),
                                    experts, rows_token, rows_expert)
-            c_r = _per_expert(u2, a2b, segments, inter, transpose=False)
+            r2 = _rank16(rank2)
             dyq, dys = kernels.permute_quantize(dy, slots)
             w2_t = provider.transposed_data(ctx.w2)
-            r = kernels.gemm(dyq, dys, w2_t, w2_scale, offsets, transposed_scale=True, addend=c_r)
-            del c_r
+            r = kernels.gemm(dyq, dys, w2_t, w2_scale, offsets, transposed_scale=True,
+                             lora=(_padded(u2, r2), _padded(a2b.transpose(1, 2), r2)))
             dh, a_prime, dscore = kernels.routed_swiglu_backward(
                 r, h13, weights.reshape(-1), order, limit)
             del r
             # Input gradient: dx_j = dh_j @ W13[e] + (dh_j @ (s B13[e])) @ A13[e].
             u13 = _per_expert(dh, b13b, segments, rank13, transpose=False)
-            c_x = _per_expert(u13, a13b, segments, width, transpose=False)
+            r13 = _rank16(rank13)
             dhq, dhs = kernels.quantize_rows(dh, gate_up=True)
             w13_t = provider.transposed_data(ctx.w13)
             dx = kernels.gemm(dhq, dhs, w13_t, w13_scale, offsets, transposed_scale=True,
-                              addend=c_x)
-            del c_x, dhq, dhs
+                              lora=(_padded(u13, r13), _padded(a13b.transpose(1, 2), r13)))
+            del dhq, dhs
             grad_hidden = kernels.unpermute_sum(dx, slots)
             del dx
             # Factor gradients (fp32 sums), scale applied once.

@@ -211,7 +211,7 @@ def _ragged(counts):
 
 
 def _gemm_case(device, counts, n, k, *, seed, transposed=False, interleave=False, extreme=False,
-               addend=False):
+               addend=False, lora_rank=0):
     g = torch.Generator().manual_seed(seed)
     experts = len(counts)
     offsets = _ragged(counts)
@@ -232,12 +232,27 @@ def _gemm_case(device, counts, n, k, *, seed, transposed=False, interleave=False
         wd, ws = K.quantize_weight_blocks(w.to(device))
         wq_kernel = wd
     c = torch.randn(rows, n, generator=g).to(torch.bfloat16) if addend else None
+    lora = None
+    if lora_rank:
+        zz = (torch.randn(rows, lora_rank, generator=g) * 0.5).to(torch.bfloat16)
+        bb = (torch.randn(experts, n, lora_rank, generator=g) * 0.1).to(torch.bfloat16)
+        lora = (zz.to(device), bb.to(device))
     out = K.gemm(xq, xs, wq_kernel, ws, offsets.to(device), transposed_scale=transposed,
-                 interleave=interleave, addend=None if c is None else c.to(device))
+                 interleave=interleave, addend=None if c is None else c.to(device), lora=lora)
     want = O.grouped_gemm(xq.cpu(), xs.cpu(), wd.cpu(), ws.cpu(), offsets, transposed=transposed,
                           interleave=interleave)
     if c is not None:
         want = want + c.double()
+    if lora_rank:
+        # The rank term in weight-row order (gate rows, then up rows), then
+        # in the output's column order.
+        term = torch.zeros(rows, n, dtype=torch.float64)
+        for e in range(experts):
+            lo, hi = int(offsets[e]), int(offsets[e + 1])
+            term[lo:hi] = zz[lo:hi].double() @ bb[e].double().t()
+        if interleave:
+            term = term.view(rows, 2, n // 2).transpose(1, 2).reshape(rows, n)
+        want = want + term
     return out.cpu(), want, offsets
 
 
@@ -247,6 +262,9 @@ def _gemm_case(device, counts, n, k, *, seed, transposed=False, interleave=False
     dict(counts=[129, 64, 257], n=256, k=384, interleave=True),     # gate/up interleaved output
     dict(counts=[100, 200, 0, 33], n=256, k=512, transposed=True),  # input-gradient orientation
     dict(counts=[90, 190], n=128, k=256, addend=True),              # LoRA-style addend
+    dict(counts=[0, 70, 131, 15, 260], n=256, k=512, lora_rank=16),  # rank term, empty expert
+    dict(counts=[129, 64, 257], n=512, k=384, interleave=True, lora_rank=32),  # gate/up order
+    dict(counts=[100, 200, 0, 33], n=256, k=512, transposed=True, lora_rank=16),  # input gradient
 ])
 def test_grouped_gemm_matches_fp64(device, case):
     out, want, offsets = _gemm_case(device, seed=sum(case["counts"]), **case)
