@@ -156,21 +156,6 @@ int mi355x_quantize_transpose_fp8(const void* x, int64_t pitch, int width, const
                                   int gather_div, int gate_up, const int32_t* row_blocks,
                                   int padded, uint8_t* qt, float* scales, void* stream);
 
-/* Both operands of one routed activation in one pass over its gathered
- * rows: q [rows, width] e4m3 with scales [width/128][rows], the sorted rows
- * quantized 1x128 exactly as mi355x_permute_quantize_fp8 writes them (sorted
- * row r is source row gather[r] / gather_div, or r without gather), and
- * qt [width][padded] with qt_scales [padded/128][width], exactly as
- * mi355x_quantize_transpose_fp8 writes them (no gate/up mode). Replaces the
- * pair quantize_rows_fp8 (quantize_rows.py:140) + quantize_transpose_fp8
- * (quantize_transpose.py:126) that the weight-gradient path runs on the
- * same routed gradient rows (sonicmoe/moe.py:351-365). */
-int mi355x_permute_quantize_transpose_fp8(const void* x, int64_t pitch, int width,
-                                          const int32_t* gather, int gather_div,
-                                          const int32_t* row_blocks, int padded, int rows,
-                                          uint8_t* q, float* q_scales, uint8_t* qt,
-                                          float* qt_scales, void* stream);
-
 /* out[t] = bf16(residual[t] + sum_j weights[t,j] * y[slots[t,j]]), fp32 sum in
  * j order. Replaces combine (moe_dispatch.py:21-72, :168-196). */
 int mi355x_unpermute_combine(const void* y, const int32_t* slots, const float* weights,

@@ -41,8 +41,6 @@ SIGNATURES = {
     "mi355x_transpose_fp8": (_I, [_P, _I, _I, _I, _P, _P]),
     "mi355x_wgrad_padded_rows": (_S, [_I, _I]),
     "mi355x_padded_row_blocks": (_I, [_P, _I, _I, _P, _P]),
-    "mi355x_permute_quantize_transpose_fp8": (_I, [_P, _I64, _I, _P, _I, _P, _I, _I, _P, _P, _P,
-                                                   _P, _P]),
     "mi355x_quantize_transpose_fp8": (_I, [_P, _I64, _I, _P, _I, _I, _P, _I, _P, _P, _P]),
     "mi355x_unpermute_combine": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
     "mi355x_unpermute_sum": (_I, [_P, _P, _I, _I, _I, _P, _P]),

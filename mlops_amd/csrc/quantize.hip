@@ -357,12 +357,10 @@ __device__ __forceinline__ void transpose_tile_pow2(bool active, uint16_t* tile,
 }
 
 
-template <bool kRows>
 __global__ void __launch_bounds__(256) quantize_transpose_kernel(
     const uint16_t* __restrict__ x, int64_t pitch, int width, const int32_t* __restrict__ gather,
     int gather_div, int gate_up, const int32_t* __restrict__ row_blocks, int padded,
-    uint8_t* __restrict__ qt, float* __restrict__ scales, uint8_t* __restrict__ q,
-    float* __restrict__ q_scales, int rows) {
+    uint8_t* __restrict__ qt, float* __restrict__ scales) {
   __shared__ __align__(16) uint16_t tile[128 * kQtPitch];
   __shared__ __align__(16) float pmax[8][128];
   const int pb = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
@@ -385,27 +383,6 @@ __global__ void __launch_bounds__(256) quantize_transpose_kernel(
     }
   }
   __syncthreads();
-  if constexpr (kRows) {
-    // The same rows quantized 1x128 in sorted order (what
-    // permute_quantize_kernel writes for them): 16 lanes per row, one
-    // 128-byte line each, read from the tile before the transposer reuses it.
-    const int lane16 = tid & 15, grp = tid >> 4;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int rr = grp + 16 * i;
-      if (rr < nvalid) {  // uniform over the 16-lane group
-        float v[8];
-        unpack_bf16x8(*(const uint4*)&tile[rr * kQtPitch + lane16 * 8], v);
-        float amax = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
-        amax = group_max<16>(amax);
-        const float sc = fmaxf(amax * kInv448, kMinScale);
-        *(uint2*)(q + (size_t)(r0 + rr) * width + c0 + lane16 * 8) = quant8(v, sc);
-        if (lane16 == 0) q_scales[(size_t)cb * rows + r0 + rr] = sc;
-      }
-    }
-  }
   transpose_tile_pow2(true, tile, pmax, tid, qt, scales, c0, c0, gate_up ? width / 2 : 0, width,
                       padded, pb);
 }
@@ -722,31 +699,9 @@ extern "C" int mi355x_quantize_transpose_fp8(const void* x, int64_t pitch, int w
   MI355X_REQUIRE(gather == nullptr || gather_div > 0, "quantize_transpose: gather_div must be > 0");
   if (padded == 0) return MI355X_OK;
   dim3 grid(padded / 128, width / 128);
-  hipLaunchKernelGGL(quantize_transpose_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(quantize_transpose_kernel, grid, dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)x, pitch, width, gather, gather_div, gate_up, row_blocks,
-                     padded, qt, scales, nullptr, nullptr, 0);
-  MI355X_LAUNCH_CHECK();
-  return MI355X_OK;
-}
-
-extern "C" int mi355x_permute_quantize_transpose_fp8(const void* x, int64_t pitch, int width,
-                                                     const int32_t* gather, int gather_div,
-                                                     const int32_t* row_blocks, int padded,
-                                                     int rows, uint8_t* q, float* q_scales,
-                                                     uint8_t* qt, float* qt_scales,
-                                                     void* stream) {
-  MI355X_REQUIRE(width > 0 && width % 128 == 0,
-                 "permute_quantize_transpose: width must be a multiple of 128");
-  MI355X_REQUIRE(padded >= 0 && padded % 128 == 0,
-                 "permute_quantize_transpose: padded must be a multiple of 128");
-  MI355X_REQUIRE(gather == nullptr || gather_div > 0,
-                 "permute_quantize_transpose: gather_div must be > 0");
-  MI355X_REQUIRE(rows >= 0, "permute_quantize_transpose: negative rows");
-  if (padded == 0 || rows == 0) return MI355X_OK;
-  dim3 grid(padded / 128, width / 128);
-  hipLaunchKernelGGL(quantize_transpose_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, pitch, width, gather, gather_div, 0, row_blocks, padded,
-                     qt, qt_scales, q, q_scales, rows);
+                     padded, qt, scales);
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
 }

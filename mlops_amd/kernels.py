@@ -346,31 +346,6 @@ def quantize_transpose(
     return qt, scales, padded
 
 
-def permute_quantize_transpose(x: torch.Tensor, offsets: torch.Tensor, assignments: int, *,
-                               gather, gather_div: int, padded: int, row_blocks):
-    """:func:`permute_quantize` and :func:`quantize_transpose` of the same routed
-    rows in one pass: ``(q [A, W] e4m3, scales [W/128, A], qt [W, P],
-    qt_scales [P/128, W])``, each bitwise what the separate kernel writes."""
-    if x.dtype != torch.bfloat16 or x.ndim != 2:
-        raise ValueError("permute_quantize_transpose takes bf16 [rows, width]")
-    width = x.shape[1]
-    experts = offsets.numel() - 1
-    device = _on_gpu(x, offsets, gather, row_blocks)
-    _check(row_blocks, (padded // 128, 2), torch.int32, "row_blocks")
-    _check(gather, (assignments,), torch.int32, "gather")
-    q = torch.empty((assignments, width), dtype=FP8, device=device)
-    scales = torch.empty((width // 128, assignments), dtype=torch.float32, device=device)
-    qt = torch.empty((width, padded), dtype=FP8, device=device)
-    qt_scales = torch.empty((padded // 128, width), dtype=torch.float32, device=device)
-    nbytes = 2 * assignments * width + assignments * width + width * padded
-    _timed("permute_quantize_transpose", device, 0, nbytes,
-           "mi355x_permute_quantize_transpose_fp8", _ptr(x), x.stride(0), width, _ptr(gather),
-           int(gather_div), _ptr(row_blocks), int(padded), assignments, _ptr(q), _ptr(scales),
-           _ptr(qt), _ptr(qt_scales), _stream(device))
-    del experts
-    return q, scales, qt, qt_scales
-
-
 def combine(y, slots, weights, residual):
     """``residual[t] + sum_j weights[t,j] * y[slots[t,j]]`` in fp32, rounded once."""
     tokens, top_k = slots.shape

@@ -201,27 +201,24 @@ def backward_routed(
         dy = grad_output.reshape(rows, width).contiguous()
         if dy.dtype != torch.bfloat16:
             dy = dy.to(torch.bfloat16)
-        padded = kernels.wgrad_padded_rows(assignments, experts)
-        blocks = kernels.padded_row_blocks(offsets, padded)
-        # The routed dy rows, quantized for the input-gradient GEMM and, when
-        # W2's gradient is wanted, transposed for it, in one pass.
-        if need_w2:
-            dyq, dys, dy_t, dy_ts = kernels.permute_quantize_transpose(
-                dy, offsets, assignments, gather=order, gather_div=int(top_k), padded=padded,
-                row_blocks=blocks)
-        else:
-            dyq, dys = kernels.permute_quantize(dy, slots)
         # Through the down projection: r = dy_routed @ W2, then SwiGLU backward.
+        dyq, dys = kernels.permute_quantize(dy, slots)
         w2_t = _transposed(w2, w2_data)
         r = kernels.gemm(dyq, dys, w2_t, w2_scale, offsets, transposed_scale=True)
         # SwiGLU backward fused with the quantizers of its outputs: dh row-
         # quantized for the input gradient, dh and a' transposed for the
         # weight gradients (each only when that gradient is wanted).
+        padded = kernels.wgrad_padded_rows(assignments, experts)
+        blocks = kernels.padded_row_blocks(offsets, padded)
         dhq, dhs, dh_t, dh_ts, ap_t, ap_ts, dscore, _ = kernels.swiglu_bwd_quantize(
             r, h13, route_weights.reshape(-1), order, offsets, padded=padded, limit=swiglu_limit,
             transposed_dh=need_w13, transposed_ap=need_w2, row_blocks=blocks,
         )
         if need_w2:
+            dy_t, dy_ts, _ = kernels.quantize_transpose(
+                dy, offsets, assignments, gather=order, gather_div=int(top_k), padded=padded,
+                row_blocks=blocks,
+            )
             grad_w2 = _grad_at(kernels.wgrad(dy_t, dy_ts, ap_t, ap_ts, offsets, out_dtype=direct,
                                              rows=assignments),
                                weight_grad_dtype)

@@ -424,41 +424,3 @@ def test_gemm_swiglu_fused_matches_separate_pass(device, limit, inter):
     q_ref, s_ref = K.swiglu_quantize(h, limit)
     assert torch.equal(_bytes(act), _bytes(q_ref))
     assert torch.equal(act_s, s_ref)
-
-
-def test_permute_quantize_transpose_equals_the_separate_kernels(device):
-    """One pass over the gathered rows writes, byte for byte, what
-    permute_quantize and quantize_transpose write separately (empty experts,
-    partial blocks, extreme and zero rows included)."""
-    g = torch.Generator().manual_seed(17)
-    tokens, top_k, experts, width = 300, 3, 9, 384
-    ids = torch.stack([torch.randperm(experts - 2, generator=g)[:top_k] for _ in range(tokens)])
-    ids = ids.to(torch.int32).to(device)  # the last two experts stay empty
-    x = torch.randn(tokens, width, generator=g)
-    x[5] = 0.0
-    x[7] *= 2.0 ** 20
-    x = x.to(torch.bfloat16).to(device)
-    counts, offsets, order, slots = K.permute_plan(ids, experts)
-    assignments = tokens * top_k
-    padded = K.wgrad_padded_rows(assignments, experts)
-    blocks = K.padded_row_blocks(offsets, padded)
-    q, qs, qt, qts = K.permute_quantize_transpose(x, offsets, assignments, gather=order,
-                                                  gather_div=top_k, padded=padded,
-                                                  row_blocks=blocks)
-    q_ref, qs_ref = K.permute_quantize(x, slots)
-    qt_ref, qts_ref, _ = K.quantize_transpose(x, offsets, assignments, gather=order,
-                                              gather_div=top_k, padded=padded, row_blocks=blocks)
-    assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
-    assert torch.equal(qs, qs_ref)
-    # Padding between experts is written by neither kernel: compare the rows
-    # each expert owns.
-    bounds = offsets.tolist()
-    start = 0
-    for e in range(experts):
-        n = bounds[e + 1] - bounds[e]
-        if n:
-            cols = slice(start, start + n)
-            assert torch.equal(qt[:, cols].view(torch.uint8), qt_ref[:, cols].view(torch.uint8)), e
-        start += -(-n // 128) * 128
-    used = [b for b in range(padded // 128) if blocks[b, 1] > 0]
-    assert torch.equal(qts[used], qts_ref[used])
