@@ -236,6 +236,15 @@ int mi355x_gemm_fp8_block_lora(const uint8_t* a, const float* a_scale, int rows,
                                const int32_t* offsets, int interleave, const void* lora_z,
                                const void* lora_b, int lora_rank, void* out, void* stream);
 
+/* Thin grouped product of expert LoRA: out[r, 0:R] = sum_k a[r, k] *
+ * bt[e][0:R, k] for the rows r of expert e (offsets[E+1]), a bf16 [rows, K],
+ * bt bf16 [E, R, K], out bf16 [rows, R], fp32 sums; K a multiple of 32, R a
+ * multiple of 16 up to 64. Replaces the rank projections of expert LoRA that
+ * stream routed rows (lora/grouped.py grouped_linear of lora/experts.py:47,
+ * :49; sonicmoe/lora.py _low :87, _through :98). */
+int mi355x_rank_product(const void* a, int rows, int k, const void* bt, int rank,
+                        const int32_t* offsets, int experts, void* out, void* stream);
+
 /* The up projection with SwiGLU fused: mi355x_gemm_fp8_block in gate/up mode
  * (w13 [E, 2I, K], interleave = 1) writing h [rows, 2I] bf16 interleaved, and
  * from the same bf16 values act = silu(min(g, L)) * clamp(u, +-L) (limit <=

@@ -54,6 +54,7 @@ SIGNATURES = {
         _I,
         [_P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _P],
     ),
+    "mi355x_rank_product": (_I, [_P, _I, _I, _P, _I, _P, _I, _P, _P]),
     "mi355x_gemm_fp8_block_lora": (_I, [_P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _I,
                                         _P, _P]),
     "mi355x_gemm_fp8_block_swiglu": (

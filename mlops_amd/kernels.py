@@ -448,6 +448,21 @@ def gemm(a, a_scale, w, w_scale, offsets, *, transposed_scale=False, interleave=
     return out
 
 
+def rank_product(a, bt, offsets):
+    """``out[r] = a[r] @ bt[e]^T`` for the rows of each expert: bf16 ``[rows, R]``
+    from bf16 ``a [rows, K]`` and ``bt [E, R, K]`` (``mi355x_rank_product``)."""
+    rows, k = a.shape
+    experts, rank, bk = bt.shape
+    if a.dtype != torch.bfloat16 or bt.dtype != torch.bfloat16 or bk != k:
+        raise ValueError("rank_product takes bf16 a [rows, K] and bt [E, R, K]")
+    _check(offsets, (experts + 1,), torch.int32, "offsets")
+    device = _on_gpu(a, bt, offsets)
+    out = torch.empty((rows, rank), dtype=torch.bfloat16, device=device)
+    _timed("rank_product", device, 0, 2 * rows * k + 2 * rows * rank, "mi355x_rank_product",
+           _ptr(a), rows, k, _ptr(bt), rank, _ptr(offsets), experts, _ptr(out), _stream(device))
+    return out
+
+
 def _gemm_lora(a, a_scale, w, w_scale, offsets, transposed_scale, interleave, z, b):
     rows, k = a.shape
     experts, n, wk = w.shape

@@ -80,6 +80,14 @@ def _per_expert(rows: torch.Tensor, factors: torch.Tensor, segments, out_cols: i
     return out
 
 
+def _row_rank(rows: torch.Tensor, factors_t: torch.Tensor, offsets, segments) -> torch.Tensor:
+    """``rows[r] @ factors_t[e]^T`` for each expert's rows, bf16 ``[rows, R]``:
+    the thin product kernel for padded ranks up to 64, else per-expert GEMMs."""
+    if factors_t.shape[1] <= 64:
+        return kernels.rank_product(rows, factors_t, offsets)
+    return _per_expert(rows, factors_t, segments, factors_t.shape[1], transpose=True)
+
+
 def _factor_grad(left: torch.Tensor, right: torch.Tensor, segments, shape) -> torch.Tensor:
     """``sum over each expert's rows of left_j right_j^T`` -> fp32 ``[E, *shape]``:
     ``left[s:t]^T @ right[s:t]`` from bf16 operands with fp32 sums and output."""
@@ -152,11 +160,13 @@ class _ExpertLoRA(torch.autograd.Function):
             h13 = kernels.gemm(xq, xs, w13_data, w13_scale, offsets, interleave=True,
                                lora=(_padded(z13, r13), _padded(b13s, r13)))
             aq, as_, act = kernels.swiglu_quantize(h13, limit, activation=True)
-            # Down projection: z2 = a @ A2^T per routed row.
-            z2 = _per_expert(act, a2b, segments, rank2, transpose=True)
+            # Down projection: z2 = a @ A2^T per routed row (the thin product
+            # streams a once; rank padded to 16).
+            z2p = _row_rank(act, _padded(a2b.transpose(1, 2), r2).transpose(1, 2).contiguous(),
+                            offsets, segments)
             del act
-            y = kernels.gemm(aq, as_, w2_data, w2_scale, offsets,
-                             lora=(_padded(z2, r2), _padded(b2b, r2)))
+            z2 = z2p[:, :rank2]
+            y = kernels.gemm(aq, as_, w2_data, w2_scale, offsets, lora=(z2p, _padded(b2b, r2)))
             output = kernels.combine(y, slots, weights, base)
             aux, probability_sum, _, _ = kernels.router_stats(logits, ids, top_k, mode,
                                                               opts["lengths"])
@@ -204,12 +214,14 @@ class _ExpertLoRA(torch.autograd.Function):
                 r, h13, weights.reshape(-1), order, limit)
             del r
             # Input gradient: dx_j = dh_j @ W13[e] + (dh_j @ (s B13[e])) @ A13[e].
-            u13 = _per_expert(dh, b13b, segments, rank13, transpose=False)
             r13 = _rank16(rank13)
+            u13p = _row_rank(dh, _padded(b13b, r13).transpose(1, 2).contiguous(), offsets,
+                             segments)
+            u13 = u13p[:, :rank13]
             dhq, dhs = kernels.quantize_rows(dh, gate_up=True)
             w13_t = provider.transposed_data(ctx.w13)
             dx = kernels.gemm(dhq, dhs, w13_t, w13_scale, offsets, transposed_scale=True,
-                              lora=(_padded(u13, r13), _padded(a13b.transpose(1, 2), r13)))
+                              lora=(u13p, _padded(a13b.transpose(1, 2), r13)))
             del dhq, dhs
             grad_hidden = kernels.unpermute_sum(dx, slots)
             del dx

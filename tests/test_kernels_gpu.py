@@ -424,3 +424,24 @@ def test_gemm_swiglu_fused_matches_separate_pass(device, limit, inter):
     q_ref, s_ref = K.swiglu_quantize(h, limit)
     assert torch.equal(_bytes(act), _bytes(q_ref))
     assert torch.equal(act_s, s_ref)
+
+
+@pytest.mark.parametrize("counts,k,rank", [
+    ([0, 37, 5, 0, 150, 16], 512, 16),   # empty experts, blocks spanning boundaries
+    ([300, 1, 200], 1536, 32),
+    ([64], 96, 48),
+])
+def test_rank_product_matches_fp32(device, counts, k, rank):
+    g = torch.Generator().manual_seed(sum(counts) + k)
+    offsets = _ragged(counts)
+    rows, experts = int(offsets[-1]), len(counts)
+    a = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+    bt = (torch.randn(experts, rank, k, generator=g) * 0.05).to(torch.bfloat16)
+    out = K.rank_product(a.to(device), bt.to(device), offsets.to(device)).cpu()
+    want = torch.zeros(rows, rank)
+    for e in range(experts):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        want[lo:hi] = a[lo:hi].float() @ bt[e].float().t()
+    # fp32 sums of exact bf16 products, one bf16 rounding of the result
+    assert max_rel(out.float(), want) < 1e-2
+    assert frob_rel(out.float(), want) < 4e-3
