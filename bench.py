@@ -43,7 +43,66 @@ CONFIGS = {
     "mixtral_8x7b_lora": dict(tokens=8192, hidden=4096, inter=14336, experts=8, top_k=2,
                               lora_rank=16),
     "config1": dict(tokens=256, hidden=512, inter=1024, experts=8, top_k=2),
+    # The single grouped GEMM (E=8, K=4096, N=2048, M_e ~ U{256..4096} step
+    # 128, seeded): one step is one launch on resident e4m3 operands.
+    "grouped_gemm_c2": dict(gemm_only=True, experts=8, k=4096, n=2048, seed=2),
 }
+
+
+def make_gemm_inputs(cfg, device):
+    """C2's operands, quantized once (1x128 activation and 128x128 weight
+    scales): ``(xq, xs, wq, ws, offsets, rows)``."""
+    import numpy as np
+    from mlops_amd import kernels as K
+
+    rng = np.random.default_rng(cfg["seed"])
+    counts = (rng.integers(2, 33, size=cfg["experts"]) * 128).tolist()
+    offsets = torch.tensor([0] + list(np.cumsum(counts)), dtype=torch.int32, device=device)
+    rows = int(sum(counts))
+    g = torch.Generator(device=device).manual_seed(cfg["seed"])
+    x = torch.randn(rows, cfg["k"], generator=g, device=device).to(torch.bfloat16)
+    w = torch.randn(cfg["experts"], cfg["n"], cfg["k"], generator=g, device=device) * 0.02
+    xq, xs = K.quantize_rows(x)
+    wq, ws = K.quantize_weight_blocks(w.to(torch.bfloat16))
+    return xq, xs, wq, ws, offsets, rows
+
+
+def gemm_main(args, cfg):
+    """One grouped GEMM per step; prints the JSON line for C2."""
+    from mlops_amd import kernels as K
+
+    device = torch.device("cuda", 0)
+    xq, xs, wq, ws, offsets, rows = make_gemm_inputs(cfg, device)
+    step = lambda: K.gemm(xq, xs, wq, ws, offsets)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = K.LaunchTimer()
+    K.set_launch_timer(timer)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    K.set_launch_timer(None)
+    gemm = timer.summary()["gemm_fp8_block"]
+    flops = 2 * rows * cfg["n"] * cfg["k"]
+    achieved = gemm["flops"] / (gemm["ms_total"] * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "block-FP8 grouped GEMM TFLOP/s (% MFMA peak), 1 GPU",
+        "value": flops * args.steps / elapsed / 1e12,
+        "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8_e4m3 (block-scaled), fp32 accumulate, bf16 out",
+        "data": "synthetic (N(0,1) activations, N(0,0.02) weights)",
+        "config": {"workload": "grouped_gemm_c2 single grouped GEMM", "experts": cfg["experts"],
+                   "k": cfg["k"], "n": cfg["n"], "rows": rows},
+        "roofline": {"kernel": "mi355x_gemm_fp8_block", "bound": "mfma", "achieved": achieved,
+                     "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / FP8_PEAK_TFLOPS, "traffic": None},
+    }))
 
 
 def make_inputs(cfg, device, seed=0):
@@ -193,6 +252,9 @@ def main():
     from mlops_amd import kernels
 
     cfg = CONFIGS[args.config]
+    if cfg.get("gemm_only"):
+        gemm_main(args, cfg)
+        return
     device = torch.device("cuda", 0)
     lora = "lora_rank" in cfg
     if lora:
