@@ -239,6 +239,9 @@ def main():
     parser.add_argument("--config", default="qwen3_30b_a3b", choices=sorted(CONFIGS))
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-sample-tokens", type=int, default=128)
+    parser.add_argument("--implementation", default=None,
+                        help="force a registered moe implementation (default: the registry's "
+                             "choice, mi355x.moe.block_fp8), e.g. mi355x.moe.composed")
     parser.add_argument("--calibration-copy-mib", type=int, default=0,
                         help="after the timed steps, run one device copy of this many MiB "
                              "(the known-size kernel that calibrates rocprofv3 byte counters)")
@@ -268,6 +271,10 @@ def main():
         for t in (wr, w13, w2):
             t.requires_grad_(True)
         step = lambda: gpu_step(mlops_amd.moe, inputs, cfg)
+    if args.implementation is not None:
+        from mlops_amd.dispatch import set_implementations
+
+        set_implementations({"moe": args.implementation})
 
     for _ in range(args.warmup):
         step()
@@ -323,6 +330,7 @@ def main():
         "config": {
             "workload": f"{args.config} MoE layer fwd+bwd, block-FP8",
             **cfg,
+            **({"implementation": args.implementation} if args.implementation else {}),
             "routing_mode": "topk_then_softmax",
             "weights": ("frozen block-FP8 base (128x128 blocks), rank-16 bf16 LoRA factors, "
                         "logits +2 on expert 0" if lora else

@@ -170,9 +170,9 @@ int mi355x_unpermute_sum(const void* dx, const int32_t* slots, int tokens, int t
 /* Routed SwiGLU backward over sorted rows: from r = dy @ W2 [A,I] (bf16),
  * h [A,2I] interleaved and the route score of each sorted row
  * (weights[order[row]]): dscore = <r, act> (fp32), dh = dSwiGLU(score * r)
- * interleaved (bf16), a' = score * act (bf16). Replaces
- * routed_swiglu_rows_backward (kernels/quack_moe/swiglu_rows.py:101-146,
- * :278-318). */
+ * interleaved (bf16), a' = score * act (bf16). dh may be h itself (written
+ * in place). Replaces routed_swiglu_rows_backward
+ * (kernels/quack_moe/swiglu_rows.py:101-146, :278-318). */
 int mi355x_routed_swiglu_bwd(const void* r, const void* h, const float* weights,
                              const int32_t* order, int rows, int width, float limit, void* dh,
                              void* a_prime, float* dscore, void* stream);

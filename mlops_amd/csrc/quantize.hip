@@ -389,10 +389,13 @@ __global__ void __launch_bounds__(256) quantize_transpose_kernel(
 
 // ---------------------------------------------------------------------------
 // Routed SwiGLU backward, one wave per sorted row.
+// h and dh may be the same buffer (dh written in place over h): each lane
+// loads its h values before it stores their gradients, and no other lane
+// reads them, so they carry no __restrict__.
 __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
-    const uint16_t* __restrict__ rmat, const uint16_t* __restrict__ h,
+    const uint16_t* __restrict__ rmat, const uint16_t* h,
     const float* __restrict__ weights, const int32_t* __restrict__ order, int rows, int width,
-    float limit, uint16_t* __restrict__ dh, uint16_t* __restrict__ a_prime,
+    float limit, uint16_t* dh, uint16_t* __restrict__ a_prime,
     float* __restrict__ dscore) {
   const int wave = threadIdx.x >> 6, lane = lane_id();
   const int row = blockIdx.x * 4 + wave;
@@ -400,49 +403,56 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
   const float score = weights[order[row]];
   const uint16_t* hr = h + (size_t)row * 2 * width;
   const uint16_t* rr = rmat + (size_t)row * width;
-  float dot = 0.0f;
+  // The score dot in swiglu_bwd_quantize_kernel's order: a lane's 8
+  // products, summed over each 128-column block's 16 lanes, and the block
+  // sums added in block order, so both kernels give the same dscore.
+  float dsum = 0.0f;
   for (int base = 0; base < width; base += 512) {
     const int j = base + lane * 8;
-    if (j >= width) continue;
-    float a[8], b[8], r[8];
-    load_bf16x8(hr + 2 * j, a);
-    load_bf16x8(hr + 2 * j + 8, b);
-    load_bf16x8(rr + j, r);
-    float dg[8], du[8], ap[8];
+    float dot = 0.0f;
+    if (j < width) {
+      float a[8], b[8], r[8];
+      load_bf16x8(hr + 2 * j, a);
+      load_bf16x8(hr + 2 * j + 8, b);
+      load_bf16x8(rr + j, r);
+      float dg[8], du[8], ap[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float rg = i < 4 ? a[2 * i] : b[2 * (i - 4)];
-      const float ru = i < 4 ? a[2 * i + 1] : b[2 * (i - 4) + 1];
-      float gv = rg, uv = ru;
-      clamp_gate_up(gv, uv, limit);
-      const float sig = sigmoid_f(gv);
-      const float silu = gv * sig;
-      const float act = silu * uv;
-      dot += r[i] * act;
-      const float gg = r[i] * score;
-      float dgate = gg * uv * (sig + silu * (1.0f - sig));
-      float dup = gg * silu;
-      if (limit > 0.0f) {
-        dgate = rg <= limit ? dgate : 0.0f;
-        dup = (ru >= -limit && ru <= limit) ? dup : 0.0f;
+      for (int i = 0; i < 8; ++i) {
+        const float rg = i < 4 ? a[2 * i] : b[2 * (i - 4)];
+        const float ru = i < 4 ? a[2 * i + 1] : b[2 * (i - 4) + 1];
+        float gv = rg, uv = ru;
+        clamp_gate_up(gv, uv, limit);
+        const float sig = sigmoid_f(gv);
+        const float silu = gv * sig;
+        const float act = silu * uv;
+        dot += r[i] * act;
+        const float gg = r[i] * score;
+        float dgate = gg * uv * (sig + silu * (1.0f - sig));
+        float dup = gg * silu;
+        if (limit > 0.0f) {
+          dgate = rg <= limit ? dgate : 0.0f;
+          dup = (ru >= -limit && ru <= limit) ? dup : 0.0f;
+        }
+        dg[i] = dgate;
+        du[i] = dup;
+        ap[i] = act * score;
       }
-      dg[i] = dgate;
-      du[i] = dup;
-      ap[i] = act * score;
+      uint4 o0, o1, o2;
+      o0.x = pack_bf16x2(dg[0], du[0]); o0.y = pack_bf16x2(dg[1], du[1]);
+      o0.z = pack_bf16x2(dg[2], du[2]); o0.w = pack_bf16x2(dg[3], du[3]);
+      o1.x = pack_bf16x2(dg[4], du[4]); o1.y = pack_bf16x2(dg[5], du[5]);
+      o1.z = pack_bf16x2(dg[6], du[6]); o1.w = pack_bf16x2(dg[7], du[7]);
+      o2.x = pack_bf16x2(ap[0], ap[1]); o2.y = pack_bf16x2(ap[2], ap[3]);
+      o2.z = pack_bf16x2(ap[4], ap[5]); o2.w = pack_bf16x2(ap[6], ap[7]);
+      *(uint4*)(dh + (size_t)row * 2 * width + 2 * j) = o0;
+      *(uint4*)(dh + (size_t)row * 2 * width + 2 * j + 8) = o1;
+      *(uint4*)(a_prime + (size_t)row * width + j) = o2;
     }
-    uint4 o0, o1, o2;
-    o0.x = pack_bf16x2(dg[0], du[0]); o0.y = pack_bf16x2(dg[1], du[1]);
-    o0.z = pack_bf16x2(dg[2], du[2]); o0.w = pack_bf16x2(dg[3], du[3]);
-    o1.x = pack_bf16x2(dg[4], du[4]); o1.y = pack_bf16x2(dg[5], du[5]);
-    o1.z = pack_bf16x2(dg[6], du[6]); o1.w = pack_bf16x2(dg[7], du[7]);
-    o2.x = pack_bf16x2(ap[0], ap[1]); o2.y = pack_bf16x2(ap[2], ap[3]);
-    o2.z = pack_bf16x2(ap[4], ap[5]); o2.w = pack_bf16x2(ap[6], ap[7]);
-    *(uint4*)(dh + (size_t)row * 2 * width + 2 * j) = o0;
-    *(uint4*)(dh + (size_t)row * 2 * width + 2 * j + 8) = o1;
-    *(uint4*)(a_prime + (size_t)row * width + j) = o2;
+    dot = group_sum<16>(dot);
+    const int blocks = min(4, (width - base + 127) / 128);  // 128-column blocks here
+    for (int q = 0; q < blocks; ++q) dsum += __shfl(dot, 16 * q, 64);
   }
-  dot = wave_sum(dot);
-  if (lane == 0) dscore[row] = dot;
+  if (lane == 0) dscore[row] = dsum;
 }
 
 

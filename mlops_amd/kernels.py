@@ -371,12 +371,17 @@ def unpermute_sum(dx, slots):
     return out
 
 
-def routed_swiglu_backward(r, h, weights, order, limit=None):
-    """``(dh [A,2I] interleaved, a' [A,I], dscore fp32 [A])``."""
+def routed_swiglu_backward(r, h, weights, order, limit=None, *, dh_out=None):
+    """``(dh [A,2I] interleaved, a' [A,I], dscore fp32 [A])``. ``dh`` is written
+    into ``dh_out`` when given, which may be ``h`` itself (in place)."""
     rows, width = r.shape
     _check(h, (rows, 2 * width), torch.bfloat16, "h")
-    device = _on_gpu(r, h, weights, order)
-    dh = torch.empty_like(h)
+    device = _on_gpu(r, h, weights, order, dh_out)
+    if dh_out is not None:
+        _check(dh_out, (rows, 2 * width), torch.bfloat16, "dh_out")
+        if not dh_out.is_contiguous():
+            raise ValueError("dh_out must be contiguous")
+    dh = torch.empty_like(h) if dh_out is None else dh_out
     a_prime = torch.empty_like(r)
     dscore = torch.empty(rows, dtype=torch.float32, device=device)
     _native.call("mi355x_routed_swiglu_bwd", _ptr(r), _ptr(h), _ptr(weights), _ptr(order), rows,

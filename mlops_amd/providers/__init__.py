@@ -8,7 +8,7 @@ from __future__ import annotations
 
 from importlib import import_module
 
-_CATALOG = ("mlops_amd.providers.mi355x.moe",)
+_CATALOG = ("mlops_amd.providers.mi355x.moe", "mlops_amd.providers.mi355x.moe_composed")
 _REGISTERED = False
 
 

@@ -36,9 +36,23 @@ def _args(tokens=4, hidden=256, experts=8, inter=128, device="cpu", dtype=torch.
 
 def test_catalog_contains_the_provider():
     table = implementation_registry()["moe"]
-    assert list(table) == ["mi355x.moe.block_fp8"]
+    assert sorted(table) == ["mi355x.moe.block_fp8", "mi355x.moe.composed"]
     impl = table["mi355x.moe.block_fp8"]
     assert impl.priority > 110 and impl.deterministic and impl.forward and impl.backward
+    # The two-region form is semantic-only (no explicit forward/backward, as
+    # the reference's composed implementations) and ranks below the fused op.
+    composed = table["mi355x.moe.composed"]
+    assert composed.deterministic and composed.forward is None and composed.backward is None
+    assert 110 < composed.priority < impl.priority
+
+
+def test_composed_refuses_the_explicit_surface():
+    from mlops_amd.providers.mi355x import moe_composed
+
+    result = moe_composed._supports(*_args(), surface="explicit", top_k=2,
+                                    routing_mode="topk_then_softmax",
+                                    compute_precision="fp8_block")
+    assert not result and "semantic-only" in result.reason
 
 
 def test_duplicate_id_and_pairing_rules():
@@ -189,6 +203,40 @@ def test_flop_formulas_on_fake_tensors():
     assert expected == (2 * tokens * hidden * experts + 3 * tokens * experts
                         + 2 * a * hidden * 2 * inter + 5 * a * inter + 2 * a * inter * hidden
                         + 2 * a * hidden)
+
+
+def test_composed_flop_formulas_sum_to_the_layer():
+    """prepare + finish price the same logical FLOPs as the fused operator
+    (reference logical_costs.py:418-494), forward and backward."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    import mlops_amd.providers.mi355x.moe_composed  # noqa: F401  (registers the ops)
+
+    tokens, hidden, inter, experts, k = 64, 256, 128, 4, 2
+    a = tokens * k
+    ops = torch.ops.mlops_mi355x
+    with FakeTensorMode():
+        x = torch.empty(tokens, hidden, dtype=torch.bfloat16)
+        wr = torch.empty(experts, hidden)
+        w13 = torch.empty(experts, 2 * inter, hidden, dtype=torch.float8_e4m3fn)
+        w2 = torch.empty(experts, hidden, inter, dtype=torch.float8_e4m3fn)
+        s13, s2 = torch.empty(experts, 2, 2), torch.empty(experts, 2, 1)
+        with FlopCounterMode(display=False) as forward:
+            outs = ops.moe_mi355x_prepare_fwd(x, wr, w13, torch.empty(0), k,
+                                              "topk_then_softmax", 1, 1, 1.0, [tokens],
+                                              "float32", None, [s13])
+            (aux, counts, psum, logits, weights, ids, order, offsets, slots, h13) = outs
+            out = ops.moe_mi355x_finish_fwd(h13, w2, weights, order, offsets, slots, x, k, None,
+                                            None, [s2])
+        with FlopCounterMode(display=False) as backward:
+            ops.moe_mi355x_finish_bwd(out, h13, w2, weights, order, offsets, slots, k, None,
+                                      None, [s2], True)
+            ops.moe_mi355x_prepare_bwd(aux, psum, weights, h13, x, wr, w13, logits, weights, ids,
+                                       order, offsets, slots, k, "topk_then_softmax", [tokens],
+                                       None, [s13], True, True)
+    assert tuple(h13.shape) == (a, 2 * inter) and tuple(out.shape) == (tokens, hidden)
+    assert forward.get_total_flops() == moe_flops(x, wr, w13, w2, k, forward=True)
+    assert backward.get_total_flops() == moe_flops(x, wr, w13, w2, k, forward=False)
 
 
 def test_op_namespace_is_separate():
