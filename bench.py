@@ -42,6 +42,10 @@ CONFIGS = {
     # hidden rows only.
     "mixtral_8x7b_lora": dict(tokens=8192, hidden=4096, inter=14336, experts=8, top_k=2,
                               lora_rank=16),
+    # C3's layer at compute_precision="fp8_current" (per-row e4m3 scaling, the
+    # reference's other FP8 format): the same per-call bf16 masters.
+    "qwen3_30b_a3b_fp8_current": dict(tokens=16384, hidden=2048, inter=768, experts=128,
+                                      top_k=8, precision="fp8_current"),
     "config1": dict(tokens=256, hidden=512, inter=1024, experts=8, top_k=2),
     # The single grouped GEMM (E=8, K=4096, N=2048, M_e ~ U{256..4096} step
     # 128, seeded): one step is one launch on resident e4m3 operands.
@@ -159,7 +163,8 @@ def gpu_step(moe, args, cfg):
     for t in (wr, w13, w2):
         t.grad = None
     out, aux, counts, psum = moe(x, res, wr, w13, w2, top_k=cfg["top_k"],
-                                 routing_mode="topk_then_softmax", compute_precision="fp8_block")
+                                 routing_mode="topk_then_softmax",
+                                 compute_precision=cfg.get("precision", "fp8_block"))
     torch.autograd.backward([out, aux], [dy, torch.full_like(aux, 0.01)])
 
 
@@ -298,7 +303,8 @@ def main():
     # gradients (the rank-r LoRA products add under 1%, not counted).
     layer_flops = (12 if lora else 18) * a * cfg["hidden"] * cfg["inter"]
 
-    gemm = summary.get("gemm_fp8_block", {})
+    gemm_kernel = "gemm_fp8_rowwise" if cfg.get("precision") == "fp8_current" else "gemm_fp8_block"
+    gemm = summary.get(gemm_kernel, {})
     achieved = gemm["flops"] / (gemm["ms_total"] * 1e-3) / 1e12 if gemm else None
     per_kernel = {}
     for name, entry in summary.items():
@@ -334,18 +340,20 @@ def main():
             "routing_mode": "topk_then_softmax",
             "weights": ("frozen block-FP8 base (128x128 blocks), rank-16 bf16 LoRA factors, "
                         "logits +2 on expert 0" if lora else
+                        "bf16 masters quantized per call (one descale per row, both "
+                        "orientations)" if cfg.get("precision") == "fp8_current" else
                         "bf16 masters quantized per call (128x128 blocks)"),
         },
         "layer_tflops": layer_flops * args.steps / elapsed / 1e12,
         "gemm_tflops_all": all_gemm_flops / (all_gemm_ms * 1e-3) / 1e12 if all_gemm_ms else None,
         "roofline": {
-            "kernel": "mi355x_gemm_fp8_block (grouped fwd/dgrad GEMM)",
+            "kernel": f"mi355x_{gemm_kernel} (grouped fwd/dgrad GEMM)",
             "bound": "mfma",
             "achieved": achieved,
             "peak": FP8_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / FP8_PEAK_TFLOPS if achieved else None,
-            "traffic": load_traffic("gemm_fp8_block"),
+            "traffic": load_traffic(gemm_kernel),
         },
         "kernels": per_kernel,
     }

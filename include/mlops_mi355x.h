@@ -236,6 +236,58 @@ int mi355x_gemm_fp8_block_lora(const uint8_t* a, const float* a_scale, int rows,
                                const int32_t* offsets, int interleave, const void* lora_z,
                                const void* lora_b, int lora_rank, void* out, void* stream);
 
+/* ---- "fp8_current": one e4m3 descale per operand row (current scaling) ----
+ * Row-scaled grouped GEMM: out[r, n] = bf16((acc * a_scale[r]) * w_scale[e, n])
+ * with acc = sum_k e4m3(a[r, k]) e4m3(w[e][n, k]) in fp32, for the rows r of
+ * expert e. a: e4m3 [rows, K], a_scale fp32 [rows]; w: e4m3 [E, N, K]
+ * (the weight's rows, or its transposed copy for an input gradient), w_scale
+ * fp32 [E, N]. N a multiple of 256, K of 128. Replaces the scale-aware
+ * epilogue GEMMs of the fp8_current path (kernels/quack_moe/fp8.py;
+ * providers/sonicmoe/fp8.py:226-247 _project_down, :330-357
+ * input_gradient_rows, the products of :205-224 up_projection and :271-309
+ * down_backward_activations). */
+int mi355x_gemm_fp8_rowwise(const uint8_t* a, const float* a_scale, int rows, const uint8_t* w,
+                            const float* w_scale, int experts, int n, int k,
+                            const int32_t* offsets, void* out, void* stream);
+
+/* Per-row e4m3 quantizer: q[r] = e4m3(clip(x[src] / s, +-448)), scales[r] =
+ * s = max(amax(x[src]) * (1/448), 1e-12), src = gather[r] / gather_div (a
+ * routed row's token) or r. x bf16 rows of the given pitch. Replaces
+ * quantize_rows_fp8 (kernels/quack_moe/quantize_rows.py:140-207). */
+int mi355x_quantize_rows_current_fp8(const void* x, int rows, int width, int64_t pitch,
+                                     const int32_t* gather, int gather_div, uint8_t* q,
+                                     float* scales, void* stream);
+
+/* The per-row quantizer above for the routed copies of token rows: row t of
+ * x [tokens, width] (bf16) quantized once and stored, with its scale, at
+ * each of its sorted slots slots[t, 0..top_k). Equals
+ * mi355x_quantize_rows_current_fp8 over the gathered rows (gather = order,
+ * gather_div = top_k). Replaces quantize_rows_fp8(..., gather=)
+ * (kernels/quack_moe/quantize_rows.py:140-207) as the fp8_current path calls
+ * it (providers/sonicmoe/fp8.py:214, :295). */
+int mi355x_permute_quantize_current_fp8(const void* x, int tokens, int width, int top_k,
+                                        const int32_t* slots, uint8_t* q, float* scales,
+                                        void* stream);
+
+/* SwiGLU of interleaved h [rows, 2I] (gate from above and up on both sides
+ * clamped at limit when limit > 0), quantized per row as above: q [rows, I],
+ * scales [rows]. Replaces swiglu_quantize_rows_fp8
+ * (kernels/quack_moe/swiglu_rows.py:246-276). */
+int mi355x_swiglu_quantize_rows_current_fp8(const void* h, int rows, int width, float limit,
+                                            uint8_t* q, float* scales, void* stream);
+
+/* Both orientations of expert weights w [E, out, in] (bf16, or fp32 when
+ * is_fp32): q [E, out, in] with scales [E, out] (per row), qt [E, in, out]
+ * with scales_t [E, in] (per column of w), each as the per-row quantizer
+ * above; with interleave the out rows of both are stored gate/up-adjacent
+ * (stored 2j = gate row j, 2j + 1 = up row j). in a multiple of 8, out of 16.
+ * Replaces quantize_weights_fp8 (kernels/quack_moe/quantize_transpose.py
+ * :316-339) behind QuackFP8Weight.quantize
+ * (expert_parallel/quack/parameters/fp8.py:36-54, 111-121). */
+int mi355x_quantize_weights_current_fp8(const void* w, int is_fp32, int experts, int out, int in,
+                                        int interleave, uint8_t* q, float* scales, uint8_t* qt,
+                                        float* scales_t, void* stream);
+
 /* Thin grouped product of expert LoRA: out[r, 0:R] = sum_k a[r, k] *
  * bt[e][0:R, k] for the rows r of expert e (offsets[E+1]), a bf16 [rows, K],
  * bt bf16 [E, R, K], out bf16 [rows, R], fp32 sums; K a multiple of 32, R a

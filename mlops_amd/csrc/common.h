@@ -126,6 +126,35 @@ __device__ __forceinline__ float sigmoid_f(float g) {
 }
 __device__ __forceinline__ float silu_f(float g) { return g * sigmoid_f(g); }
 
+// Eight bf16 values from one 16-byte load (or from its bits), as fp32.
+__device__ __forceinline__ void load_bf16x8(const uint16_t* p, float* v) {
+  uint4 r = *(const uint4*)p;
+  uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16_to_f32(w4[i] & 0xffff);
+    v[2 * i + 1] = bf16_to_f32(w4[i] >> 16);
+  }
+}
+
+__device__ __forceinline__ void unpack_bf16x8(uint4 r, float* v) {
+  const uint32_t w4[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16_to_f32(w4[i] & 0xffff);
+    v[2 * i + 1] = bf16_to_f32(w4[i] >> 16);
+  }
+}
+
+__device__ __forceinline__ uint2 quant8(const float* v, float s) {
+  const float inv = 1.0f / s;
+  uint32_t lo = f32x4_to_e4m3(quant_div_inv(v[0], s, inv), quant_div_inv(v[1], s, inv),
+                              quant_div_inv(v[2], s, inv), quant_div_inv(v[3], s, inv));
+  uint32_t hi = f32x4_to_e4m3(quant_div_inv(v[4], s, inv), quant_div_inv(v[5], s, inv),
+                              quant_div_inv(v[6], s, inv), quant_div_inv(v[7], s, inv));
+  return make_uint2(lo, hi);
+}
+
 // ---------------------------------------------------------------- waves
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -106,6 +106,11 @@ __device__ __forceinline__ v4f mfma(v8i a, v8i b) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, zero, 0, 0, 0, 0, 0, 0);
 }
 
+// The same MFMA accumulating into c (row-scaled operands: no per-block fold).
+__device__ __forceinline__ v4f mfma_acc(v8i a, v8i b, v4f c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
 // Exclusive prefix of ceil(rows_e / tile) over experts -> prefix[0..E].
 __device__ inline void tile_prefix(const int32_t* __restrict__ offsets, int experts, int tile,
                                    int* prefix, int* tmp) {

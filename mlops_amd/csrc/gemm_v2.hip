@@ -50,7 +50,10 @@ __device__ __forceinline__ int weight_row(int tr, int nt, int interleave, int ha
 
 typedef short v4s __attribute__((ext_vector_type(4)));
 
-template <bool kAct, bool kAdd, bool kLora>
+// kRow: row-scaled operands (one descale per activation row, a_scale[rows],
+// and one per weight output row, w_scale[E, N]): the K loop accumulates in
+// the MFMA itself and the epilogue applies (acc * a_scale) * w_scale once.
+template <bool kAct, bool kAdd, bool kLora, bool kRow = false>
 __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ a_scale, int rows,
     const uint8_t* __restrict__ w, const float* __restrict__ w_scale, int w_scale_t, int experts,
@@ -91,6 +94,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
                            16 * ((lane & 7) ^ swz(tr));
       dma16(bbase, off, base + A_BYTES + (wave * B_LOADS + i) * 1024);
     }
+    if constexpr (kRow) return;  // no per-step scales
     const float* sbase = a_scale + (size_t)kb * rows;
     if (lane < 32) {
       const uint32_t off = 4u * (uint32_t)min(t.row0 + wave * 32 + lane, rows - 1);
@@ -178,6 +182,22 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       const uint8_t* base = smem + stage * STAGE_BYTES;
       const uint8_t* ta = base;
       const uint8_t* tb = base + A_BYTES;
+      if constexpr (kRow) {
+        v8i bcur = frag(tb, wn * 128 + (lane & 15), lane);
+        v8i af[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) af[i] = frag(ta, wm * 64 + i * 16 + (lane & 15), lane);
+#pragma unroll
+        for (int jb = 0; jb < 8; ++jb) {
+          v8i bnext = bcur;
+          if (jb < 7) bnext = frag(tb, wn * 128 + (jb + 1) * 16 + (lane & 15), lane);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i][jb] = mfma_acc(af[i], bcur, acc[i][jb]);
+          bcur = bnext;
+        }
+        stage ^= 1;
+        continue;
+      }
       const float* sa = (const float*)(base + A_BYTES + B_BYTES);
       const float2 sbw = *(const float2*)(base + A_BYTES + B_BYTES + SA_BYTES + wave * 8);
       const float sb_lo = sbw.x, sb_hi = sbw.y;
@@ -234,6 +254,14 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     uint32_t elane = lane;
     asm volatile("" : "+v"(elane));
     const uint32_t lane_col = (elane & 15) * 8;
+    // kRow: the lane's 8 output columns' weight descales.
+    float wsc[8];
+    if constexpr (kRow) {
+      const float* wsb = w_scale + (size_t)ct.e * N + ct.nt * BN + wn * 128 + lane_col;
+      const float4 w0 = *(const float4*)wsb, w1 = *(const float4*)(wsb + 4);
+      wsc[0] = w0.x; wsc[1] = w0.y; wsc[2] = w0.z; wsc[3] = w0.w;
+      wsc[4] = w1.x; wsc[5] = w1.y; wsc[6] = w1.z; wsc[7] = w1.w;
+    }
     // SwiGLU fused into the up projection (gate/up mode with act_q): the
     // activation of the stored bf16 gate/up pairs, quantized 1x128 as
     // swiglu_quantize_kernel does. A lane holds 4 of a row's 64 act columns
@@ -279,6 +307,11 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
           }
           if (wm * 64 + lrow < ct.nvalid) {
             const uint32_t off = (uint32_t)lrow * (uint32_t)N + lane_col;
+            if constexpr (kRow) {
+              const float xs = a_scale[ct.row0 + wm * 64 + lrow];
+#pragma unroll
+              for (int m = 0; m < 8; ++m) v[m] = (v[m] * xs) * wsc[m];
+            }
             if (kAdd) {
               const uint4 c = cadd[ii][r];
               uint32_t w4[4] = {c.x, c.y, c.z, c.w};
@@ -381,6 +414,23 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
     addend != nullptr ? launch(grouped_gemm_v2_kernel<false, true, false>)
                       : launch(grouped_gemm_v2_kernel<false, false, false>);
   }
+  MI355X_LAUNCH_CHECK();
+  return 0;
+}
+
+// Row-scaled form (see kRow): a_scale [rows], w_scale [E, N]; returns 1 if
+// the shape is not this kernel's (N % 256 != 0).
+int mi355x_gemm_v2_rowwise_launch(const uint8_t* a, const float* a_scale, int rows,
+                                  const uint8_t* w, const float* w_scale, int experts, int n,
+                                  int k, const int32_t* offsets, void* out, void* stream) {
+  if (n % BN != 0 || experts > kMaxExperts) return 1;
+  const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
+  const int grid = upper < cu_count() ? upper : cu_count();
+  hipLaunchKernelGGL((grouped_gemm_v2_kernel<false, false, false, true>), dim3(grid),
+                     dim3(kThreads), 0, (hipStream_t)stream, a, a_scale, rows, w, w_scale, 0,
+                     experts, n, k, offsets, 0, (const uint16_t*)nullptr, (uint16_t*)out,
+                     (uint8_t*)nullptr, (float*)nullptr, 0.0f, (const uint16_t*)nullptr,
+                     (const uint16_t*)nullptr, 0);
   MI355X_LAUNCH_CHECK();
   return 0;
 }

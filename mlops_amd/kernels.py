@@ -513,6 +513,97 @@ def gemm_swiglu(a, a_scale, w, w_scale, offsets, *, limit=None, addend=None):
     return h, act, act_scales
 
 
+# ---------------------------------------------------------------- fp8_current
+def quantize_rows_current(x: torch.Tensor, *, gather=None, gather_div: int = 1):
+    """Per-row e4m3 ``(q [R, W], scales fp32 [R])`` of bf16 ``x`` rows, or of
+    the rows ``x[gather[r] // gather_div]`` when ``gather`` is given
+    (``mi355x_quantize_rows_current_fp8``)."""
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
+        raise ValueError("quantize_rows_current takes bf16 [rows, width] with unit column stride")
+    rows = x.shape[0] if gather is None else gather.numel()
+    width = x.shape[1]
+    if gather is not None and gather.dtype != torch.int32:
+        raise ValueError("gather must be int32")
+    device = _on_gpu(x, gather)
+    q = torch.empty((rows, width), dtype=FP8, device=device)
+    scales = torch.empty(rows, dtype=torch.float32, device=device)
+    _native.call("mi355x_quantize_rows_current_fp8", _ptr(x), rows, width, x.stride(0),
+                 _ptr(gather), int(gather_div), _ptr(q), _ptr(scales), _stream(device))
+    return q, scales
+
+
+def permute_quantize_current(x: torch.Tensor, slots: torch.Tensor):
+    """Per-row e4m3 of the routed copies of token rows: ``(q [T*k, W], scales
+    [T*k])`` with row ``slots[t, j]`` = token ``t`` quantized
+    (``mi355x_permute_quantize_current_fp8``)."""
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or not x.is_contiguous():
+        raise ValueError("permute_quantize_current takes contiguous bf16 [tokens, width]")
+    tokens, width = x.shape
+    if slots.ndim != 2 or slots.shape[0] != tokens or slots.dtype != torch.int32:
+        raise ValueError("slots must be int32 [tokens, top_k]")
+    top_k = slots.shape[1]
+    device = _on_gpu(x, slots)
+    q = torch.empty((tokens * top_k, width), dtype=FP8, device=device)
+    scales = torch.empty(tokens * top_k, dtype=torch.float32, device=device)
+    _native.call("mi355x_permute_quantize_current_fp8", _ptr(x), tokens, width, top_k,
+                 _ptr(slots), _ptr(q), _ptr(scales), _stream(device))
+    return q, scales
+
+
+def swiglu_quantize_rows_current(h: torch.Tensor, limit: float | None = None):
+    """SwiGLU of interleaved bf16 ``h [R, 2I]`` quantized per row:
+    ``(q [R, I], scales fp32 [R])`` (``mi355x_swiglu_quantize_rows_current_fp8``)."""
+    if h.dtype != torch.bfloat16 or h.ndim != 2 or not h.is_contiguous():
+        raise ValueError("swiglu_quantize_rows_current takes contiguous bf16 [rows, 2I]")
+    rows, width = h.shape[0], h.shape[1] // 2
+    device = _on_gpu(h)
+    q = torch.empty((rows, width), dtype=FP8, device=device)
+    scales = torch.empty(rows, dtype=torch.float32, device=device)
+    _native.call("mi355x_swiglu_quantize_rows_current_fp8", _ptr(h), rows, width, _limit(limit),
+                 _ptr(q), _ptr(scales), _stream(device))
+    return q, scales
+
+
+def quantize_weights_current(w: torch.Tensor, *, interleaved: bool = False):
+    """Both orientations of bf16/fp32 ``w [E, out, in]``, per-row scaled:
+    ``(data [E,out,in], transposed [E,in,out], scale [E,out], transposed_scale
+    [E,in])``, rows gate/up-adjacent when ``interleaved``
+    (``mi355x_quantize_weights_current_fp8``)."""
+    if w.ndim != 3 or w.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("quantize_weights_current takes bf16/fp32 [experts, out, in]")
+    w = w.contiguous()
+    device = _on_gpu(w)
+    experts, out, inner = w.shape
+    data = torch.empty(w.shape, dtype=FP8, device=device)
+    transposed = torch.empty((experts, inner, out), dtype=FP8, device=device)
+    scale = torch.empty((experts, out), dtype=torch.float32, device=device)
+    transposed_scale = torch.empty((experts, inner), dtype=torch.float32, device=device)
+    _native.call("mi355x_quantize_weights_current_fp8", _ptr(w), int(w.dtype == torch.float32),
+                 experts, out, inner, int(interleaved), _ptr(data), _ptr(scale),
+                 _ptr(transposed), _ptr(transposed_scale), _stream(device))
+    return data, transposed, scale, transposed_scale
+
+
+def gemm_rowwise(a, a_scale, w, w_scale, offsets):
+    """Row-scaled grouped e4m3 GEMM: bf16 ``out[r] = (a[r] @ w[e]^T) * a_scale[r]
+    * w_scale[e]`` per expert (``mi355x_gemm_fp8_rowwise``)."""
+    rows, k = a.shape
+    experts, n, wk = w.shape
+    if a.dtype != FP8 or w.dtype != FP8 or wk != k:
+        raise ValueError("gemm_rowwise takes e4m3 rows [A,K] and e4m3 weights [E,N,K]")
+    _check(a_scale, (rows,), torch.float32, "row scales")
+    _check(w_scale, (experts, n), torch.float32, "weight row scales")
+    _check(offsets, (experts + 1,), torch.int32, "offsets")
+    device = _on_gpu(a, a_scale, w, w_scale, offsets)
+    out = torch.empty((rows, n), dtype=torch.bfloat16, device=device)
+    _timed(
+        "gemm_fp8_rowwise", device, 2 * rows * n * k, rows * k + experts * n * k + 2 * rows * n,
+        "mi355x_gemm_fp8_rowwise", _ptr(a), _ptr(a_scale), rows, _ptr(w), _ptr(w_scale),
+        experts, n, k, _ptr(offsets), _ptr(out), _stream(device),
+    )
+    return out
+
+
 def wgrad(p, p_scale, q, q_scale, offsets, *, out_dtype=torch.bfloat16, rows=None):
     """``out[e] = sum over expert e's rows of p[:, row] q[:, row]^T`` -> ``[E, M, N]``.
     ``rows`` (the routed row count, for the launch timer's FLOP count) is optional."""

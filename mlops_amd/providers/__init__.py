@@ -8,7 +8,11 @@ from __future__ import annotations
 
 from importlib import import_module
 
-_CATALOG = ("mlops_amd.providers.mi355x.moe", "mlops_amd.providers.mi355x.moe_composed")
+_CATALOG = (
+    "mlops_amd.providers.mi355x.moe",
+    "mlops_amd.providers.mi355x.moe_composed",
+    "mlops_amd.providers.mi355x.moe_current",
+)
 _REGISTERED = False
 
 

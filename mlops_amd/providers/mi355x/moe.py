@@ -31,6 +31,7 @@ import torch
 
 from ... import kernels, router
 from ...block_fp8 import BlockFP8Weight
+from ...row_fp8 import RowFP8Weight
 from ...dispatch import logical_costs as logical
 from ...dispatch.context import weight_gradient_dtype
 from ...dispatch.costs import flop_formula
@@ -53,6 +54,8 @@ def _arch(device: torch.device) -> str:
 
 def _precision(compute_precision, w13, w2):
     """``"fp8_block"`` when this implementation serves the request, else a refusal."""
+    if any(isinstance(w, RowFP8Weight) for w in (w13, w2)):
+        return None, "RowFP8Weight weights compute at fp8_current"
     containers = isinstance(w13, BlockFP8Weight) or isinstance(w2, BlockFP8Weight)
     if compute_precision == "fp8_block":
         return "fp8_block", None
@@ -70,10 +73,19 @@ def supports(
     shared_mode="add", swiglu_limit=None, **_kwargs,
 ) -> SupportResult:
     """Metadata-only checks; never runs a kernel."""
-    del surface, routed_scaling, shared_gate_weight, shared_mode, swiglu_limit
     _, refusal = _precision(compute_precision, w13_experts, w2_experts)
     if refusal is not None:
         return SupportResult.no(refusal)
+    return check_shapes(
+        h2, residual, router_weight, w13_experts, w2_experts, top_k=top_k,
+        routing_mode=routing_mode, router_bias=router_bias, n_group=n_group,
+        topk_group=topk_group, lengths=lengths, shared_w13=shared_w13, shared_w2=shared_w2)
+
+
+def check_shapes(h2, residual, router_weight, w13_experts, w2_experts, *, top_k, routing_mode,
+                 router_bias=None, n_group=1, topk_group=1, lengths=None, shared_w13=None,
+                 shared_w2=None) -> SupportResult:
+    """The device, dtype, shape and routing rules every MI355X MoE operator shares."""
     tensors = (h2, residual, router_weight, w13_experts, w2_experts)
     if not all(isinstance(t, torch.Tensor) for t in tensors):
         return SupportResult.no("MoE core arguments must be tensors")

@@ -39,6 +39,13 @@ PINNED = {
     "swiglu / routed_swiglu_backward": "torch autograd of silu(min(g,L))*clamp(u,L)",
     "native_moe": "dense-masked (reference) vs sparse-gathered evaluation; autograd gradients",
     "fp8_moe_forward / fp8_moe_backward": "equals native_moe when the quantizers are identities",
+    "quantize_rows_current": "128-wide rows equal the pinned quantize_rows_1x128; per-row closed"
+                             " form with numpy; zero row; amax element maps to +-448",
+    "quantize_weights_current": "the reference container test's bounds (row-max relative error"
+                                " < 0.07 both orientations); interleaved = chunk/stack of the plain"
+                                " layout; dequantized interleaved == plain",
+    "rowwise_gemm": "fp64 product vs a per-row dot-product loop",
+    "current_moe_forward": "equals native_moe when the quantizers are identities",
 }
 
 
@@ -285,7 +292,55 @@ def quantize_transpose_padded(rows_bf16, offsets, padded):
     return q, scales.t().contiguous(), total
 
 
+def quantize_rows_current(x):
+    """``(q e4m3 [R, W], scales fp32 [R])``: one descale per row --
+    kernels/quack_moe/quantize_rows.py:35-41, 210-226 (``amax * (1/448)`` in
+    fp32, floor 1e-12, RN division, clip to +-448, e4m3 rounding)."""
+    x = x.float()
+    amax = x.abs().amax(-1)
+    scales = torch.clamp_min(amax * torch.tensor(INV448, dtype=torch.float32), 1e-12)
+    q = _e4m3((x / scales[:, None]).clamp(-E4M3_MAX, E4M3_MAX))
+    return q, scales
+
+
+def interleave_rows(w):
+    """``[E, out, in]`` gate-then-up rows -> stored 2j = gate j, 2j + 1 = up j
+    (expert_parallel/quack/parameters/fp8.py:24-27)."""
+    experts, out, inner = w.shape
+    return w.view(experts, 2, out // 2, inner).transpose(1, 2).reshape(w.shape)
+
+
+def quantize_weights_current(w, interleaved=False):
+    """``(data [E,out,in], transposed [E,in,out], scale [E,out],
+    transposed_scale [E,in])``: both orientations quantized per row, rows
+    gate/up-adjacent when ``interleaved`` -- kernels/quack_moe/
+    quantize_transpose.py:316-339 (the GPU path: reciprocal-multiply descale,
+    :116-117 and :247-255 for the transposed orientation)."""
+    v = w.float()
+    if interleaved:
+        v = interleave_rows(v)
+    experts, out, inner = v.shape
+    data, scale = quantize_rows_current(v.reshape(experts * out, inner))
+    cols, cscale = quantize_rows_current(v.transpose(1, 2).reshape(experts * inner, out))
+    return (data.view(experts, out, inner), cols.view(experts, inner, out),
+            scale.view(experts, out), cscale.view(experts, inner))
+
+
 # ------------------------------------------------------------------ GEMMs
+def rowwise_gemm(aq, a_scales, wq, w_scales, offsets):
+    """fp64 ``(a @ w[e]^T) * a_scale[r] * w_scale[e, n]`` per expert: the
+    row-scaled epilogue GEMM of the fp8_current path (kernels/quack_moe/
+    fp8.py, providers/sonicmoe/fp8.py:205-247). ``wq`` is ``[E, N, K]``."""
+    a = aq.double() * a_scales.double()[:, None]
+    w = wq.double() * w_scales.double()[..., None]
+    out = torch.zeros(a.shape[0], w.shape[1], dtype=torch.float64)
+    for e in range(w.shape[0]):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi > lo:
+            out[lo:hi] = a[lo:hi] @ w[e].t()
+    return out
+
+
 def grouped_gemm(aq, a_scales, wq, w_scale, offsets, *, transposed=False, interleave=False):
     """fp64 product of the dequantized operands per expert -- the quantity
     kernels/block_fp8.py:120-236 and quack_moe/block_fp8_gemm.py:1424-1482
@@ -461,6 +516,36 @@ def fp8_moe_forward(x, residual, router_weight, w13_q, w13_s, w2_q, w2_s, *, top
     act = swiglu(h13, swiglu_limit)
     aq, as_ = quantize_rows_1x128(act)
     y = grouped_gemm(aq, as_, w2_q, w2_s, offsets).to(torch.bfloat16)
+    out = combine(y, slots, weights, residual)
+    aux, counts, prob_sum = routing_statistics(logits, ids, routing_mode, lengths, experts)
+    return dict(out=out, aux=aux, counts=counts, prob_sum=prob_sum, logits=logits,
+                weights=weights, ids=ids, order=order, offsets=offsets, slots=slots, xq=xq, xs=xs,
+                h13=h13, aq=aq, as_=as_, y=y)
+
+
+def current_moe_forward(x, residual, router_weight, w13, w2, *, top_k, routing_mode,
+                        router_bias=None, n_group=1, topk_group=1, routed_scaling=1.0,
+                        lengths=None, swiglu_limit=None, logits=None):
+    """The fp8_current layer forward at the MI355X provider's quantization
+    points: routed rows quantized per row, the up product against the
+    gate/up-adjacent rows of ``w13`` (``(data, transposed, scale,
+    transposed_scale)`` as quantize_weights_current gives with interleaved),
+    bf16 ``h13`` (interleaved), SwiGLU of it quantized per row, the down
+    product, combine. Restates providers/sonicmoe/moe.py:441-515 with
+    sonicmoe/fp8.py:205-264 (the activation from the stored pre-activation, as
+    project_down_from_preactivation does)."""
+    rows, width = x.shape
+    lengths = (rows,) if lengths is None else tuple(lengths)
+    experts = router_weight.shape[0]
+    if logits is None:
+        logits = router_logits(x, router_weight)
+    weights, ids = route(logits, top_k, routing_mode, bias=router_bias, n_group=n_group,
+                         topk_group=topk_group, routed_scaling=routed_scaling)
+    order, offsets, slots = sort_assignments(ids, experts)
+    xq, xs = quantize_rows_current(x[order.long() // top_k])
+    h13 = rowwise_gemm(xq, xs, w13[0], w13[2], offsets).to(torch.bfloat16)
+    aq, as_ = quantize_rows_current(swiglu(h13, swiglu_limit))
+    y = rowwise_gemm(aq, as_, w2[0], w2[2], offsets).to(torch.bfloat16)
     out = combine(y, slots, weights, residual)
     aux, counts, prob_sum = routing_statistics(logits, ids, routing_mode, lengths, experts)
     return dict(out=out, aux=aux, counts=counts, prob_sum=prob_sum, logits=logits,

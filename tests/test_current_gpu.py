@@ -1,0 +1,303 @@
+"""fp8_current (per-row e4m3 scaling) on the MI355X: kernels and layer.
+
+* Quantizers bit-exact against the oracle (``oracle.quantize_rows_current``,
+  ``quantize_weights_current``). The SwiGLU row quantizer is held to the same
+  bar as the block one: the hardware exp differs from the library's in the
+  last ulp.
+* The row-scaled GEMM within 1e-2 per-expert max-relative of the fp64 product
+  of its e4m3 operands (the GEMMs' bar, test_block_fp8_transpose_gemm.py
+  :486-531). Cases include an empty expert, partial tiles and both
+  orientations of a weight.
+* The layer: the forward within 1e-2 of the oracle at the provider's
+  quantization points (``oracle.current_moe_forward``), and everything
+  against the bf16 form on the same weights at the reference's bounds
+  (tests/test_sonicmoe_fp8.py:112-125). Also: per-call quantization equals
+  stored containers bitwise (:176-181); the SwiGLU limit reaches the kernels
+  (:144-173); the explicit surface equals autograd; repeat runs are bitwise
+  equal.
+"""
+
+import math
+
+import pytest
+import torch
+
+import mlops_amd
+from mlops_amd import RowFP8Weight
+from mlops_amd import kernels as K
+from mlops_amd.dispatch import use_implementation, weight_gradients_at
+from mlops_amd.explicit import moe as explicit
+from oracle import moe_oracle as O
+from tests.conftest import frob_rel, max_rel
+
+pytestmark = pytest.mark.gpu
+
+CURRENT = "mi355x.moe.fp8_current"
+
+
+def _bytes(t):
+    return t.cpu().view(torch.uint8)
+
+
+@pytest.mark.parametrize("width,gathered", [(2048, True), (384, False), (8, False)])
+def test_quantize_rows_current_bit_exact(device, width, gathered):
+    g = torch.Generator().manual_seed(40)
+    x = (torch.randn(300, width, generator=g) * 3).to(torch.bfloat16)
+    x[7] = 0
+    x[11, 3] = 2.0 ** 40  # one huge element: every other value of the row underflows
+    gather, div = None, 1
+    if gathered:
+        gather = torch.randint(0, 300 * 4, (1000,), generator=g, dtype=torch.int32)
+        div = 4
+    q, s = K.quantize_rows_current(x.to(device), gather=None if gather is None else gather.to(device),
+                                   gather_div=div)
+    src = x if gather is None else x[gather.long() // div]
+    oq, os_ = O.quantize_rows_current(src)
+    assert torch.equal(_bytes(q), oq.view(torch.uint8))
+    assert torch.equal(s.cpu(), os_)
+
+
+@pytest.mark.parametrize("tokens,width,top_k", [(300, 2048, 8), (7, 768, 3)])
+def test_permute_quantize_current_equals_gathered(device, tokens, width, top_k):
+    """Token-major quantization of the routed copies equals quantizing the
+    gathered rows, bit for bit."""
+    g = torch.Generator().manual_seed(49)
+    x = (torch.randn(tokens, width, generator=g) * 2).to(torch.bfloat16)
+    x[1] = 0
+    ids = torch.stack([torch.randperm(8, generator=g)[:top_k] for _ in range(tokens)]).int()
+    order, offsets, slots = O.sort_assignments(ids, 8)
+    q, s = K.permute_quantize_current(x.to(device), slots.to(device))
+    gq, gs = K.quantize_rows_current(x.to(device), gather=order.to(device), gather_div=top_k)
+    assert torch.equal(_bytes(q), _bytes(gq)) and torch.equal(s, gs)
+    oq, os_ = O.quantize_rows_current(x[order.long() // top_k])
+    assert torch.equal(_bytes(q), oq.view(torch.uint8)) and torch.equal(s.cpu(), os_)
+
+
+@pytest.mark.parametrize("shape,dtype,interleaved", [
+    ((4, 256, 384), torch.bfloat16, True),
+    ((3, 208, 136), torch.float32, False),
+    ((2, 1536, 2048), torch.bfloat16, True),
+    ((2, 64, 4096 + 256), torch.bfloat16, False),  # rows wider than one 2048-column chunk
+])
+def test_quantize_weights_current_bit_exact(device, shape, dtype, interleaved):
+    g = torch.Generator().manual_seed(41)
+    w = (torch.randn(*shape, generator=g) * 0.02).to(dtype)
+    w[0, 5] = 0
+    w[1, :, 9] = 0
+    data, transposed, scale, tscale = K.quantize_weights_current(w.to(device),
+                                                                 interleaved=interleaved)
+    od, ot, os_, ots = O.quantize_weights_current(w, interleaved=interleaved)
+    assert torch.equal(_bytes(data), od.view(torch.uint8))
+    assert torch.equal(scale.cpu(), os_)
+    assert torch.equal(_bytes(transposed), ot.view(torch.uint8))
+    assert torch.equal(tscale.cpu(), ots)
+
+
+def test_container_quantize_and_publication(device):
+    """The reference's container checks (tests/test_sonicmoe_fp8.py:261-303)."""
+    weight = torch.randn(3, 16, 32, device=device, dtype=torch.bfloat16)
+    plain = RowFP8Weight.quantize(weight)
+    data, transposed, scale, tscale = plain.components()
+    assert data.shape == (3, 16, 32) and transposed.shape == (3, 32, 16)
+    interleaved = RowFP8Weight.quantize(weight, interleaved=True)
+    expected = torch.stack(data.chunk(2, dim=1), dim=2).reshape(data.shape)
+    assert torch.equal(interleaved._data.view(torch.uint8), expected.view(torch.uint8))
+    assert torch.equal(interleaved.dequantize(), plain.dequantize())
+    published = RowFP8Weight(*[torch.empty_like(v) for v in interleaved.components()],
+                             dtype=torch.bfloat16, interleaved=True)
+    published.copy_(weight * 1.5)
+    again = RowFP8Weight.quantize(weight * 1.5, interleaved=True)
+    for value, other in zip(published.components(), again.components()):
+        assert torch.equal(value.view(torch.uint8), other.view(torch.uint8))
+
+
+@pytest.mark.parametrize("limit", [None, 0.5])
+def test_swiglu_quantize_rows_current(device, limit):
+    g = torch.Generator().manual_seed(42)
+    h = torch.randn(257, 2 * 768, generator=g).to(torch.bfloat16)
+    q, s = K.swiglu_quantize_rows_current(h.to(device), limit)
+    oq, os_ = O.quantize_rows_current(O.swiglu(h, limit))
+    assert max_rel(s.cpu(), os_) < 1e-6
+    same = (_bytes(q) == oq.view(torch.uint8)).float().mean().item()
+    assert same > 0.999
+    assert frob_rel(q.cpu().float() * s.cpu()[:, None], oq.float() * os_[:, None]) < 1e-2
+
+
+def _ragged(counts):
+    offsets = torch.zeros(len(counts) + 1, dtype=torch.int32)
+    offsets[1:] = torch.cumsum(torch.tensor(counts), 0)
+    return offsets
+
+
+@pytest.mark.parametrize("counts,n,k", [
+    ([300, 0, 17, 256, 1], 512, 512),
+    ([1024, 1000, 999], 1536, 2048),
+    ([5], 256, 256),
+])
+def test_gemm_rowwise_matches_fp64(device, counts, n, k):
+    g = torch.Generator().manual_seed(43)
+    experts = len(counts)
+    offsets = _ragged(counts)
+    rows = int(offsets[-1])
+    w = (torch.randn(experts, n, k, generator=g) * 0.02).to(torch.bfloat16)
+    wq, wt, ws, wts = K.quantize_weights_current(w.to(device))
+    x = (torch.randn(rows, k, generator=g)).to(torch.bfloat16)
+    xq, xs = K.quantize_rows_current(x.to(device))
+    out = K.gemm_rowwise(xq, xs, wq, ws, offsets.to(device)).cpu()
+    want = O.rowwise_gemm(xq.cpu(), xs.cpu(), wq.cpu(), ws.cpu(), offsets)
+    for e in range(experts):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi > lo:
+            assert max_rel(out[lo:hi].double(), want[lo:hi]) < 1e-2, e
+    # The input-gradient orientation: rows [rows, N] against the transposed copy.
+    y = torch.randn(rows, n, generator=g).to(torch.bfloat16)
+    yq, ys = K.quantize_rows_current(y.to(device))
+    dx = K.gemm_rowwise(yq, ys, wt, wts, offsets.to(device)).cpu()
+    want = O.rowwise_gemm(yq.cpu(), ys.cpu(), wt.cpu(), wts.cpu(), offsets)
+    nonempty = [e for e in range(experts) if counts[e]]
+    for e in nonempty:
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        assert max_rel(dx[lo:hi].double(), want[lo:hi]) < 1e-2, e
+
+
+# ---------------------------------------------------------------- layer
+def _inputs(device, tokens=256, hidden=512, experts=8, inter=256, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(tokens, hidden, generator=g).to(torch.bfloat16)
+    res = torch.randn(tokens, hidden, generator=g).to(torch.bfloat16)
+    wr = torch.randn(experts, hidden, generator=g) / math.sqrt(hidden)
+    w13 = (torch.randn(experts, 2 * inter, hidden, generator=g) / math.sqrt(hidden)).to(torch.bfloat16)
+    w2 = (torch.randn(experts, hidden, inter, generator=g) / math.sqrt(inter)).to(torch.bfloat16)
+    dy = torch.randn(tokens, hidden, generator=g).to(torch.bfloat16)
+    return [t.to(device) for t in (x, res, wr, w13, w2, dy)]
+
+
+NAMES = ("out", "aux", "counts", "psum", "gx", "gres", "gr", "g13", "g2")
+# The reference's bounds for fp8_current against the bf16 form
+# (tests/test_sonicmoe_fp8.py:112-125); 2e-2 for the rest. The weight
+# gradients get the block-FP8 bound (8e-2, test_sonicmoe_block_fp8.py:350)
+# instead of 6e-2: here they come from e4m3 operands, where the reference's
+# fp8_current path computes them in bf16.
+BOUNDS = {"out": 4e-2, "gx": 8e-2, "gr": 8e-2, "g13": 8e-2, "g2": 8e-2}
+
+
+def _run(x, res, wr, w13, w2, dy, *, fp8_weights=True, grad_dtype=None, **kw):
+    x = x.clone().requires_grad_(True)
+    res = res.clone().requires_grad_(True)
+    wr = wr.clone().requires_grad_(True)
+    if fp8_weights:
+        w13 = RowFP8Weight.quantize(w13.detach(), interleaved=True).requires_grad_(True)
+        w2 = RowFP8Weight.quantize(w2.detach()).requires_grad_(True)
+    else:
+        w13 = w13.clone().requires_grad_(True)
+        w2 = w2.clone().requires_grad_(True)
+    with weight_gradients_at(grad_dtype):
+        out, aux, counts, psum = mlops_amd.moe(x, res, wr, w13, w2, **kw)
+    torch.autograd.backward([out, aux], [dy, torch.ones_like(aux) * 0.3])
+    return dict(out=out.detach(), aux=aux.detach(), counts=counts, psum=psum.detach(), gx=x.grad,
+                gres=res.grad, gr=wr.grad, g13=w13.grad, g2=w2.grad)
+
+
+def _native(x, res, wr, w13, w2, dy, **kw):
+    """The reference's native path on the bf16 weights (fp32 autograd)."""
+    leaves = [t.float().clone().requires_grad_(True) for t in (x, res, wr, w13, w2)]
+    out, aux, counts, psum = O.native_moe(*leaves, **kw)
+    torch.autograd.backward([out, aux], [dy.float(), torch.ones_like(aux) * 0.3])
+    return dict(out=out.detach(), aux=aux.detach(), counts=counts, psum=psum.detach(),
+                gx=leaves[0].grad, gres=leaves[1].grad, gr=leaves[2].grad, g13=leaves[3].grad,
+                g2=leaves[4].grad)
+
+
+@pytest.mark.parametrize("mode", ["softmax_then_topk", "topk_then_softmax", "sigmoid_noaux_tc"])
+def test_layer_against_the_oracle_and_the_bf16_form(device, mode):
+    x, res, wr, w13, w2, dy = _inputs(device, seed=44)
+    kw = dict(top_k=2, routing_mode=mode)
+    if mode == "sigmoid_noaux_tc":
+        kw.update(n_group=4, topk_group=2)
+    r = _run(x, res, wr, w13, w2, dy, **kw)
+    # The forward at the provider's own quantization points.
+    from mlops_amd import router
+    w13c = RowFP8Weight.quantize(w13, interleaved=True)
+    w2c = RowFP8Weight.quantize(w2)
+    cpu = lambda c: tuple(t.cpu() for t in c.components())
+    w13o, w2o = cpu(w13c), cpu(w2c)
+    fwd = O.current_moe_forward(x.cpu(), res.cpu(), wr.cpu(), (w13o[0], w13o[1], w13o[2], w13o[3]),
+                                (w2o[0], w2o[1], w2o[2], w2o[3]), logits=router.router_logits(x, wr).cpu(),
+                                **kw)
+    assert torch.equal(r["counts"].cpu(), fwd["counts"])
+    assert frob_rel(r["out"].cpu().float(), fwd["out"].float()) < 1e-2
+    # Everything against the bf16 form at the reference's bounds.
+    ref = _native(x.cpu(), res.cpu(), wr.cpu(), w13.cpu(), w2.cpu(), dy.cpu(), **kw)
+    for name in NAMES:
+        a, b = r[name].cpu(), ref[name].cpu()
+        if not a.is_floating_point():
+            assert torch.equal(a, b), name
+            continue
+        assert frob_rel(a.float(), b.float()) <= BOUNDS.get(name, 2e-2), name
+    assert r["g13"].dtype == torch.bfloat16 and r["g2"].dtype == torch.bfloat16
+
+
+def test_fp32_weight_gradients(device):
+    """Under an fp32 gradient policy the operator writes fp32 weight
+    gradients; autograd then delivers them at each leaf's dtype (a container's
+    logical dtype), as for the plain bf16 weights of the same call."""
+    x, res, wr, w13, w2, dy = _inputs(device, seed=45)
+    kw = dict(top_k=2, routing_mode="softmax_then_topk")
+    r = _run(x, res, wr, w13, w2, dy, grad_dtype=torch.float32, **kw)
+    plain = _run(x, res, wr, w13, w2, dy, fp8_weights=False, grad_dtype=torch.float32,
+                 compute_precision="fp8_current", **kw)
+    assert r["g13"].dtype == plain["g13"].dtype == torch.bfloat16
+    assert r["gr"].dtype == torch.float32
+    w13c = RowFP8Weight.quantize(w13, interleaved=True)
+    w2c = RowFP8Weight.quantize(w2)
+    outs = explicit.forward(x, res, wr, w13c, w2c, **kw)
+    (out, aux, counts, psum, logits, weights, ids, order, offsets, slots, h13) = outs
+    with weight_gradients_at(torch.float32):
+        grads = explicit.backward(dy, torch.zeros_like(aux), torch.zeros_like(psum), x, wr, w13c,
+                                  w2c, logits, weights, ids, order, offsets, slots, h13, **kw,
+                                  lengths=[x.shape[0]])
+    assert grads[3].dtype == torch.float32 and grads[4].dtype == torch.float32
+
+
+def test_per_call_quantization_equals_stored_containers(device):
+    """A bf16 weight asked for fp8_current math is quantized per call exactly
+    as the stored containers are (reference tests/test_sonicmoe_fp8.py:176-181)."""
+    args = _inputs(device, seed=46)
+    stored = _run(*args, top_k=2, routing_mode="softmax_then_topk")
+    per_call = _run(*args, fp8_weights=False, top_k=2, routing_mode="softmax_then_topk",
+                    compute_precision="fp8_current")
+    for name in NAMES:
+        assert torch.equal(stored[name], per_call[name]), name
+
+
+def test_the_limit_reaches_the_kernels(device):
+    """(reference tests/test_sonicmoe_fp8.py:144-173)"""
+    args = _inputs(device, seed=47)
+    kw = dict(top_k=2, routing_mode="softmax_then_topk")
+    far = _run(*args, swiglu_limit=3.5, **kw)
+    ref = _native(*[t.cpu() for t in args], swiglu_limit=3.5, **kw)
+    assert frob_rel(far["out"].cpu().float(), ref["out"].float()) < BOUNDS["out"]
+    clamped = _run(*args, swiglu_limit=0.75, **kw)
+    plain = _run(*args, **kw)
+    for name in ("out", "gx", "g13", "g2"):
+        assert frob_rel(clamped[name].float(), plain[name].float()) > 5e-2, name
+
+
+def test_explicit_surface_equals_autograd_and_repeats(device):
+    x, res, wr, w13, w2, dy = _inputs(device, seed=48)
+    kw = dict(top_k=2, routing_mode="topk_then_softmax")
+    r = _run(x, res, wr, w13, w2, dy, **kw)
+    again = _run(x, res, wr, w13, w2, dy, **kw)
+    for name in NAMES:
+        assert torch.equal(r[name], again[name]), name
+    w13c = RowFP8Weight.quantize(w13, interleaved=True)
+    w2c = RowFP8Weight.quantize(w2)
+    with use_implementation("moe", CURRENT):
+        outs = explicit.forward(x, res, wr, w13c, w2c, **kw)
+        (out, aux, counts, psum, logits, weights, ids, order, offsets, slots, h13) = outs
+        grads = explicit.backward(dy, torch.full_like(aux, 0.3), torch.zeros_like(psum), x, wr, w13c,
+                                  w2c, logits, weights, ids, order, offsets, slots, h13, **kw,
+                                  lengths=[x.shape[0]])
+    assert torch.equal(out, r["out"])
+    for got, name in zip(grads, ("gx", "gres", "gr", "g13", "g2")):
+        assert torch.equal(got, r[name]), name

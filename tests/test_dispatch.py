@@ -36,7 +36,10 @@ def _args(tokens=4, hidden=256, experts=8, inter=128, device="cpu", dtype=torch.
 
 def test_catalog_contains_the_provider():
     table = implementation_registry()["moe"]
-    assert sorted(table) == ["mi355x.moe.block_fp8", "mi355x.moe.composed"]
+    assert sorted(table) == ["mi355x.moe.block_fp8", "mi355x.moe.composed",
+                             "mi355x.moe.fp8_current"]
+    current = table["mi355x.moe.fp8_current"]
+    assert current.deterministic and current.forward and current.backward
     impl = table["mi355x.moe.block_fp8"]
     assert impl.priority > 110 and impl.deterministic and impl.forward and impl.backward
     # The two-region form is semantic-only (no explicit forward/backward, as
@@ -134,6 +137,78 @@ def test_support_refusals_with_a_gfx950_device(monkeypatch):
     for args, extra, reason in cases:
         result = provider.supports(*map(gpu, args), **{**base, **extra})
         assert not result and reason in result.reason, (extra, result.reason)
+
+
+def test_fp8_current_support_rules(monkeypatch):
+    """Which operator serves which precision and container (reference
+    tests/test_sonicmoe_fp8.py:314-341, 386-423), past the device gate."""
+    from mlops_amd import RowFP8Weight
+    from mlops_amd.providers.mi355x import moe_current
+
+    monkeypatch.setattr(torch.version, "hip", "7.0", raising=False)
+    monkeypatch.setattr(provider, "_arch", lambda device: "gfx950:sramecc+:xnack-")
+
+    class FakeCuda(torch.Tensor):
+        pass
+
+    monkeypatch.setattr(FakeCuda, "is_cuda", property(lambda self: True))
+    gpu = lambda t: t.as_subclass(FakeCuda)
+    base = dict(surface="semantic", top_k=2, routing_mode="topk_then_softmax")
+
+    def container(w, interleaved=False):
+        e, out, inner = w.shape
+        fp8 = torch.float8_e4m3fn
+        return RowFP8Weight(torch.zeros(e, out, inner, dtype=fp8), torch.zeros(e, inner, out, dtype=fp8),
+                            torch.ones(e, out), torch.ones(e, inner), dtype=torch.bfloat16,
+                            interleaved=interleaved)
+
+    x, res, wr, w13, w2 = map(gpu, _args(hidden=256, inter=256))
+    ok = moe_current.supports(x, res, wr, w13, w2, compute_precision="fp8_current", **base)
+    assert ok, ok.reason
+    # The block operator refuses fp8_current; the current one refuses block weights.
+    refused = provider.supports(x, res, wr, w13, w2, compute_precision="fp8_current", **base)
+    assert not refused and "block-FP8 only" in refused.reason
+    c13, c2 = container(w13, interleaved=True), container(w2)
+    assert moe_current.supports(x, res, wr, c13, c2, **base)
+    refused = provider.supports(x, res, wr, c13, c2, compute_precision="fp8_block", **base)
+    assert not refused and "fp8_current" in refused.reason
+    refused = moe_current.supports(x, res, wr, container(w13), c2, **base)
+    assert not refused and "interleaved=True" in refused.reason
+    narrow = map(gpu, _args(hidden=256, inter=128))
+    refused = moe_current.supports(*narrow, compute_precision="fp8_current", **base)
+    assert not refused and "multiples of 256" in refused.reason
+    refused = moe_current.supports(x, res, wr, w13, w2, compute_precision="fp8_block", **base)
+    assert not refused
+
+
+def test_row_fp8_container_on_cpu():
+    """Components, shapes and the interleaved row order in both orientations
+    (reference tests/test_sonicmoe_fp8.py:261-303), built from components."""
+    from mlops_amd import QuackFP8Weight, RowFP8Weight
+
+    assert QuackFP8Weight is RowFP8Weight
+    g = torch.Generator().manual_seed(0)
+    e, out, inner = 2, 8, 16
+    data = (torch.randn(e, out, inner, generator=g) * 50).to(torch.float8_e4m3fn)
+    scale = torch.rand(e, out, generator=g) + 0.5
+    logical = data.float() * scale[..., None]
+    # The interleaved container of the same rows: stored 2j = gate j, 2j+1 = up j.
+    stored = torch.stack(data.chunk(2, dim=1), dim=2).reshape(data.shape)
+    stored_scale = torch.stack(scale.chunk(2, dim=1), dim=2).reshape(scale.shape)
+    fp8 = torch.float8_e4m3fn
+    weight = RowFP8Weight(stored, torch.zeros(e, inner, out, dtype=fp8), stored_scale,
+                          torch.ones(e, inner), dtype=torch.bfloat16, interleaved=True)
+    assert weight.shape == (e, out, inner) and weight.dtype == torch.bfloat16
+    assert weight.interleaved and len(weight.components()) == 4
+    assert torch.equal(weight.dequantize(dtype=torch.float32), logical)
+    clone = weight.clone()
+    assert torch.equal(clone._data.view(torch.uint8), stored.view(torch.uint8))
+    with pytest.raises(ValueError, match="row orders"):
+        clone.copy_(RowFP8Weight(*weight.components(), interleaved=False))
+    with pytest.raises(ValueError, match="MI355X"):
+        RowFP8Weight.quantize(torch.randn(e, out, inner))
+    with pytest.raises(ValueError, match="transpose"):
+        RowFP8Weight(data, torch.zeros(e, out, inner, dtype=fp8), scale, torch.ones(e, inner))
 
 
 def test_facade_validation():

@@ -439,3 +439,86 @@ def test_oracle_lora_with_zero_b_factors_is_the_plain_layer():
     ref = O.native_moe(x, res, wr, w13, w2, **opts)
     for a, b in zip(got, ref):
         assert torch.equal(a, b)
+
+
+# --------------------------------------------------------------------------
+# fp8_current (per-row scaling) functions of the oracle.
+def test_quantize_rows_current_closed_form():
+    """128-wide rows are the pinned 1x128 quantizer's single group; wider rows
+    follow the per-row closed form (numpy fp32); zero rows stay zero; the
+    amax element maps to +-448."""
+    torch.manual_seed(21)
+    x = (torch.randn(9, 128) * 5).to(torch.bfloat16)
+    q, s = O.quantize_rows_current(x)
+    q1, s1 = O.quantize_rows_1x128(x)
+    assert torch.equal(q.view(torch.uint8), q1.view(torch.uint8))
+    assert torch.equal(s, s1[0])
+    x = (torch.randn(7, 384) * 3).to(torch.bfloat16)
+    x[2] = 0
+    q, s = O.quantize_rows_current(x)
+    assert q.shape == (7, 384) and s.shape == (7,)
+    xf = x.float().numpy()
+    for r in range(7):
+        amax = np.float32(np.abs(xf[r]).max())
+        want = max(np.float32(amax * (np.float32(1.0) / np.float32(448.0))), np.float32(1e-12))
+        assert s[r].item() == float(want)
+        if amax > 0:
+            assert q[r].float().abs().max().item() == 448.0
+    assert torch.all(q[2].float() == 0)
+    assert frob_rel(q.float() * s[:, None], x.float()) < 4e-2
+
+
+def test_quantize_weights_current_container_bounds():
+    """The reference's container checks (tests/test_sonicmoe_fp8.py:261-291):
+    per-row relative error < 0.07 of the row maximum in both orientations; the
+    interleaved container stores row 2j = gate j, 2j + 1 = up j in both, and
+    dequantizes to the same logical weight."""
+    torch.manual_seed(22)
+    w = torch.randn(3, 8, 32).to(torch.bfloat16)
+    data, transposed, scale, tscale = O.quantize_weights_current(w)
+    assert data.shape == (3, 8, 32) and transposed.shape == (3, 32, 8)
+    assert scale.shape == (3, 8) and tscale.shape == (3, 32)
+    row_max = w.float().abs().amax(-1, keepdim=True)
+    restored = data.float() * scale[..., None]
+    assert float(((restored - w.float()).abs() / row_max).max()) < 0.07
+    restored_t = (transposed.float() * tscale[..., None]).transpose(1, 2)
+    assert float(((restored_t - w.float()).abs() / row_max).max()) < 0.07
+    i_data, i_transposed, i_scale, _ = O.quantize_weights_current(w, interleaved=True)
+    expected = torch.stack(data.chunk(2, dim=1), dim=2).reshape(data.shape)
+    assert torch.equal(i_data.view(torch.uint8), expected.view(torch.uint8))
+    expected_t = torch.stack(transposed.chunk(2, dim=2), dim=3).reshape(transposed.shape)
+    assert torch.equal(i_transposed.view(torch.uint8), expected_t.view(torch.uint8))
+    logical = (i_data.float() * i_scale[..., None]).view(3, 4, 2, 32).transpose(1, 2)
+    assert torch.equal(logical.reshape(3, 8, 32), restored)
+
+
+def test_rowwise_gemm_matches_loop():
+    torch.manual_seed(23)
+    w = torch.randn(3, 64, 128) * 0.02
+    wq, _, ws, _ = O.quantize_weights_current(w)
+    offsets = torch.tensor([0, 5, 5, 12], dtype=torch.int32)
+    xq, xs = O.quantize_rows_current(torch.randn(12, 128).to(torch.bfloat16))
+    out = O.rowwise_gemm(xq, xs, wq, ws, offsets)
+    for row in range(12):
+        e = 0 if row < 5 else 2
+        for n in (0, 33, 63):
+            want = sum(xq[row, kk].double().item() * wq[e, n, kk].double().item()
+                       for kk in range(128)) * xs[row].item() * ws[e, n].item()
+            assert abs(out[row, n].item() - want) < 1e-9 * max(1.0, abs(want))
+
+
+def test_current_forward_is_the_layer_when_quantizers_are_identities(monkeypatch):
+    """With the e4m3 rounding replaced by the identity, the fp8_current
+    forward is the native layer up to its bf16 roundings: a wrong gather,
+    gate/up order, scale or orientation fails this."""
+    monkeypatch.setattr(O, "_e4m3", lambda values: values)
+    x, res, wr, w13, w2 = _layer_inputs(seed=24)
+    res = torch.zeros_like(res)  # the routed part alone, without bf16 residual rounding
+    w13c = O.quantize_weights_current(w13, interleaved=True)
+    w2c = O.quantize_weights_current(w2)
+    fwd = O.current_moe_forward(x, res, wr, w13c, w2c, top_k=2, routing_mode="softmax_then_topk",
+                                swiglu_limit=0.05)
+    out, _, counts, _ = O.native_moe(x.float(), res.float(), wr, w13.float(), w2.float(), top_k=2,
+                                     routing_mode="softmax_then_topk", swiglu_limit=0.05)
+    assert torch.equal(fwd["counts"], counts)
+    assert frob_rel(fwd["out"].float(), out.detach().float()) < 1e-2
