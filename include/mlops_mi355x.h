@@ -286,7 +286,11 @@ int mi355x_swiglu_quantize_rows_current_fp8(const void* h, int rows, int width, 
  * (expert_parallel/quack/parameters/fp8.py:36-54, 111-121). */
 int mi355x_quantize_weights_current_fp8(const void* w, int is_fp32, int experts, int out, int in,
                                         int interleave, uint8_t* q, float* scales, uint8_t* qt,
-                                        float* scales_t, void* stream);
+                                        float* scales_t, void* workspace, size_t workspace_bytes,
+                                        void* stream);
+/* Bytes of device workspace mi355x_quantize_weights_current_fp8 needs (the
+ * column maxima of each 128-row tile). */
+size_t mi355x_quantize_weights_current_workspace_size(int experts, int out, int in);
 
 /* Thin grouped product of expert LoRA: out[r, 0:R] = sum_k a[r, k] *
  * bt[e][0:R, k] for the rows r of expert e (offsets[E+1]), a bf16 [rows, K],

@@ -142,29 +142,30 @@ __global__ void __launch_bounds__(256) swiglu_rows_current_kernel(
 }
 
 // Both orientations of weights w [E, out, in] in two passes over w:
-//  1. weight_amax_kernel: one block per (128 stored rows, expert). It writes
-//     each row's scale (a wave reduces a whole row), and merges the rows'
-//     column maxima into col_bits[e, c] with an integer atomicMax on the
-//     float bits. Maxima are >= 0, so unsigned order is float order, and the
-//     merge is order-independent.
-//  2. weight_quantize_kernel: one block per (64 x 64 tile, expert). It
+//  1. weight_amax_kernel: one block per (64 stored rows, expert). It writes
+//     each row's scale (a wave reduces a whole row), and the maxima of its
+//     rows per column to colpart[e][tile][c] in the workspace.
+//  2. col_scale_kernel reduces colpart over the row tiles into the column
+//     scales.
+//  3. weight_quantize_kernel: one block per (128 x 128 tile, expert). It
 //     quantizes the tile with its rows' scales into q, and with its columns'
-//     scales (from col_bits) into qt, through an LDS transpose.
-//  3. col_scale_kernel turns col_bits into the column scales in place.
+//     scales into qt through an LDS transpose.
 // Stored row p of an expert is logical row p, or with interleave the
 // gate/up-adjacent order (2j = gate j, 2j + 1 = up j), in both orientations.
 __device__ __forceinline__ int logical_row(int p, int out, int interleave) {
   return interleave ? ((p & 1) ? out / 2 + (p >> 1) : (p >> 1)) : p;
 }
 
-constexpr int kAmaxRows = 128;
+constexpr int kAmaxRows = 64;  // 3 x 256 blocks fill the GPU evenly for E = 128, out = 1536
+constexpr int kQTile = 128;
 
 template <typename T>
 __global__ void __launch_bounds__(256) weight_amax_kernel(
     const T* __restrict__ w, int out, int in, int interleave, float* __restrict__ scales,
-    uint32_t* __restrict__ col_bits) {
+    float* __restrict__ colpart) {
   __shared__ float colmax[4][2048 + 8];  // per-wave column maxima of a 2048-column chunk
-  const int e = blockIdx.y, p0 = blockIdx.x * kAmaxRows;
+  const int e = blockIdx.y, tile = blockIdx.x, p0 = tile * kAmaxRows;
+  const int tiles = gridDim.x;
   const int wave = threadIdx.x >> 6, lane = lane_id();
   const T* we = w + (size_t)e * out * in;
   const int prows = min(kAmaxRows, out - p0);
@@ -173,33 +174,47 @@ __global__ void __launch_bounds__(256) weight_amax_kernel(
     float cm[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) cm[i] = 0.0f;
-    // Wave w takes rows w, w + 4, ...; lane l takes 8 columns per 512.
-    for (int pr = wave; pr < prows; pr += 4) {
-      const int p = p0 + pr;
-      const T* row = we + (size_t)logical_row(p, out, interleave) * in + c0;
-      float rmax = 0.0f;
+    // Wave w takes rows w, w + 4, ..., two at a time (all eight loads of a
+    // pair issued before the maxima); lane l takes 8 columns per 512.
+    for (int pr = wave; pr < prows; pr += 8) {
+      float rmax[2] = {0.0f, 0.0f};
+      float v[2][4][8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int col = u * 512 + lane * 8;
-        if (col < cw) {
-          float v[8];
-          load8(row + col, v);
+      for (int h = 0; h < 2; ++h) {
+        const int p = p0 + pr + 4 * h;
+        const T* row = we + (size_t)logical_row(p, out, interleave) * in + c0;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float a = fabsf(v[i]);
-            rmax = fmaxf(rmax, a);
-            cm[u * 8 + i] = fmaxf(cm[u * 8 + i], a);
+        for (int u = 0; u < 4; ++u) {
+          const int col = u * 512 + lane * 8;
+          if (pr + 4 * h < prows && col < cw) {
+            load8(row + col, v[h][u]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[h][u][i] = 0.0f;
           }
         }
       }
-      rmax = wave_max(rmax);
-      // The row's running maximum over the column chunks lives in scales[]
-      // (this block is the row's only writer), finished after the last chunk.
-      if (lane == 0) {
-        const size_t at = (size_t)e * out + p;
-        const float prev = c0 == 0 ? 0.0f : scales[at];
-        const float m = fmaxf(prev, rmax);
-        scales[at] = c0 + 2048 >= in ? fmaxf(m * kInv448, kMinScale) : m;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float a = fabsf(v[h][u][i]);
+            rmax[h] = fmaxf(rmax[h], a);
+            cm[u * 8 + i] = fmaxf(cm[u * 8 + i], a);
+          }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float m_row = wave_max(rmax[h]);
+        // The row's running maximum over the column chunks lives in scales[]
+        // (this block is the row's only writer), finished after the last chunk.
+        if (lane == 0 && pr + 4 * h < prows) {
+          const size_t at = (size_t)e * out + p0 + pr + 4 * h;
+          const float prev = c0 == 0 ? 0.0f : scales[at];
+          const float m = fmaxf(prev, m_row);
+          scales[at] = c0 + 2048 >= in ? fmaxf(m * kInv448, kMinScale) : m;
+        }
       }
     }
 #pragma unroll
@@ -207,61 +222,83 @@ __global__ void __launch_bounds__(256) weight_amax_kernel(
 #pragma unroll
       for (int i = 0; i < 8; ++i) colmax[wave][u * 512 + lane * 8 + i] = cm[u * 8 + i];
     __syncthreads();
-    for (int c = threadIdx.x; c < cw; c += 256) {
-      const float m = fmaxf(fmaxf(colmax[0][c], colmax[1][c]), fmaxf(colmax[2][c], colmax[3][c]));
-      atomicMax(&col_bits[(size_t)e * in + c0 + c], __float_as_uint(m));
-    }
+    float* part = colpart + ((size_t)e * tiles + tile) * in + c0;
+    for (int c = threadIdx.x; c < cw; c += 256)
+      part[c] = fmaxf(fmaxf(colmax[0][c], colmax[1][c]), fmaxf(colmax[2][c], colmax[3][c]));
     __syncthreads();
   }
 }
 
-constexpr int kQTile = 64;
+__global__ void __launch_bounds__(256) col_scale_kernel(const float* __restrict__ colpart,
+                                                        int experts, int tiles, int in,
+                                                        float* __restrict__ scales_t) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // e * in + c
+  if (i >= (size_t)experts * in) return;
+  const size_t e = i / in, c = i - e * in;
+  const float* part = colpart + e * tiles * in + c;
+  float m = 0.0f;
+  for (int k = 0; k < tiles; ++k) m = fmaxf(m, part[(size_t)k * in]);
+  scales_t[i] = fmaxf(m * kInv448, kMinScale);
+}
 
 template <typename T>
 __global__ void __launch_bounds__(256) weight_quantize_kernel(
     const T* __restrict__ w, int out, int in, int interleave, const float* __restrict__ scales,
-    const uint32_t* __restrict__ col_bits, uint8_t* __restrict__ q, uint8_t* __restrict__ qt) {
-  __shared__ uint8_t tile[kQTile][kQTile + 16];  // [column][stored row]
+    const float* __restrict__ scales_t, uint8_t* __restrict__ q, uint8_t* __restrict__ qt) {
+  __shared__ uint8_t tile[kQTile][kQTile + 8];  // [column][stored row]
+  __shared__ float colscale[kQTile];
   const int e = blockIdx.z, p0 = blockIdx.y * kQTile, c0 = blockIdx.x * kQTile;
-  const int t = threadIdx.x, cg = t & 7, rl = t >> 3;  // 8 column groups x 32 rows
+  const int t = threadIdx.x, cg = t & 15, rg = t >> 4;  // 16 column groups x 16 row groups
   const int col = c0 + cg * 8;
+  const bool col_ok = col < in;
   const T* we = w + (size_t)e * out * in;
-  float cs[8], ci[8];
+  // The thread's 8 consecutive rows rg * 8 + i, all loads issued first.
+  float v[8][8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float amax = col + i < in ? __uint_as_float(col_bits[(size_t)e * in + col + i]) : 0.0f;
-    cs[i] = fmaxf(amax * kInv448, kMinScale);
-    ci[i] = 1.0f / cs[i];
-  }
+    const int p = p0 + rg * 8 + i;
+    if (p < out && col_ok) {
+      load8(we + (size_t)logical_row(p, out, interleave) * in + col, v[i]);
+    } else {
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    const int pl = rl + 32 * half, p = p0 + pl;
-    if (p < out && col < in) {
-      float v[8];
-      load8(we + (size_t)logical_row(p, out, interleave) * in + col, v);
-      const float rs = scales[(size_t)e * out + p];
-      *(uint2*)(q + ((size_t)e * out + p) * in + col) = quant8(v, rs);
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        tile[cg * 8 + i][pl] =
-            (uint8_t)(f32x2_to_e4m3(quant_div_inv(v[i], cs[i], ci[i]), 0.0f) & 0xffu);
+      for (int j = 0; j < 8; ++j) v[i][j] = 0.0f;
     }
   }
+  if (t < kQTile) colscale[t] = c0 + t < in ? scales_t[(size_t)e * in + c0 + t] : 1.0f;
   __syncthreads();
-  // 64 qt rows x 64 bytes: thread t writes 16 bytes of row t / 4.
-  const int cc = t >> 2, seg = (t & 3) * 16;
-  if (c0 + cc < in && p0 + seg < out)
-    *(uint4*)(qt + ((size_t)e * in + c0 + cc) * out + p0 + seg) = *(const uint4*)&tile[cc][seg];
-}
-
-__global__ void __launch_bounds__(256) fill_zero_kernel(uint32_t* __restrict__ p, size_t n) {
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < n) p[i] = 0u;
-}
-
-__global__ void __launch_bounds__(256) col_scale_kernel(float* __restrict__ scales_t, size_t n) {
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < n) scales_t[i] = fmaxf(scales_t[i] * kInv448, kMinScale);
+  float cs[8], ci[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    cs[j] = colscale[cg * 8 + j];
+    ci[j] = 1.0f / cs[j];
+  }
+  uint32_t lo[8], hi[8];  // column j's bytes of the thread's 8 rows
+#pragma unroll
+  for (int j = 0; j < 8; ++j) lo[j] = hi[j] = 0u;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int p = p0 + rg * 8 + i;
+    if (p < out && col_ok)
+      *(uint2*)(q + ((size_t)e * out + p) * in + col) = quant8(v[i], scales[(size_t)e * out + p]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t b = f32x2_to_e4m3(quant_div_inv(v[i][j], cs[j], ci[j]), 0.0f) & 0xffu;
+      if (i < 4) lo[j] |= b << (8 * i);
+      else hi[j] |= b << (8 * (i - 4));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) *(uint2*)&tile[cg * 8 + j][rg * 8] = make_uint2(lo[j], hi[j]);
+  __syncthreads();
+  // 128 qt rows x 128 bytes, four passes of 32 rows: thread t writes 16 bytes.
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int cc = pass * 32 + (t >> 3), seg = (t & 7) * 16;
+    if (c0 + cc < in && p0 + seg < out) {
+      const uint2 a = *(const uint2*)&tile[cc][seg], b = *(const uint2*)&tile[cc][seg + 8];
+      *(uint4*)(qt + ((size_t)e * in + c0 + cc) * out + p0 + seg) = make_uint4(a.x, a.y, b.x, b.y);
+    }
+  }
 }
 
 }  // namespace
@@ -295,32 +332,44 @@ extern "C" int mi355x_swiglu_quantize_rows_current_fp8(const void* h, int rows, 
   return MI355X_OK;
 }
 
+extern "C" size_t mi355x_quantize_weights_current_workspace_size(int experts, int out, int in) {
+  if (experts <= 0 || out <= 0 || in <= 0) return 0;
+  return (size_t)experts * ((out + kAmaxRows - 1) / kAmaxRows) * in * sizeof(float);
+}
+
 extern "C" int mi355x_quantize_weights_current_fp8(const void* w, int is_fp32, int experts,
                                                    int out, int in, int interleave, uint8_t* q,
                                                    float* scales, uint8_t* qt, float* scales_t,
+                                                   void* workspace, size_t workspace_bytes,
                                                    void* stream) {
   MI355X_REQUIRE(experts > 0 && out > 0 && in > 0, "quantize_weights_current: empty weight");
   MI355X_REQUIRE(in % 8 == 0, "quantize_weights_current: in must be a multiple of 8");
   MI355X_REQUIRE(out % 16 == 0, "quantize_weights_current: out must be a multiple of 16");
+  MI355X_REQUIRE(workspace != nullptr &&
+                     workspace_bytes >= mi355x_quantize_weights_current_workspace_size(experts, out, in),
+                 "quantize_weights_current: workspace too small");
   hipStream_t s = (hipStream_t)stream;
-  const size_t ncol = (size_t)experts * in;
-  uint32_t* col_bits = (uint32_t*)scales_t;  // column maxima, then scales in place
-  const dim3 amax_grid((out + kAmaxRows - 1) / kAmaxRows, experts);
+  const int tiles = (out + kAmaxRows - 1) / kAmaxRows;
+  float* colpart = (float*)workspace;
+  const dim3 amax_grid(tiles, experts);
   const dim3 tile_grid((in + kQTile - 1) / kQTile, (out + kQTile - 1) / kQTile, experts);
-  const unsigned lin = (unsigned)((ncol + 255) / 256);
-  hipLaunchKernelGGL(fill_zero_kernel, dim3(lin), dim3(256), 0, s, col_bits, ncol);
   if (is_fp32) {
     hipLaunchKernelGGL(weight_amax_kernel<float>, amax_grid, dim3(256), 0, s, (const float*)w,
-                       out, in, interleave, scales, col_bits);
-    hipLaunchKernelGGL(weight_quantize_kernel<float>, tile_grid, dim3(256), 0, s, (const float*)w,
-                       out, in, interleave, scales, col_bits, q, qt);
+                       out, in, interleave, scales, colpart);
   } else {
     hipLaunchKernelGGL(weight_amax_kernel<uint16_t>, amax_grid, dim3(256), 0, s,
-                       (const uint16_t*)w, out, in, interleave, scales, col_bits);
-    hipLaunchKernelGGL(weight_quantize_kernel<uint16_t>, tile_grid, dim3(256), 0, s,
-                       (const uint16_t*)w, out, in, interleave, scales, col_bits, q, qt);
+                       (const uint16_t*)w, out, in, interleave, scales, colpart);
   }
-  hipLaunchKernelGGL(col_scale_kernel, dim3(lin), dim3(256), 0, s, scales_t, ncol);
+  const size_t ncol = (size_t)experts * in;
+  hipLaunchKernelGGL(col_scale_kernel, dim3((unsigned)((ncol + 255) / 256)), dim3(256), 0, s,
+                     colpart, experts, tiles, in, scales_t);
+  if (is_fp32) {
+    hipLaunchKernelGGL(weight_quantize_kernel<float>, tile_grid, dim3(256), 0, s, (const float*)w,
+                       out, in, interleave, scales, scales_t, q, qt);
+  } else {
+    hipLaunchKernelGGL(weight_quantize_kernel<uint16_t>, tile_grid, dim3(256), 0, s,
+                       (const uint16_t*)w, out, in, interleave, scales, scales_t, q, qt);
+  }
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
 }

@@ -578,9 +578,12 @@ def quantize_weights_current(w: torch.Tensor, *, interleaved: bool = False):
     transposed = torch.empty((experts, inner, out), dtype=FP8, device=device)
     scale = torch.empty((experts, out), dtype=torch.float32, device=device)
     transposed_scale = torch.empty((experts, inner), dtype=torch.float32, device=device)
+    size = _native.query("mi355x_quantize_weights_current_workspace_size", experts, out, inner)
+    workspace = torch.empty(size, dtype=torch.uint8, device=device)
     _native.call("mi355x_quantize_weights_current_fp8", _ptr(w), int(w.dtype == torch.float32),
                  experts, out, inner, int(interleaved), _ptr(data), _ptr(scale),
-                 _ptr(transposed), _ptr(transposed_scale), _stream(device))
+                 _ptr(transposed), _ptr(transposed_scale), _ptr(workspace), size,
+                 _stream(device))
     return data, transposed, scale, transposed_scale
 
 
