@@ -117,39 +117,37 @@ __global__ void __launch_bounds__(256) permute_quantize_kernel(
   for (int j = 0; j < 32; ++j)
     if (j < top_k) dest[j] = slots[(size_t)t * top_k + j];
   const uint16_t* src = x + (size_t)t * width;
-  for (int base = 0; base < width; base += 512) {
-    const int col = base + lane * 8;
-    const bool ok = col < width;
-    float v[8];
-    if (ok) {
-      uint4 raw = *(const uint4*)(src + col);
-      uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+  // The whole row's loads first (up to kRowChunks 512-column chunks), then
+  // every store: loads and stores share one completion counter, so a load
+  // issued after the previous chunk's stores would wait for them.
+  constexpr int kRowChunks = 4;
+  for (int base0 = 0; base0 < width; base0 += 512 * kRowChunks) {
+    uint4 raw[kRowChunks];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[2 * i] = bf16_to_f32(w4[i] & 0xffff);
-        v[2 * i + 1] = bf16_to_f32(w4[i] >> 16);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    for (int c = 0; c < kRowChunks; ++c) {
+      const int col = base0 + c * 512 + lane * 8;
+      raw[c] = col < width ? *(const uint4*)(src + col) : make_uint4(0, 0, 0, 0);
     }
-    float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = group_max<16>(amax);
-    const float s = fmaxf(amax * kInv448, kMinScale);
-    const float inv = 1.0f / s;
-    uint32_t lo = f32x4_to_e4m3(quant_div_inv(v[0], s, inv), quant_div_inv(v[1], s, inv),
-                                quant_div_inv(v[2], s, inv), quant_div_inv(v[3], s, inv));
-    uint32_t hi = f32x4_to_e4m3(quant_div_inv(v[4], s, inv), quant_div_inv(v[5], s, inv),
-                                quant_div_inv(v[6], s, inv), quant_div_inv(v[7], s, inv));
-    if (ok) {
-      const int kb = col >> 7;
+    for (int c = 0; c < kRowChunks; ++c) {
+      const int col = base0 + c * 512 + lane * 8;
+      if (base0 + c * 512 >= width) break;  // uniform over the wave
+      float v[8];
+      unpack_bf16x8(raw[c], v);
+      float amax = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 32; ++j) {
-        if (j < top_k) {
-          *(uint2*)(q + (size_t)dest[j] * width + col) = make_uint2(lo, hi);
-          if ((lane & 15) == 0) scales[(size_t)kb * rows + dest[j]] = s;
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+      amax = group_max<16>(amax);
+      const float s = fmaxf(amax * kInv448, kMinScale);
+      const uint2 packed = quant8(v, s);
+      if (col < width) {
+        const int kb = col >> 7;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+          if (j < top_k) {
+            *(uint2*)(q + (size_t)dest[j] * width + col) = packed;
+            if ((lane & 15) == 0) scales[(size_t)kb * rows + dest[j]] = s;
+          }
         }
       }
     }

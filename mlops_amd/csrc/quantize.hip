@@ -119,62 +119,79 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __re
   const int r = blockIdx.x * 4 + wave;
   if (r >= rows) return;
   const uint16_t* src = x + (size_t)r * pitch;
+  // Up to four 512-column chunks' loads are issued before any of their
+  // stores: loads and stores share one completion counter, so a load issued
+  // after a store would wait for it.
+  constexpr int kChunks = 4;
   if (!gate_up) {
-    for (int base = 0; base < width; base += 512) {
-      const int col = base + lane * 8;
-      const bool ok = col < width;
-      float v[8];
-      if (ok) load_bf16x8(src + col, v);
-      else
+    for (int base0 = 0; base0 < width; base0 += 512 * kChunks) {
+      uint4 raw[kChunks];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-      float amax = 0.0f;
+      for (int c = 0; c < kChunks; ++c) {
+        const int col = base0 + c * 512 + lane * 8;
+        raw[c] = col < width ? *(const uint4*)(src + col) : make_uint4(0, 0, 0, 0);
+      }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-      amax = group_max<16>(amax);
-      const float s = fmaxf(amax * kInv448, kMinScale);
-      uint2 packed = quant8(v, s);
-      if (ok) {
-        *(uint2*)(q + (size_t)r * width + col) = packed;
-        if ((lane & 15) == 0) scales[(size_t)(col >> 7) * rows + r] = s;
+      for (int c = 0; c < kChunks; ++c) {
+        if (base0 + c * 512 >= width) break;  // uniform over the wave
+        const int col = base0 + c * 512 + lane * 8;
+        float v[8];
+        unpack_bf16x8(raw[c], v);
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        amax = group_max<16>(amax);
+        const float s = fmaxf(amax * kInv448, kMinScale);
+        const uint2 packed = quant8(v, s);
+        if (col < width) {
+          *(uint2*)(q + (size_t)r * width + col) = packed;
+          if ((lane & 15) == 0) scales[(size_t)(col >> 7) * rows + r] = s;
+        }
       }
     }
     return;
   }
   const int half = width / 2;
-  for (int base = 0; base < half; base += 512) {
-    const int j = base + lane * 8;  // gate/up pair index
-    const bool ok = j < half;
-    float g[8], u[8];
-    if (ok) {
-      float a[8], b[8];
-      load_bf16x8(src + 2 * j, a);
-      load_bf16x8(src + 2 * j + 8, b);
+  for (int base0 = 0; base0 < half; base0 += 512 * kChunks) {
+    uint4 ra[kChunks], rb[kChunks];
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      const int j = base0 + c * 512 + lane * 8;  // gate/up pair index
+      ra[c] = rb[c] = make_uint4(0, 0, 0, 0);
+      if (j < half) {
+        ra[c] = *(const uint4*)(src + 2 * j);
+        rb[c] = *(const uint4*)(src + 2 * j + 8);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      if (base0 + c * 512 >= half) break;  // uniform over the wave
+      const int j = base0 + c * 512 + lane * 8;
+      float a[8], b[8], g[8], u[8];
+      unpack_bf16x8(ra[c], a);
+      unpack_bf16x8(rb[c], b);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         g[i] = a[2 * i]; u[i] = a[2 * i + 1];
         g[4 + i] = b[2 * i]; u[4 + i] = b[2 * i + 1];
       }
-    } else {
+      float ga = 0.0f, ua = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) g[i] = u[i] = 0.0f;
-    }
-    float ga = 0.0f, ua = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      ga = fmaxf(ga, fabsf(g[i]));
-      ua = fmaxf(ua, fabsf(u[i]));
-    }
-    ga = group_max<16>(ga);
-    ua = group_max<16>(ua);
-    const float sg = fmaxf(ga * kInv448, kMinScale), su = fmaxf(ua * kInv448, kMinScale);
-    uint2 pg = quant8(g, sg), pu = quant8(u, su);
-    if (ok) {
-      *(uint2*)(q + (size_t)r * width + j) = pg;
-      *(uint2*)(q + (size_t)r * width + half + j) = pu;
-      if ((lane & 15) == 0) {
-        scales[(size_t)(j >> 7) * rows + r] = sg;
-        scales[(size_t)((half + j) >> 7) * rows + r] = su;
+      for (int i = 0; i < 8; ++i) {
+        ga = fmaxf(ga, fabsf(g[i]));
+        ua = fmaxf(ua, fabsf(u[i]));
+      }
+      ga = group_max<16>(ga);
+      ua = group_max<16>(ua);
+      const float sg = fmaxf(ga * kInv448, kMinScale), su = fmaxf(ua * kInv448, kMinScale);
+      const uint2 pg = quant8(g, sg), pu = quant8(u, su);
+      if (j < half) {
+        *(uint2*)(q + (size_t)r * width + j) = pg;
+        *(uint2*)(q + (size_t)r * width + half + j) = pu;
+        if ((lane & 15) == 0) {
+          scales[(size_t)(j >> 7) * rows + r] = sg;
+          scales[(size_t)((half + j) >> 7) * rows + r] = su;
+        }
       }
     }
   }
@@ -379,50 +396,68 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
   // products, summed over each 128-column block's 16 lanes, and the block
   // sums added in block order, so both kernels give the same dscore.
   float dsum = 0.0f;
-  for (int base = 0; base < width; base += 512) {
-    const int j = base + lane * 8;
-    float dot = 0.0f;
-    if (j < width) {
-      float a[8], b[8], r[8];
-      load_bf16x8(hr + 2 * j, a);
-      load_bf16x8(hr + 2 * j + 8, b);
-      load_bf16x8(rr + j, r);
-      float dg[8], du[8], ap[8];
+  // Two 512-column chunks' loads are issued before either's stores (loads
+  // and stores share one completion counter).
+  for (int base0 = 0; base0 < width; base0 += 1024) {
+    uint4 hv0[2], hv1[2], rv[2];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float rg = i < 4 ? a[2 * i] : b[2 * (i - 4)];
-        const float ru = i < 4 ? a[2 * i + 1] : b[2 * (i - 4) + 1];
-        float gv = rg, uv = ru;
-        clamp_gate_up(gv, uv, limit);
-        const float sig = sigmoid_f(gv);
-        const float silu = gv * sig;
-        const float act = silu * uv;
-        dot += r[i] * act;
-        const float gg = r[i] * score;
-        float dgate = gg * uv * (sig + silu * (1.0f - sig));
-        float dup = gg * silu;
-        if (limit > 0.0f) {
-          dgate = rg <= limit ? dgate : 0.0f;
-          dup = (ru >= -limit && ru <= limit) ? dup : 0.0f;
-        }
-        dg[i] = dgate;
-        du[i] = dup;
-        ap[i] = act * score;
+    for (int c = 0; c < 2; ++c) {
+      const int j = base0 + c * 512 + lane * 8;
+      hv0[c] = hv1[c] = rv[c] = make_uint4(0, 0, 0, 0);
+      if (j < width) {
+        hv0[c] = *(const uint4*)(hr + 2 * j);
+        hv1[c] = *(const uint4*)(hr + 2 * j + 8);
+        rv[c] = *(const uint4*)(rr + j);
       }
-      uint4 o0, o1, o2;
-      o0.x = pack_bf16x2(dg[0], du[0]); o0.y = pack_bf16x2(dg[1], du[1]);
-      o0.z = pack_bf16x2(dg[2], du[2]); o0.w = pack_bf16x2(dg[3], du[3]);
-      o1.x = pack_bf16x2(dg[4], du[4]); o1.y = pack_bf16x2(dg[5], du[5]);
-      o1.z = pack_bf16x2(dg[6], du[6]); o1.w = pack_bf16x2(dg[7], du[7]);
-      o2.x = pack_bf16x2(ap[0], ap[1]); o2.y = pack_bf16x2(ap[2], ap[3]);
-      o2.z = pack_bf16x2(ap[4], ap[5]); o2.w = pack_bf16x2(ap[6], ap[7]);
-      *(uint4*)(dh + (size_t)row * 2 * width + 2 * j) = o0;
-      *(uint4*)(dh + (size_t)row * 2 * width + 2 * j + 8) = o1;
-      *(uint4*)(a_prime + (size_t)row * width + j) = o2;
     }
-    dot = group_sum<16>(dot);
-    const int blocks = min(4, (width - base + 127) / 128);  // 128-column blocks here
-    for (int q = 0; q < blocks; ++q) dsum += __shfl(dot, 16 * q, 64);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int base = base0 + c * 512;
+      if (base >= width) break;  // uniform over the wave
+      const int j = base + lane * 8;
+      float dot = 0.0f;
+      if (j < width) {
+        float a[8], b[8], r[8];
+        unpack_bf16x8(hv0[c], a);
+        unpack_bf16x8(hv1[c], b);
+        unpack_bf16x8(rv[c], r);
+        float dg[8], du[8], ap[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float rg = i < 4 ? a[2 * i] : b[2 * (i - 4)];
+          const float ru = i < 4 ? a[2 * i + 1] : b[2 * (i - 4) + 1];
+          float gv = rg, uv = ru;
+          clamp_gate_up(gv, uv, limit);
+          const float sig = sigmoid_f(gv);
+          const float silu = gv * sig;
+          const float act = silu * uv;
+          dot += r[i] * act;
+          const float gg = r[i] * score;
+          float dgate = gg * uv * (sig + silu * (1.0f - sig));
+          float dup = gg * silu;
+          if (limit > 0.0f) {
+            dgate = rg <= limit ? dgate : 0.0f;
+            dup = (ru >= -limit && ru <= limit) ? dup : 0.0f;
+          }
+          dg[i] = dgate;
+          du[i] = dup;
+          ap[i] = act * score;
+        }
+        uint4 o0, o1, o2;
+        o0.x = pack_bf16x2(dg[0], du[0]); o0.y = pack_bf16x2(dg[1], du[1]);
+        o0.z = pack_bf16x2(dg[2], du[2]); o0.w = pack_bf16x2(dg[3], du[3]);
+        o1.x = pack_bf16x2(dg[4], du[4]); o1.y = pack_bf16x2(dg[5], du[5]);
+        o1.z = pack_bf16x2(dg[6], du[6]); o1.w = pack_bf16x2(dg[7], du[7]);
+        o2.x = pack_bf16x2(ap[0], ap[1]); o2.y = pack_bf16x2(ap[2], ap[3]);
+        o2.z = pack_bf16x2(ap[4], ap[5]); o2.w = pack_bf16x2(ap[6], ap[7]);
+        *(uint4*)(dh + (size_t)row * 2 * width + 2 * j) = o0;
+        *(uint4*)(dh + (size_t)row * 2 * width + 2 * j + 8) = o1;
+        *(uint4*)(a_prime + (size_t)row * width + j) = o2;
+      }
+      dot = group_sum<16>(dot);
+      const int blocks = min(4, (width - base + 127) / 128);  // 128-column blocks here
+      for (int q = 0; q < blocks; ++q) dsum += __shfl(dot, 16 * q, 64);
+    }
   }
   if (lane == 0) dscore[row] = dsum;
 }
