@@ -117,36 +117,44 @@ __global__ void __launch_bounds__(256) permute_quantize_kernel(
   for (int j = 0; j < 32; ++j)
     if (j < top_k) dest[j] = slots[(size_t)t * top_k + j];
   const uint16_t* src = x + (size_t)t * width;
-  // The whole row's loads first (up to kRowChunks 512-column chunks), then
-  // every store: loads and stores share one completion counter, so a load
-  // issued after the previous chunk's stores would wait for them.
-  constexpr int kRowChunks = 4;
-  for (int base0 = 0; base0 < width; base0 += 512 * kRowChunks) {
-    uint4 raw[kRowChunks];
+  // 16 columns per lane (a 128-column scale group is 8 lanes), so each
+  // destination row gets one 16-byte store per lane: a wave writes 1 KB of
+  // whole lines per store. The row's loads (up to 2 chunks of 1024 columns)
+  // are issued before any store: loads and stores share one completion
+  // counter, so a load issued after a store would wait for it.
+  constexpr int kRowChunks = 2;
+  for (int base0 = 0; base0 < width; base0 += 1024 * kRowChunks) {
+    uint4 raw[kRowChunks][2];
 #pragma unroll
     for (int c = 0; c < kRowChunks; ++c) {
-      const int col = base0 + c * 512 + lane * 8;
-      raw[c] = col < width ? *(const uint4*)(src + col) : make_uint4(0, 0, 0, 0);
+      const int col = base0 + c * 1024 + lane * 16;
+      raw[c][0] = raw[c][1] = make_uint4(0, 0, 0, 0);
+      if (col < width) {
+        raw[c][0] = *(const uint4*)(src + col);
+        raw[c][1] = *(const uint4*)(src + col + 8);
+      }
     }
 #pragma unroll
     for (int c = 0; c < kRowChunks; ++c) {
-      const int col = base0 + c * 512 + lane * 8;
-      if (base0 + c * 512 >= width) break;  // uniform over the wave
-      float v[8];
-      unpack_bf16x8(raw[c], v);
+      const int col = base0 + c * 1024 + lane * 16;
+      if (base0 + c * 1024 >= width) break;  // uniform over the wave
+      float v[16];
+      unpack_bf16x8(raw[c][0], v);
+      unpack_bf16x8(raw[c][1], v + 8);
       float amax = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-      amax = group_max<16>(amax);
+      for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+      amax = group_max<8>(amax);
       const float s = fmaxf(amax * kInv448, kMinScale);
-      const uint2 packed = quant8(v, s);
+      const uint2 lo = quant8(v, s), hi = quant8(v + 8, s);
+      const uint4 packed = make_uint4(lo.x, lo.y, hi.x, hi.y);
       if (col < width) {
         const int kb = col >> 7;
 #pragma unroll
         for (int j = 0; j < 32; ++j) {
           if (j < top_k) {
-            *(uint2*)(q + (size_t)dest[j] * width + col) = packed;
-            if ((lane & 15) == 0) scales[(size_t)kb * rows + dest[j]] = s;
+            *(uint4*)(q + (size_t)dest[j] * width + col) = packed;
+            if ((lane & 7) == 0) scales[(size_t)kb * rows + dest[j]] = s;
           }
         }
       }
