@@ -16,7 +16,13 @@ with the row and transposing quantizers. Those produce, byte for byte, what
 the fused pass does, so every output and gradient equals the fused
 operator's.
 
-The fused operator stays the default (``PRIORITY`` below it); this one is
+It serves both FP8 precisions, as the reference's composed form does:
+block-FP8 weights run the kernels of ``mi355x.moe.block_fp8``, and
+``fp8_current`` weights (per-row scales, `RowFP8Weight`) those of
+``mi355x.moe.fp8_current``. Either way the results equal that fused
+operator's.
+
+The fused operators stay the default (``PRIORITY`` below theirs); this one is
 selected by its implementation ID.
 """
 
@@ -31,24 +37,68 @@ from ...dispatch.context import weight_gradient_dtype
 from ...dispatch.costs import flop_formula
 from ...dispatch.registry import Implementation, SupportResult, register_implementation
 from ...routing import current_route_weight_precision, next_override
+from ...row_fp8 import RowFP8Weight
 from . import moe as fused
+from . import moe_current as current
 
 IMPLEMENTATION_ID = "mi355x.moe.composed"
 PRIORITY = 115  # below mi355x.moe.block_fp8 (120), which is faster
 
 
-def _supports(*args, surface, **kwargs) -> SupportResult:
+def _is_current(compute_precision, w13, w2) -> bool:
+    return compute_precision == "fp8_current" or (
+        compute_precision is None and any(isinstance(w, RowFP8Weight) for w in (w13, w2)))
+
+
+def _supports(h2, residual, router_weight, w13_experts, w2_experts, *, surface, **kwargs):
+    """The fused operator's rules at the requested precision (fp8_block, or
+    fp8_current, as the reference's composed form serves both)."""
     if surface == "explicit":
         return SupportResult.no("trace-visible MoE composition is a semantic-only implementation")
-    return fused.supports(*args, surface=surface, **kwargs)
+    rules = current if _is_current(kwargs.get("compute_precision"), w13_experts, w2_experts) else fused
+    return rules.supports(h2, residual, router_weight, w13_experts, w2_experts, surface=surface,
+                          **kwargs)
+
+
+class _Weight(tuple):
+    """A weight's operands: ``(data, scale[, data_t])`` for 128x128 blocks, or
+    ``(data, transposed, scale, transposed_scale)`` per row (``current``)."""
+
+    current = False
 
 
 def _weight(data, components):
-    """``(data, scale[, data_t])`` from the unwrapped data and its components."""
-    if len(components) not in (1, 2):
-        raise ValueError("a composed region takes its weight's scale (and optionally its "
-                         "transposed data) as components")
-    return (data, *components)
+    """The operands from the unwrapped data and its components: one or two
+    (the block scale, then optionally the transposed data) for block-FP8,
+    three (transposed data, scale, transposed scale) for fp8_current."""
+    if len(components) in (1, 2):
+        return _Weight((data, *components))
+    if len(components) == 3:
+        weight = _Weight((data, *components))
+        weight.current = True
+        return weight
+    raise ValueError("a composed region takes its weight's scale (and optionally its transposed "
+                     "data), or the three per-row components, as components")
+
+
+def _rows(x, slots, weight):
+    """The routed copies of token rows quantized for ``weight``'s GEMMs."""
+    return (kernels.permute_quantize_current(x, slots) if getattr(weight, "current", False)
+            else kernels.permute_quantize(x, slots))
+
+
+def _forward_gemm(aq, as_, weight, offsets, *, interleave=False):
+    if getattr(weight, "current", False):
+        return kernels.gemm_rowwise(aq, as_, weight[0], weight[2], offsets)
+    return kernels.gemm(aq, as_, weight[0], weight[1], offsets, interleave=interleave)
+
+
+def _input_gradient_gemm(aq, as_, weight, offsets):
+    """``rows @ W`` through the weight's transposed copy."""
+    if getattr(weight, "current", False):
+        return kernels.gemm_rowwise(aq, as_, weight[1], weight[3], offsets)
+    return kernels.gemm(aq, as_, fused._transposed(weight, weight[0]), weight[1], offsets,
+                        transposed_scale=True)
 
 
 def _grad_dtypes(weight_grad_dtype, router_weight=None):
@@ -81,8 +131,10 @@ def prepare_forward(h2, router_weight, w13, *, top_k, routing_mode, router_bias=
             topk_group=int(topk_group), routed_scaling=float(routed_scaling), forced_ids=forced,
         )
         counts, offsets, order, slots = kernels.permute_plan(ids, experts)
-        xq, xs = kernels.permute_quantize(x, slots)
-        h13 = kernels.gemm(xq, xs, w13[0], w13[1], offsets, interleave=True)
+        xq, xs = _rows(x, slots, w13)
+        # Block-FP8 w13 is stored gate rows then up rows and the GEMM
+        # interleaves its output; an fp8_current w13 is stored interleaved.
+        h13 = _forward_gemm(xq, xs, w13, offsets, interleave=True)
         aux, probability_sum, _, _ = kernels.router_stats(logits, ids, int(top_k), routing_mode,
                                                           lengths)
     return aux, counts, probability_sum, logits, weights, ids, order, offsets, slots, h13
@@ -93,8 +145,11 @@ def finish_forward(h13, w2, route_weights, offsets, slots, residual, *, swiglu_l
     width = residual.shape[-1]
     with torch.no_grad():
         base = residual.reshape(-1, width).contiguous()
-        aq, as_ = kernels.swiglu_quantize(h13, swiglu_limit)
-        y = kernels.gemm(aq, as_, w2[0], w2[1], offsets)
+        if getattr(w2, "current", False):
+            aq, as_ = kernels.swiglu_quantize_rows_current(h13, swiglu_limit)
+        else:
+            aq, as_ = kernels.swiglu_quantize(h13, swiglu_limit)
+        y = _forward_gemm(aq, as_, w2, offsets)
         return kernels.combine(y, slots, route_weights, base).reshape(residual.shape)
 
 
@@ -113,9 +168,8 @@ def finish_backward(grad_output, h13, w2, route_weights, order, offsets, slots, 
         dy = grad_output.reshape(-1, width).contiguous()
         if dy.dtype != torch.bfloat16:
             dy = dy.to(torch.bfloat16)
-        dyq, dys = kernels.permute_quantize(dy, slots)
-        r = kernels.gemm(dyq, dys, fused._transposed(w2, w2[0]), w2[1], offsets,
-                         transposed_scale=True)
+        dyq, dys = _rows(dy, slots, w2)
+        r = _input_gradient_gemm(dyq, dys, w2, offsets)
         grad_h13, a_prime, dscore = kernels.routed_swiglu_backward(
             r, h13, route_weights.reshape(-1), order, swiglu_limit, dh_out=grad_h13_out)
         grad_route_weights = dscore[slots.reshape(-1).long()].view(route_weights.shape)
@@ -153,9 +207,12 @@ def prepare_backward(grad_aux, grad_probability_sum, grad_route_weights, grad_h1
         if grad_h13.dtype != torch.bfloat16:
             grad_h13 = grad_h13.to(torch.bfloat16)
         grad_h13 = grad_h13.contiguous()
-        dhq, dhs = kernels.quantize_rows(grad_h13, gate_up=True)
-        dx = kernels.gemm(dhq, dhs, fused._transposed(w13, w13[0]), w13[1], offsets,
-                          transposed_scale=True)
+        if getattr(w13, "current", False):
+            # The interleaved K order of the transposed w13 copy is h13's.
+            dhq, dhs = kernels.quantize_rows_current(grad_h13)
+        else:
+            dhq, dhs = kernels.quantize_rows(grad_h13, gate_up=True)
+        dx = _input_gradient_gemm(dhq, dhs, w13, offsets)
         if need_w13:
             padded = kernels.wgrad_padded_rows(assignments, experts)
             blocks = kernels.padded_row_blocks(offsets, padded)
@@ -382,6 +439,9 @@ def _container_rule(cls, func, types, args, kwargs):
                           else getattr(value, "_transposed", None))
             if transposed is not None:
                 components.append(transposed)
+        elif isinstance(value, RowFP8Weight):
+            args[index] = value._data
+            components.extend((value._transposed, value._scale, value._transposed_scale))
     args[slot] = components
     return func(*args)
 
@@ -389,6 +449,7 @@ def _container_rule(cls, func, types, args, kwargs):
 for _op in (_prepare_op, _prepare_backward_op, _finish_op, _finish_backward_op,
             _finish_backward_donate_h13_op):
     _op.register_torch_dispatch(BlockFP8Weight, _container_rule)
+    _op.register_torch_dispatch(RowFP8Weight, _container_rule)
 
 
 def _prepare_context(ctx, inputs, output):
@@ -468,10 +529,11 @@ def apply(
 ):
     """``(out, aux, counts, probability_sum)`` through the two regions (reference
     ``sonicmoe/moe_composed.py:751-834``)."""
-    _, refusal = fused._precision(compute_precision, w13_experts, w2_experts)
+    rules = current if _is_current(compute_precision, w13_experts, w2_experts) else fused
+    _, refusal = rules._precision(compute_precision, w13_experts, w2_experts)
     if refusal is not None:
         raise ValueError(refusal)
-    w13, w2 = fused._containers(w13_experts, w2_experts)
+    w13, w2 = rules._containers(w13_experts, w2_experts)
     rows = h2.numel() // h2.shape[-1]
     normalized = (rows,) if lengths is None else tuple(int(x) for x in lengths)
     bias = (torch.empty(0, dtype=torch.float32, device=h2.device) if router_bias is None

@@ -174,3 +174,31 @@ def test_opcheck_composed_ops(device):
               "topk_then_softmax", [rows], None, [w13s], True, True)
     torch.library.opcheck(ops.moe_mi355x_prepare_bwd.default, prep_b,
                           test_utils=("test_faketensor",))
+
+
+@pytest.mark.parametrize("containers", [True, False])
+def test_composed_fp8_current_equals_the_fused_operator(device, containers):
+    """The composed form at fp8_current (RowFP8Weight containers, or bf16
+    masters quantized per call) equals mi355x.moe.fp8_current bitwise."""
+    from mlops_amd import RowFP8Weight
+
+    x, res, wr, w13, w2, dy = _inputs(device, seed=12)
+    results = []
+    for implementation in ("mi355x.moe.fp8_current", COMPOSED):
+        xv = x.clone().requires_grad_(True)
+        wrv = wr.clone().requires_grad_(True)
+        if containers:
+            a = RowFP8Weight.quantize(w13, interleaved=True).detach().requires_grad_(True)
+            b = RowFP8Weight.quantize(w2).detach().requires_grad_(True)
+            kw = {}
+        else:
+            a, b = w13.clone().requires_grad_(True), w2.clone().requires_grad_(True)
+            kw = dict(compute_precision="fp8_current")
+        with use_implementation("moe", implementation):
+            out, aux, counts, psum = mlops_amd.moe(xv, res, wrv, a, b, top_k=2,
+                                                   routing_mode="softmax_then_topk",
+                                                   swiglu_limit=3.0, **kw)
+        torch.autograd.backward([out, aux], [dy, torch.ones_like(aux) * 0.1])
+        results.append(dict(out=out.detach(), aux=aux.detach(), counts=counts, gx=xv.grad,
+                            gr=wrv.grad, g13=a.grad, g2=b.grad))
+    _assert_equal(*results)
