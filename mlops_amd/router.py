@@ -55,20 +55,24 @@ def router_weight_gradient(grad_logits, hidden, dtype) -> torch.Tensor:
         return (grad_logits.float().t() @ hidden.float()).to(dtype)
     rows = hidden.to(operands)
     tokens, experts = grad_logits.shape
-    high = grad_logits.to(operands)
-    residue = (grad_logits.float() - high.float()).to(operands)
-    # Both pieces in one product, stacked along its output rows
-    # ([hi | mid]^T @ rows, M = 2E), split over the token (K) dimension into
-    # SPLIT_K batched products whose fp32 partials are summed: K = T is long
-    # and M x N small, and hipBLASLt runs the split form ~2x faster on MI355X.
-    pieces = torch.stack([high, residue]).transpose(1, 2).reshape(2 * experts, tokens)
+    # Both pieces side by side in one token-major buffer [T, 2E] (hi in the
+    # first E columns, mid in the last), so one product [hi | mid]^T @ rows
+    # (M = 2E) gives both, and each operand is a transposed view of a
+    # contiguous block (no transposing copy). The product is split over the
+    # token (K) dimension into SPLIT_K batched products whose fp32 partials
+    # are summed: K = T is long and M x N small, and hipBLASLt runs the split
+    # form ~2x faster on MI355X.
+    pieces = torch.empty((tokens, 2 * experts), dtype=operands, device=grad_logits.device)
+    high = pieces[:, :experts]
+    high.copy_(grad_logits)
+    torch.sub(grad_logits, high.float(), out=pieces[:, experts:])
     split = SPLIT_K if tokens % SPLIT_K == 0 and tokens >= SPLIT_K * 512 else 1
     if split > 1 and rows.is_cuda:
         chunk = tokens // split
-        both = torch.bmm(pieces.view(2 * experts, split, chunk).transpose(0, 1),
+        both = torch.bmm(pieces.view(split, chunk, 2 * experts).transpose(1, 2),
                          rows.view(split, chunk, rows.shape[1]), out_dtype=torch.float32).sum(0)
     else:
-        both = _product_fp32(pieces, rows)
+        both = _product_fp32(pieces.t(), rows)
     gradient = both[:experts].add_(both[experts:])
     return gradient.to(dtype)
 
