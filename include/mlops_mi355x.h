@@ -250,6 +250,18 @@ int mi355x_gemm_fp8_rowwise(const uint8_t* a, const float* a_scale, int rows, co
                             const float* w_scale, int experts, int n, int k,
                             const int32_t* offsets, void* out, void* stream);
 
+/* mi355x_gemm_fp8_rowwise with a rank-r term: out[r, n] = (row-scaled product)
+ * + sum_j lora_z[r, j] lora_b[e][n, j], the rank term a bf16 MFMA that starts
+ * the accumulators (divided by the row and column descales the epilogue
+ * applies). lora_z bf16 [rows, R], lora_b bf16 [E, N, R] in the weight's
+ * stored row order, R a multiple of 16 in [16, 256]. Replaces the LoRA C
+ * input of the fp8_current expert-LoRA GEMMs (providers/sonicmoe/lora.py
+ * :189-262, :540-600 through fp8.py's scale-aware epilogues). */
+int mi355x_gemm_fp8_rowwise_lora(const uint8_t* a, const float* a_scale, int rows,
+                                 const uint8_t* w, const float* w_scale, int experts, int n, int k,
+                                 const int32_t* offsets, const void* lora_z, const void* lora_b,
+                                 int lora_rank, void* out, void* stream);
+
 /* Per-row e4m3 quantizer: q[r] = e4m3(clip(x[src] / s, +-448)), scales[r] =
  * s = max(amax(x[src]) * (1/448), 1e-12), src = gather[r] / gather_div (a
  * routed row's token) or r. x bf16 rows of the given pitch. Replaces
@@ -271,10 +283,11 @@ int mi355x_permute_quantize_current_fp8(const void* x, int tokens, int width, in
 
 /* SwiGLU of interleaved h [rows, 2I] (gate from above and up on both sides
  * clamped at limit when limit > 0), quantized per row as above: q [rows, I],
- * scales [rows]. Replaces swiglu_quantize_rows_fp8
+ * scales [rows]; act (bf16 [rows, I]) receives the activation too when not
+ * null. Replaces swiglu_quantize_rows_fp8
  * (kernels/quack_moe/swiglu_rows.py:246-276). */
 int mi355x_swiglu_quantize_rows_current_fp8(const void* h, int rows, int width, float limit,
-                                            uint8_t* q, float* scales, void* stream);
+                                            uint8_t* q, float* scales, void* act, void* stream);
 
 /* Both orientations of expert weights w [E, out, in] (bf16, or fp32 when
  * is_fp32): q [E, out, in] with scales [E, out] (per row), qt [E, in, out]

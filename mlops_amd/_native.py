@@ -68,7 +68,9 @@ SIGNATURES = {
     "mi355x_gemm_fp8_rowwise": (_I, [_P, _P, _I, _P, _P, _I, _I, _I, _P, _P, _P]),
     "mi355x_quantize_rows_current_fp8": (_I, [_P, _I, _I, _I64, _P, _I, _P, _P, _P]),
     "mi355x_permute_quantize_current_fp8": (_I, [_P, _I, _I, _I, _P, _P, _P, _P]),
-    "mi355x_swiglu_quantize_rows_current_fp8": (_I, [_P, _I, _I, _F, _P, _P, _P]),
+    "mi355x_swiglu_quantize_rows_current_fp8": (_I, [_P, _I, _I, _F, _P, _P, _P, _P]),
+    "mi355x_gemm_fp8_rowwise_lora": (_I, [_P, _P, _I, _P, _P, _I, _I, _I, _P, _P, _P, _I, _P,
+                                          _P]),
     "mi355x_quantize_weights_current_fp8": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _S,
                                                  _P]),
     "mi355x_quantize_weights_current_workspace_size": (_S, [_I, _I, _I]),

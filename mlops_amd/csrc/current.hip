@@ -118,7 +118,7 @@ __device__ __forceinline__ void swiglu8(const uint16_t* p, float limit, float* a
 
 __global__ void __launch_bounds__(256) swiglu_rows_current_kernel(
     const uint16_t* __restrict__ h, int rows, int width, float limit, uint8_t* __restrict__ q,
-    float* __restrict__ scales) {
+    float* __restrict__ scales, uint16_t* __restrict__ act_out) {
   const int wave = threadIdx.x >> 6, lane = lane_id();
   const int r = blockIdx.x * 4 + wave;
   if (r >= rows) return;
@@ -137,6 +137,10 @@ __global__ void __launch_bounds__(256) swiglu_rows_current_kernel(
     float act[8];
     swiglu8(src + 2 * j, limit, act);
     *(uint2*)(dst + j) = quant8(act, s);
+    if (act_out != nullptr)  // the bf16 activation too (expert LoRA's down-projection rank term)
+      *(uint4*)(act_out + (size_t)r * width + j) =
+          make_uint4(pack_bf16x2(act[0], act[1]), pack_bf16x2(act[2], act[3]),
+                     pack_bf16x2(act[4], act[5]), pack_bf16x2(act[6], act[7]));
   }
   if (lane == 0) scales[r] = s;
 }
@@ -321,13 +325,14 @@ extern "C" int mi355x_quantize_rows_current_fp8(const void* x, int rows, int wid
 
 extern "C" int mi355x_swiglu_quantize_rows_current_fp8(const void* h, int rows, int width,
                                                        float limit, uint8_t* q, float* scales,
-                                                       void* stream) {
+                                                       void* act, void* stream) {
   MI355X_REQUIRE(width > 0 && width % 8 == 0,
                  "swiglu_quantize_rows_current: I must be a multiple of 8");
   MI355X_REQUIRE(rows >= 0, "swiglu_quantize_rows_current: negative rows");
   if (rows == 0) return MI355X_OK;
   hipLaunchKernelGGL(swiglu_rows_current_kernel, dim3((rows + 3) / 4), dim3(256), 0,
-                     (hipStream_t)stream, (const uint16_t*)h, rows, width, limit, q, scales);
+                     (hipStream_t)stream, (const uint16_t*)h, rows, width, limit, q, scales,
+                     (uint16_t*)act);
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
 }

@@ -406,7 +406,8 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
 
 int mi355x_gemm_v2_rowwise_launch(const uint8_t* a, const float* a_scale, int rows,
                                   const uint8_t* w, const float* w_scale, int experts, int n,
-                                  int k, const int32_t* offsets, void* out, void* stream);
+                                  int k, const int32_t* offsets, const void* lora_z,
+                                  const void* lora_b, int lora_rank, void* out, void* stream);
 
 int mi355x_wgrad_v2_launch(const uint8_t* p, const float* p_scale, int m_features,
                            const uint8_t* q, const float* q_scale, int n_features, int padded,
@@ -448,9 +449,32 @@ extern "C" int mi355x_gemm_fp8_rowwise(const uint8_t* a, const float* a_scale, i
   MI355X_REQUIRE(rows >= 0, "gemm_rowwise: negative rows");
   if (rows == 0) return MI355X_OK;
   const int v2 = mi355x_gemm_v2_rowwise_launch(a, a_scale, rows, w, w_scale, experts, n, k,
-                                               offsets, out, stream);
+                                               offsets, nullptr, nullptr, 0, out, stream);
   if (v2 < 0) return v2;
   MI355X_REQUIRE(v2 == 0, "gemm_rowwise: shape outside the pipelined kernel");
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_gemm_fp8_rowwise_lora(const uint8_t* a, const float* a_scale, int rows,
+                                            const uint8_t* w, const float* w_scale, int experts,
+                                            int n, int k, const int32_t* offsets,
+                                            const void* lora_z, const void* lora_b, int lora_rank,
+                                            void* out, void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= kMaxExperts,
+                 "gemm_rowwise_lora: experts must be in [1, %d]", kMaxExperts);
+  MI355X_REQUIRE(n > 0 && n % 256 == 0, "gemm_rowwise_lora: N must be a multiple of 256, got %d",
+                 n);
+  MI355X_REQUIRE(k > 0 && k % BK == 0, "gemm_rowwise_lora: K must be a multiple of %d", BK);
+  MI355X_REQUIRE(lora_rank >= 16 && lora_rank <= 256 && lora_rank % 16 == 0,
+                 "gemm_rowwise_lora: rank must be a multiple of 16 in [16, 256], got %d",
+                 lora_rank);
+  MI355X_REQUIRE(lora_z != nullptr && lora_b != nullptr, "gemm_rowwise_lora: z and b are required");
+  MI355X_REQUIRE(rows >= 0, "gemm_rowwise_lora: negative rows");
+  if (rows == 0) return MI355X_OK;
+  const int v2 = mi355x_gemm_v2_rowwise_launch(a, a_scale, rows, w, w_scale, experts, n, k,
+                                               offsets, lora_z, lora_b, lora_rank, out, stream);
+  if (v2 < 0) return v2;
+  MI355X_REQUIRE(v2 == 0, "gemm_rowwise_lora: shape outside the pipelined kernel");
   return MI355X_OK;
 }
 

@@ -167,6 +167,25 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
             acc[i][jb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(zf[i], bf, acc[i][jb], 0, 0, 0);
         }
       }
+      if constexpr (kRow) {
+        // The epilogue multiplies the whole accumulator by the row and column
+        // descales: the rank term enters divided by them, so it comes out as
+        // itself (a few fp32 roundings). Block jb of a lane is output column
+        // zl * 8 + jb of the wave's 128, as in the epilogue.
+        const float* wsb = w_scale + (size_t)ct.e * N + ct.nt * BN + wn * 128 + zl * 8;
+        const float4 w0 = *(const float4*)wsb, w1 = *(const float4*)(wsb + 4);
+        const float iw[8] = {1.0f / w0.x, 1.0f / w0.y, 1.0f / w0.z, 1.0f / w0.w,
+                             1.0f / w1.x, 1.0f / w1.y, 1.0f / w1.z, 1.0f / w1.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = min(ct.row0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r, rows - 1);
+            const float ixs = 1.0f / a_scale[row];
+#pragma unroll
+            for (int jb = 0; jb < 8; ++jb) acc[i][jb][r] = (acc[i][jb][r] * ixs) * iw[jb];
+          }
+      }
     }
 
     for (int kb = 0; kb < nk; ++kb) {
@@ -422,15 +441,19 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
 // the shape is not this kernel's (N % 256 != 0).
 int mi355x_gemm_v2_rowwise_launch(const uint8_t* a, const float* a_scale, int rows,
                                   const uint8_t* w, const float* w_scale, int experts, int n,
-                                  int k, const int32_t* offsets, void* out, void* stream) {
+                                  int k, const int32_t* offsets, const void* lora_z,
+                                  const void* lora_b, int lora_rank, void* out, void* stream) {
   if (n % BN != 0 || experts > kMaxExperts) return 1;
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   const int grid = upper < cu_count() ? upper : cu_count();
-  hipLaunchKernelGGL((grouped_gemm_v2_kernel<false, false, false, true>), dim3(grid),
-                     dim3(kThreads), 0, (hipStream_t)stream, a, a_scale, rows, w, w_scale, 0,
-                     experts, n, k, offsets, 0, (const uint16_t*)nullptr, (uint16_t*)out,
-                     (uint8_t*)nullptr, (float*)nullptr, 0.0f, (const uint16_t*)nullptr,
-                     (const uint16_t*)nullptr, 0);
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream, a, a_scale,
+                       rows, w, w_scale, 0, experts, n, k, offsets, 0, (const uint16_t*)nullptr,
+                       (uint16_t*)out, (uint8_t*)nullptr, (float*)nullptr, 0.0f,
+                       (const uint16_t*)lora_z, (const uint16_t*)lora_b, lora_rank);
+  };
+  if (lora_z != nullptr) launch(grouped_gemm_v2_kernel<false, false, true, true>);
+  else launch(grouped_gemm_v2_kernel<false, false, false, true>);
   MI355X_LAUNCH_CHECK();
   return 0;
 }

@@ -550,18 +550,21 @@ def permute_quantize_current(x: torch.Tensor, slots: torch.Tensor):
     return q, scales
 
 
-def swiglu_quantize_rows_current(h: torch.Tensor, limit: float | None = None):
+def swiglu_quantize_rows_current(h: torch.Tensor, limit: float | None = None, *,
+                                 activation: bool = False):
     """SwiGLU of interleaved bf16 ``h [R, 2I]`` quantized per row:
-    ``(q [R, I], scales fp32 [R])`` (``mi355x_swiglu_quantize_rows_current_fp8``)."""
+    ``(q [R, I], scales fp32 [R])``, plus the bf16 activation ``[R, I]`` when
+    ``activation`` (``mi355x_swiglu_quantize_rows_current_fp8``)."""
     if h.dtype != torch.bfloat16 or h.ndim != 2 or not h.is_contiguous():
         raise ValueError("swiglu_quantize_rows_current takes contiguous bf16 [rows, 2I]")
     rows, width = h.shape[0], h.shape[1] // 2
     device = _on_gpu(h)
     q = torch.empty((rows, width), dtype=FP8, device=device)
     scales = torch.empty(rows, dtype=torch.float32, device=device)
+    act = torch.empty((rows, width), dtype=torch.bfloat16, device=device) if activation else None
     _native.call("mi355x_swiglu_quantize_rows_current_fp8", _ptr(h), rows, width, _limit(limit),
-                 _ptr(q), _ptr(scales), _stream(device))
-    return q, scales
+                 _ptr(q), _ptr(scales), _ptr(act), _stream(device))
+    return (q, scales, act) if activation else (q, scales)
 
 
 def quantize_weights_current(w: torch.Tensor, *, interleaved: bool = False):
@@ -587,9 +590,13 @@ def quantize_weights_current(w: torch.Tensor, *, interleaved: bool = False):
     return data, transposed, scale, transposed_scale
 
 
-def gemm_rowwise(a, a_scale, w, w_scale, offsets):
+def gemm_rowwise(a, a_scale, w, w_scale, offsets, *, lora=None):
     """Row-scaled grouped e4m3 GEMM: bf16 ``out[r] = (a[r] @ w[e]^T) * a_scale[r]
-    * w_scale[e]`` per expert (``mi355x_gemm_fp8_rowwise``)."""
+    * w_scale[e]`` per expert (``mi355x_gemm_fp8_rowwise``). ``lora = (z bf16
+    [A, R], b bf16 [E, N, R])``, R a multiple of 16, adds ``z b[e]^T``
+    (``mi355x_gemm_fp8_rowwise_lora``)."""
+    if lora is not None:
+        return _gemm_rowwise_lora(a, a_scale, w, w_scale, offsets, *lora)
     rows, k = a.shape
     experts, n, wk = w.shape
     if a.dtype != FP8 or w.dtype != FP8 or wk != k:
@@ -603,6 +610,30 @@ def gemm_rowwise(a, a_scale, w, w_scale, offsets):
         "gemm_fp8_rowwise", device, 2 * rows * n * k, rows * k + experts * n * k + 2 * rows * n,
         "mi355x_gemm_fp8_rowwise", _ptr(a), _ptr(a_scale), rows, _ptr(w), _ptr(w_scale),
         experts, n, k, _ptr(offsets), _ptr(out), _stream(device),
+    )
+    return out
+
+
+def _gemm_rowwise_lora(a, a_scale, w, w_scale, offsets, z, b):
+    rows, k = a.shape
+    experts, n, wk = w.shape
+    rank = z.shape[1] if z.ndim == 2 else -1
+    if a.dtype != FP8 or w.dtype != FP8 or wk != k:
+        raise ValueError("gemm_rowwise takes e4m3 rows [A,K] and e4m3 weights [E,N,K]")
+    _check(a_scale, (rows,), torch.float32, "row scales")
+    _check(w_scale, (experts, n), torch.float32, "weight row scales")
+    _check(offsets, (experts + 1,), torch.int32, "offsets")
+    _check(z, (rows, rank), torch.bfloat16, "lora z")
+    _check(b, (experts, n, rank), torch.bfloat16, "lora b")
+    if not (z.is_contiguous() and b.is_contiguous()):
+        raise ValueError("lora factors must be contiguous")
+    device = _on_gpu(a, a_scale, w, w_scale, offsets, z, b)
+    out = torch.empty((rows, n), dtype=torch.bfloat16, device=device)
+    _timed(
+        "gemm_fp8_rowwise", device, 2 * rows * n * (k + rank),
+        rows * k + experts * n * k + 2 * rows * n,
+        "mi355x_gemm_fp8_rowwise_lora", _ptr(a), _ptr(a_scale), rows, _ptr(w), _ptr(w_scale),
+        experts, n, k, _ptr(offsets), _ptr(z), _ptr(b), rank, _ptr(out), _stream(device),
     )
     return out
 

@@ -8,10 +8,14 @@ expert, ``W -> W + scale * B[e] @ A[e]``:
     y   = a @ W2[e]^T  + scale * (a @ A2[e]^T) @ B2[e]^T,   a = SwiGLU(h13)
 
 The base weights are block-FP8 (``BlockFP8Weight`` containers, or plain
-masters quantized per call with ``compute_precision="fp8_block"``) and run on
-the MI355X grouped GEMMs. Each low-rank term ``z @ F^T`` starts the GEMM's
-fp32 accumulators (``mi355x_gemm_fp8_block_lora``: a rank-16-at-a-time bf16
-MFMA per output tile), where the reference's SonicMoE composition passes it
+masters quantized per call with ``compute_precision="fp8_block"``) or
+per-row FP8 (``RowFP8Weight``, or ``compute_precision="fp8_current"``), as
+the reference's SonicMoE LoRA serves both (``providers/sonicmoe/lora.py
+:36-40``), and run on the MI355X grouped GEMMs. Each low-rank term
+``z @ F^T`` starts the GEMM's fp32 accumulators
+(``mi355x_gemm_fp8_block_lora`` / ``mi355x_gemm_fp8_rowwise_lora``: a
+rank-16-at-a-time bf16 MFMA per output tile; the row-scaled form divides it
+by the descales its epilogue applies), where the reference's SonicMoE composition passes it
 as the GEMM's C input (``providers/sonicmoe/lora.py:1-45``): no LoRA term is
 materialized as ``[rows, N]`` or added by a separate pass. The scale is
 folded into the small ``B`` factors; ranks are padded with zero columns to a
@@ -33,7 +37,9 @@ from .. import kernels, router
 from ..block_fp8 import BlockFP8Weight
 from ..dispatch.context import weight_gradient_dtype
 from ..providers.mi355x import moe as provider
+from ..providers.mi355x import moe_current
 from ..routing import current_route_weight_precision, next_override
+from ..row_fp8 import RowFP8Weight
 
 IMPLEMENTATIONS = ("auto", "mi355x")
 
@@ -124,8 +130,13 @@ class _ExpertLoRA(torch.autograd.Function):
         width = hidden.shape[-1]
         tokens = hidden.numel() // width
         experts = router_weight.shape[0]
-        w13_data, w13_scale = w13.components()
-        w2_data, w2_scale = w2.components()
+        current = isinstance(w13, RowFP8Weight)
+        if current:  # rows (gate/up-adjacent for w13), transpose, per-row descales
+            w13_data, _, w13_scale, _ = w13.components()
+            w2_data, _, w2_scale, _ = w2.components()
+        else:
+            w13_data, w13_scale = w13.components()
+            w2_data, w2_scale = w2.components()
         inter = w2_data.shape[2]
         with torch.no_grad():
             x = hidden.reshape(tokens, width).contiguous()
@@ -156,17 +167,29 @@ class _ExpertLoRA(torch.autograd.Function):
             # the order of the weight rows the GEMM reads).
             z13 = _token_projection(x, a13b.reshape(experts * rank13, width).t(), experts,
                                     rows_token, rows_expert)
-            xq, xs = kernels.permute_quantize(x, slots)
-            h13 = kernels.gemm(xq, xs, w13_data, w13_scale, offsets, interleave=True,
-                               lora=(_padded(z13, r13), _padded(b13s, r13)))
-            aq, as_, act = kernels.swiglu_quantize(h13, limit, activation=True)
+            if current:
+                # The per-row w13 is stored gate/up-adjacent: B13 in that order.
+                xq, xs = kernels.permute_quantize_current(x, slots)
+                h13 = kernels.gemm_rowwise(xq, xs, w13_data, w13_scale, offsets,
+                                           lora=(_padded(z13, r13), _padded(b13b, r13)))
+                aq, as_, act = kernels.swiglu_quantize_rows_current(h13, limit, activation=True)
+            else:
+                xq, xs = kernels.permute_quantize(x, slots)
+                h13 = kernels.gemm(xq, xs, w13_data, w13_scale, offsets, interleave=True,
+                                   lora=(_padded(z13, r13), _padded(b13s, r13)))
+                aq, as_, act = kernels.swiglu_quantize(h13, limit, activation=True)
             # Down projection: z2 = a @ A2^T per routed row (the thin product
             # streams a once; rank padded to 16).
             z2p = _row_rank(act, _padded(a2b.transpose(1, 2), r2).transpose(1, 2).contiguous(),
                             offsets, segments)
             del act
             z2 = z2p[:, :rank2]
-            y = kernels.gemm(aq, as_, w2_data, w2_scale, offsets, lora=(z2p, _padded(b2b, r2)))
+            if current:
+                y = kernels.gemm_rowwise(aq, as_, w2_data, w2_scale, offsets,
+                                         lora=(z2p, _padded(b2b, r2)))
+            else:
+                y = kernels.gemm(aq, as_, w2_data, w2_scale, offsets,
+                                 lora=(z2p, _padded(b2b, r2)))
             output = kernels.combine(y, slots, weights, base)
             aux, probability_sum, _, _ = kernels.router_stats(logits, ids, top_k, mode,
                                                               opts["lengths"])
@@ -190,8 +213,13 @@ class _ExpertLoRA(torch.autograd.Function):
         tokens = hidden.numel() // width
         experts = router_weight.shape[0]
         assignments = order.numel()
-        w13_data, w13_scale = ctx.w13.components()
-        w2_data, w2_scale = ctx.w2.components()
+        current = isinstance(ctx.w13, RowFP8Weight)
+        if current:
+            _, w13_t, _, w13_ts = ctx.w13.components()
+            w2_data, w2_t, _, w2_ts = ctx.w2.components()
+        else:
+            w13_data, w13_scale = ctx.w13.components()
+            w2_data, w2_scale = ctx.w2.components()
         inter = w2_data.shape[2]
         rank13, rank2 = a13b.shape[1], a2b.shape[1]
         grad_dtype = weight_gradient_dtype()
@@ -206,10 +234,15 @@ class _ExpertLoRA(torch.autograd.Function):
             u2 = _token_projection(dy, b2b.permute(1, 0, 2).reshape(width, experts * rank2),
                                    experts, rows_token, rows_expert)
             r2 = _rank16(rank2)
-            dyq, dys = kernels.permute_quantize(dy, slots)
-            w2_t = provider.transposed_data(ctx.w2)
-            r = kernels.gemm(dyq, dys, w2_t, w2_scale, offsets, transposed_scale=True,
-                             lora=(_padded(u2, r2), _padded(a2b.transpose(1, 2), r2)))
+            lora_r = (_padded(u2, r2), _padded(a2b.transpose(1, 2), r2))
+            if current:
+                dyq, dys = kernels.permute_quantize_current(dy, slots)
+                r = kernels.gemm_rowwise(dyq, dys, w2_t, w2_ts, offsets, lora=lora_r)
+            else:
+                dyq, dys = kernels.permute_quantize(dy, slots)
+                w2_t = provider.transposed_data(ctx.w2)
+                r = kernels.gemm(dyq, dys, w2_t, w2_scale, offsets, transposed_scale=True,
+                                 lora=lora_r)
             dh, a_prime, dscore = kernels.routed_swiglu_backward(
                 r, h13, weights.reshape(-1), order, limit)
             del r
@@ -218,10 +251,16 @@ class _ExpertLoRA(torch.autograd.Function):
             u13p = _row_rank(dh, _padded(b13b, r13).transpose(1, 2).contiguous(), offsets,
                              segments)
             u13 = u13p[:, :rank13]
-            dhq, dhs = kernels.quantize_rows(dh, gate_up=True)
-            w13_t = provider.transposed_data(ctx.w13)
-            dx = kernels.gemm(dhq, dhs, w13_t, w13_scale, offsets, transposed_scale=True,
-                              lora=(u13p, _padded(a13b.transpose(1, 2), r13)))
+            lora_x = (u13p, _padded(a13b.transpose(1, 2), r13))
+            if current:
+                # dh's interleaved columns are the K order of w13's transpose.
+                dhq, dhs = kernels.quantize_rows_current(dh)
+                dx = kernels.gemm_rowwise(dhq, dhs, w13_t, w13_ts, offsets, lora=lora_x)
+            else:
+                dhq, dhs = kernels.quantize_rows(dh, gate_up=True)
+                w13_t = provider.transposed_data(ctx.w13)
+                dx = kernels.gemm(dhq, dhs, w13_t, w13_scale, offsets, transposed_scale=True,
+                                  lora=lora_x)
             del dhq, dhs
             grad_hidden = kernels.unpermute_sum(dx, slots)
             del dx
@@ -295,8 +334,9 @@ def expert_lora(
     ``b2 [E, D, r]`` (any float dtype, computed in bf16), ``router_weight
     [E, D]``. Routing options and ``swiglu_limit`` are `mlops.moe`'s.
     ``implementation`` is ``"auto"`` or ``"mi355x"`` (this build has no other
-    composition); ``compute_precision`` is ``None`` for block-FP8 containers
-    or ``"fp8_block"`` (plain masters quantized per call). Gradients reach the
+    composition); ``compute_precision`` is ``None`` for FP8 containers
+    (block or per-row), or ``"fp8_block"`` / ``"fp8_current"`` (plain masters
+    quantized per call). Gradients reach the
     factors, the router, the hidden and residual rows, and base weights that
     require them (plain masters; straight through the per-call quantizer).
     """
@@ -309,7 +349,10 @@ def expert_lora(
             raise ValueError("swiglu_limit must be positive")
     rows = hidden.numel() // hidden.shape[-1]
     lengths = (rows,) if lengths is None else tuple(int(x) for x in lengths)
-    support = provider.supports(
+    rules = moe_current if (compute_precision == "fp8_current" or (
+        compute_precision is None and any(isinstance(w, RowFP8Weight) for w in (gate_up, down)))
+    ) else provider
+    support = rules.supports(
         hidden, residual, router_weight, gate_up, down, surface="semantic", top_k=top_k,
         routing_mode=routing_mode, router_bias=router_bias, n_group=n_group,
         topk_group=topk_group, routed_scaling=routed_scaling, lengths=lengths,
@@ -327,7 +370,7 @@ def expert_lora(
                              f"got {tuple(factor.shape)}")
         if not factor.is_floating_point() or factor.device != hidden.device:
             raise ValueError(f"LoRA factor {name} must be a floating tensor on {hidden.device}")
-    w13, w2 = provider._containers(gate_up, down)
+    w13, w2 = rules._containers(gate_up, down)
     bias = None if router_bias is None or router_bias.numel() == 0 else router_bias
     opts = dict(top_k=int(top_k), routing_mode=str(routing_mode), scale=float(scale),
                 limit=swiglu_limit, router_bias=bias, n_group=int(n_group),

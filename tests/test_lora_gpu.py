@@ -15,7 +15,7 @@ import pytest
 import torch
 
 import mlops_amd
-from mlops_amd import BlockFP8Weight
+from mlops_amd import BlockFP8Weight, RowFP8Weight
 from mlops_amd.lora import expert_lora
 from oracle import moe_oracle as O
 from tests.conftest import frob_rel
@@ -44,11 +44,16 @@ def _leaf(t):
     return t.detach().clone().requires_grad_(True)
 
 
-def _run_gpu(x, res, wr, w13, w2, a13, b13, a2, b2, dy, *, train_base, mode, limit=None):
+def _run_gpu(x, res, wr, w13, w2, a13, b13, a2, b2, dy, *, train_base, mode, limit=None,
+             current=False):
     x, wr = _leaf(x), _leaf(wr)
     factors = [_leaf(t) for t in (a13, b13, a2, b2)]
     if train_base:
-        w13, w2, precision = _leaf(w13), _leaf(w2), "fp8_block"
+        w13, w2 = _leaf(w13), _leaf(w2)
+        precision = "fp8_current" if current else "fp8_block"
+    elif current:
+        w13, w2 = RowFP8Weight.quantize(w13, interleaved=True), RowFP8Weight.quantize(w2)
+        precision = None
     else:
         w13, w2, precision = BlockFP8Weight.quantize(w13), BlockFP8Weight.quantize(w2), None
     out, aux, counts, psum = expert_lora(
@@ -59,11 +64,21 @@ def _run_gpu(x, res, wr, w13, w2, a13, b13, a2, b2, dy, *, train_base, mode, lim
     return out.detach(), aux.detach(), counts, psum.detach(), grads
 
 
-def _run_oracle(x, res, wr, w13, w2, a13, b13, a2, b2, dy, *, train_base, mode, limit=None):
+def _dequantized_rows(w):
+    data, _, scale, _ = O.quantize_weights_current(w)
+    return data.float() * scale[..., None]
+
+
+def _run_oracle(x, res, wr, w13, w2, a13, b13, a2, b2, dy, *, train_base, mode, limit=None,
+                current=False):
     cpu = lambda t: t.detach().cpu()
-    # The base as the GPU path sees it: its block-FP8 values, dequantized.
-    w13d = O.dequantize_blocks(*O.quantize_blocks(cpu(w13).float()))
-    w2d = O.dequantize_blocks(*O.quantize_blocks(cpu(w2).float()))
+    # The base as the GPU path's forward sees it: its FP8 values, dequantized
+    # (per 128x128 block, or per row for fp8_current).
+    if current:
+        w13d, w2d = _dequantized_rows(cpu(w13).float()), _dequantized_rows(cpu(w2).float())
+    else:
+        w13d = O.dequantize_blocks(*O.quantize_blocks(cpu(w13).float()))
+        w2d = O.dequantize_blocks(*O.quantize_blocks(cpu(w2).float()))
     xl, wrl = _leaf(cpu(x)), _leaf(cpu(wr))
     w13l, w2l = _leaf(w13d), _leaf(w2d)
     factors = [_leaf(cpu(t)) for t in (a13, b13, a2, b2)]
@@ -95,6 +110,49 @@ def test_expert_lora_matches_native_on_dequantized_weights(device, mode, rank, t
     assert all(g.dtype == torch.float32 for g in grads[2:6])
     if train_base:
         assert grads[6].dtype == grads[7].dtype == torch.bfloat16
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rank,train_base", [(16, False), (7, True)])
+def test_expert_lora_on_an_fp8_current_base(device, rank, train_base):
+    """A per-row FP8 base (RowFP8Weight containers, or masters quantized per
+    call at fp8_current), as the reference's SonicMoE LoRA serves it: against
+    the native form on the dequantized rows at the same bounds."""
+    case = _inputs(device, rank, seed=30 + rank)
+    kw = dict(train_base=train_base, mode="softmax_then_topk", current=True)
+    out, aux, counts, psum, grads = _run_gpu(*case, **kw)
+    r_out, r_aux, r_counts, r_psum, r_grads = _run_oracle(*case, **kw)
+    assert torch.equal(counts.cpu(), r_counts)
+    assert frob_rel(out.cpu().float(), r_out.float()) < 4e-2
+    names = ["x", "router", "a13", "b13", "a2", "b2"] + (["w13", "w2"] if train_base else [])
+    for name, g, r in zip(names, grads, r_grads, strict=True):
+        assert g.shape == r.shape, name
+        err = frob_rel(g.cpu().float(), r.float())
+        assert err < BOUND, f"{name}: relative error {err:.3e}"
+
+
+@pytest.mark.gpu
+def test_zero_b_factors_are_mlops_moe_at_fp8_current(device):
+    x, res, wr, w13, w2, a13, b13, a2, b2, dy = _inputs(device, 16, seed=6)
+    b13, b2 = torch.zeros_like(b13), torch.zeros_like(b2)
+    w13c, w2c = RowFP8Weight.quantize(w13, interleaved=True), RowFP8Weight.quantize(w2)
+    options = dict(top_k=TOP_K, routing_mode="softmax_then_topk", swiglu_limit=2.75)
+
+    def run(lora):
+        xl, wrl = _leaf(x), _leaf(wr)
+        if lora:
+            outs = expert_lora(xl, res, wrl, w13c, w2c, a13, b13, a2, b2, scale=SCALE, **options)
+        else:
+            outs = mlops_amd.moe(xl, res, wrl, w13c, w2c, **options)
+        grads = torch.autograd.grad((outs[0].float() * dy.float()).sum() + 0.3 * outs[1],
+                                    [xl, wrl])
+        return [o.detach() for o in outs], grads
+
+    (outs, grads), (ref_outs, ref_grads) = run(True), run(False)
+    for a, b in zip(outs, ref_outs, strict=True):
+        assert torch.equal(a, b)
+    for a, b in zip(grads, ref_grads, strict=True):
+        assert frob_rel(a.float(), b.float()) < 1e-3
 
 
 @pytest.mark.gpu
