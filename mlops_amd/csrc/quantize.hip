@@ -358,18 +358,28 @@ __global__ void __launch_bounds__(256) quantize_transpose_kernel(
   const int c0 = cb * 128;
   // 128 rows x 128 source columns (bf16) into LDS, zeros past the expert.
   {
+    // All eight source rows first, then all eight row loads, then the LDS
+    // stores: the row loads depend on the gather loads, and loads complete
+    // in order, so interleaving them per row would hold each row's load
+    // behind the previous row's data.
     const int lane16 = tid & 15, rsub = tid >> 4;
+    int src[8];
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
       const int rr = p * 16 + rsub;
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (rr < nvalid) {
-        int src_row = r0 + rr;
-        if (gather != nullptr) src_row = gather[src_row] / gather_div;
-        val = *(const uint4*)(x + (size_t)src_row * pitch + c0 + lane16 * 8);
-      }
-      *(uint4*)&tile[rr * kQtPitch + lane16 * 8] = val;
+      src[p] = r0 + (rr < nvalid ? rr : 0);
+      if (gather != nullptr && rr < nvalid) src[p] = gather[src[p]] / gather_div;
     }
+    uint4 val[8];
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const int rr = p * 16 + rsub;
+      val[p] = make_uint4(0, 0, 0, 0);
+      if (rr < nvalid) val[p] = *(const uint4*)(x + (size_t)src[p] * pitch + c0 + lane16 * 8);
+    }
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+      *(uint4*)&tile[(p * 16 + rsub) * kQtPitch + lane16 * 8] = val[p];
   }
   __syncthreads();
   transpose_tile_pow2(true, tile, pmax, tid, qt, scales, c0, c0, gate_up ? width / 2 : 0, width,
@@ -500,20 +510,31 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
   const int nblk = width / 128;
   uint4 hv0[4], hv1[4], rv4[4], apk[4];
   float score[4];
+  // The rows' order entries first: each score is a load that depends on
+  // one, and loads complete in order, so an order load issued after a
+  // pass's h and r loads would hold the next pass's loads back until they
+  // land.
+  int orow[4];
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int rr = pass * 32 + rsub;
+    orow[pass] = rr < nvalid ? order[r0 + rr] : 0;
+  }
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int rr = pass * 32 + rsub;
     hv0[pass] = hv1[pass] = rv4[pass] = make_uint4(0, 0, 0, 0);
-    score[pass] = 0.0f;
     if (rr < nvalid) {
       const int row = r0 + rr;
       const uint16_t* hp = h + (size_t)row * 2 * width + 2 * j;
       hv0[pass] = *(const uint4*)hp;
       hv1[pass] = *(const uint4*)(hp + 8);
       rv4[pass] = *(const uint4*)(rmat + (size_t)row * width + j);
-      score[pass] = weights[order[row]];
     }
   }
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass)
+    score[pass] = pass * 32 + rsub < nvalid ? weights[orow[pass]] : 0.0f;
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int rr = pass * 32 + rsub;
