@@ -59,10 +59,16 @@ __global__ void __launch_bounds__(256) rows_current_kernel(
   amax = wave_max(amax);
   const float s = fmaxf(amax * kInv448, kMinScale);
   uint8_t* dst = q + (size_t)r * width;
-  for (int col = lane * 8; col < width; col += 512) {
-    float v[8];
-    load8(src + col, v);
-    *(uint2*)(dst + col) = quant8(v, s);
+  // Four chunks' loads before their stores: loads and stores complete in
+  // order, so a load issued after a store would wait for it.
+  for (int col0 = lane * 8; col0 < width; col0 += 4 * 512) {
+    float v[4][8];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (col0 + c * 512 < width) load8(src + col0 + c * 512, v[c]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (col0 + c * 512 < width) *(uint2*)(dst + col0 + c * 512) = quant8(v[c], s);
   }
   if (lane == 0) scales[r] = s;
 }
@@ -88,14 +94,29 @@ __global__ void __launch_bounds__(256) permute_rows_current_kernel(
   }
   amax = wave_max(amax);
   const float s = fmaxf(amax * kInv448, kMinScale);
-  const int32_t* dest = slots + (size_t)t * top_k;
-  for (int col = lane * 8; col < width; col += 512) {
-    float v[8];
-    load_bf16x8(src + col, v);
-    const uint2 packed = quant8(v, s);
-    for (int j = 0; j < top_k; ++j) *(uint2*)(q + (size_t)dest[j] * width + col) = packed;
+  // The token's slots in registers (read before any store), then four
+  // chunks' loads before their stores.
+  int dest[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j)
+    if (j < top_k) dest[j] = slots[(size_t)t * top_k + j];
+  for (int col0 = lane * 8; col0 < width; col0 += 4 * 512) {
+    float v[4][8];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (col0 + c * 512 < width) load_bf16x8(src + col0 + c * 512, v[c]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (col0 + c * 512 >= width) break;
+      const uint2 packed = quant8(v[c], s);
+#pragma unroll
+      for (int j = 0; j < 32; ++j)
+        if (j < top_k) *(uint2*)(q + (size_t)dest[j] * width + col0 + c * 512) = packed;
+    }
   }
-  if (lane < top_k) scales[dest[lane]] = s;
+#pragma unroll
+  for (int j = 0; j < 32; ++j)
+    if (j < top_k && lane == j) scales[dest[j]] = s;
 }
 
 // SwiGLU of an interleaved pre-activation row h [2I] (clamped at limit when
@@ -133,14 +154,39 @@ __global__ void __launch_bounds__(256) swiglu_rows_current_kernel(
   amax = wave_max(amax);
   const float s = fmaxf(amax * kInv448, kMinScale);
   uint8_t* dst = q + (size_t)r * width;
-  for (int j = lane * 8; j < width; j += 512) {
-    float act[8];
-    swiglu8(src + 2 * j, limit, act);
-    *(uint2*)(dst + j) = quant8(act, s);
-    if (act_out != nullptr)  // the bf16 activation too (expert LoRA's down-projection rank term)
-      *(uint4*)(act_out + (size_t)r * width + j) =
-          make_uint4(pack_bf16x2(act[0], act[1]), pack_bf16x2(act[2], act[3]),
-                     pack_bf16x2(act[4], act[5]), pack_bf16x2(act[6], act[7]));
+  // Four chunks' loads before their stores (loads and stores complete in
+  // order).
+  for (int j0 = lane * 8; j0 < width; j0 += 4 * 512) {
+    uint4 hv[4][2];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      hv[c][0] = hv[c][1] = make_uint4(0, 0, 0, 0);
+      if (j0 + c * 512 < width) {
+        hv[c][0] = *(const uint4*)(src + 2 * (j0 + c * 512));
+        hv[c][1] = *(const uint4*)(src + 2 * (j0 + c * 512) + 8);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int j = j0 + c * 512;
+      if (j >= width) break;
+      float a[8], b[8], act[8];
+      unpack_bf16x8(hv[c][0], a);
+      unpack_bf16x8(hv[c][1], b);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float g0 = a[2 * i], u0 = a[2 * i + 1], g1 = b[2 * i], u1 = b[2 * i + 1];
+        clamp_gate_up(g0, u0, limit);
+        clamp_gate_up(g1, u1, limit);
+        act[i] = silu_f(g0) * u0;
+        act[4 + i] = silu_f(g1) * u1;
+      }
+      *(uint2*)(dst + j) = quant8(act, s);
+      if (act_out != nullptr)  // the bf16 activation too (expert LoRA's down-projection term)
+        *(uint4*)(act_out + (size_t)r * width + j) =
+            make_uint4(pack_bf16x2(act[0], act[1]), pack_bf16x2(act[2], act[3]),
+                       pack_bf16x2(act[4], act[5]), pack_bf16x2(act[6], act[7]));
+    }
   }
   if (lane == 0) scales[r] = s;
 }
@@ -384,7 +430,7 @@ extern "C" int mi355x_permute_quantize_current_fp8(const void* x, int tokens, in
                                                    float* scales, void* stream) {
   MI355X_REQUIRE(width > 0 && width % 8 == 0,
                  "permute_quantize_current: width must be a multiple of 8");
-  MI355X_REQUIRE(top_k > 0 && top_k <= 64, "permute_quantize_current: top_k must be in [1, 64]");
+  MI355X_REQUIRE(top_k > 0 && top_k <= 32, "permute_quantize_current: top_k must be in [1, 32]");
   MI355X_REQUIRE(tokens >= 0, "permute_quantize_current: negative tokens");
   if (tokens == 0) return MI355X_OK;
   hipLaunchKernelGGL(permute_rows_current_kernel, dim3((tokens + 3) / 4), dim3(256), 0,
