@@ -270,8 +270,10 @@ class _ExpertLoRA(torch.autograd.Function):
                 score = weights.reshape(-1)[order.long()]
                 zs = _scatter_tokens(z2.float() * (score[:, None] * scale), tokens, experts,
                                      rows_token, rows_expert)
-                g = dy.float().t() @ zs
-                grads[3] = g.view(width, experts, rank2).permute(1, 0, 2).contiguous()
+                # dy^T zs as (zs^T dy)^T: the token-reduction product of the
+                # router weight gradient, bf16 operands with fp32 sums.
+                g = router.split_k_product(zs.to(torch.bfloat16), dy).t()
+                grads[3] = g.reshape(width, experts, rank2).permute(1, 0, 2).contiguous()
             if need[7]:    # A2: sum_j u2_j a'_j^T, a' = score * a
                 grads[2] = _factor_grad(u2, a_prime, segments, (experts, rank2, inter))
             if need[6]:    # B13: s * sum_j dh_j z13_j^T (rows back to gate then up)
@@ -279,8 +281,8 @@ class _ExpertLoRA(torch.autograd.Function):
                 grads[1] = gate_up_rows(g.mul_(scale))
             if need[5]:    # A13: sum_j u13_j x_j^T, formed on the token side
                 zd = _scatter_tokens(u13, tokens, experts, rows_token, rows_expert)
-                grads[0] = torch.mm(zd.t().to(torch.bfloat16), x, out_dtype=torch.float32
-                                    ).view(experts, rank13, width)
+                grads[0] = router.split_k_product(zd.to(torch.bfloat16), x
+                                                  ).view(experts, rank13, width)
             grads = [None if g is None else g.to(dtype)
                      for g, dtype in zip(grads, ctx.factor_dtypes)]
             # Base weight gradients, when the base is trained.

@@ -48,6 +48,23 @@ def add_router_input_gradient_(grad_hidden, grad_logits, weight):
     return grad_hidden
 
 
+def split_k_product(left: torch.Tensor, right: torch.Tensor) -> torch.Tensor:
+    """``left^T @ right`` with fp32 sums and output, for token-major operands
+    ``left [T, M]`` and ``right [T, N]`` (bf16/fp16 on the GPU) with a long
+    token dimension and small M: split over the tokens into SPLIT_K batched
+    products whose fp32 partials are summed. Each batch operand is a view (the
+    left one transposed), so nothing is copied. hipBLASLt runs this form ~2x
+    faster than the single long-K product on MI355X."""
+    tokens = left.shape[0]
+    split = SPLIT_K if tokens % SPLIT_K == 0 and tokens >= SPLIT_K * 512 else 1
+    if split > 1 and left.is_cuda:
+        chunk = tokens // split
+        return torch.bmm(left.view(split, chunk, left.shape[1]).transpose(1, 2),
+                         right.view(split, chunk, right.shape[1]),
+                         out_dtype=torch.float32).sum(0)
+    return _product_fp32(left.t(), right)
+
+
 def router_weight_gradient(grad_logits, hidden, dtype) -> torch.Tensor:
     """``grad_logits.T @ hidden`` with fp32 sums, the cotangent in two bf16 pieces."""
     operands = operand_dtype(hidden)
@@ -66,19 +83,14 @@ def router_weight_gradient(grad_logits, hidden, dtype) -> torch.Tensor:
     high = pieces[:, :experts]
     high.copy_(grad_logits)
     torch.sub(grad_logits, high.float(), out=pieces[:, experts:])
-    split = SPLIT_K if tokens % SPLIT_K == 0 and tokens >= SPLIT_K * 512 else 1
-    if split > 1 and rows.is_cuda:
-        chunk = tokens // split
-        both = torch.bmm(pieces.view(split, chunk, 2 * experts).transpose(1, 2),
-                         rows.view(split, chunk, rows.shape[1]), out_dtype=torch.float32).sum(0)
-    else:
-        both = _product_fp32(pieces.t(), rows)
+    both = split_k_product(pieces, rows)
     gradient = both[:experts].add_(both[experts:])
     return gradient.to(dtype)
 
 
 __all__ = [
     "add_router_input_gradient_",
+    "split_k_product",
     "operand_dtype",
     "router_logits",
     "router_weight_gradient",
