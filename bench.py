@@ -109,6 +109,59 @@ def gemm_main(args, cfg):
     }))
 
 
+def vendor_gemm_main(args, cfg):
+    """Calibration, not the benchmark line: the four GEMM shapes of one layer
+    step as ONE dense problem each (rows = tokens*top_k, one group), timed
+    through hipBLASLt (``torch._scaled_mm``, per-tensor and per-row scales)
+    and through this package's row-scaled and 128x128 block-scaled kernels
+    with the same operands. Prints one JSON line per shape."""
+    from mlops_amd import kernels as K
+
+    device = torch.device("cuda", 0)
+    rows = cfg["tokens"] * cfg["top_k"]
+    h, i = cfg["hidden"], cfg["inter"]
+    shapes = {"up": (2 * i, h), "down": (h, i), "dgrad_down": (i, h), "dgrad_up": (h, 2 * i)}
+    g = torch.Generator(device=device).manual_seed(0)
+
+    def timed(fn, reps=20):
+        for _ in range(3):
+            fn()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / reps
+
+    offsets = torch.tensor([0, rows], dtype=torch.int32, device=device)
+    for name, (n, k) in shapes.items():
+        x = torch.randn(rows, k, generator=g, device=device).to(torch.bfloat16)
+        w = (torch.randn(1, n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+        xq_r, xs_r = K.quantize_rows_current(x)
+        wq_r, _, ws_r, _ = K.quantize_weights_current(w)
+        xq_b, xs_b = K.quantize_rows(x)
+        wq_b, ws_b = K.quantize_weight_blocks(w)
+        one = torch.ones((), device=device)
+        runs = {
+            "hipblaslt_tensorwise": lambda: torch._scaled_mm(
+                xq_r, wq_r[0].t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16),
+            "hipblaslt_rowwise": lambda: torch._scaled_mm(
+                xq_r, wq_r[0].t(), scale_a=xs_r[:, None], scale_b=ws_r[0][None, :],
+                out_dtype=torch.bfloat16),
+            "mi355x_gemm_fp8_rowwise": lambda: K.gemm_rowwise(xq_r, xs_r, wq_r, ws_r, offsets),
+            "mi355x_gemm_fp8_block": lambda: K.gemm(xq_b, xs_b, wq_b, ws_b, offsets),
+        }
+        flops = 2 * rows * n * k
+        line = {"shape": name, "rows": rows, "n": n, "k": k}
+        for label, fn in runs.items():
+            ms = timed(fn)
+            line[label] = {"us": round(ms * 1e3, 1), "tflops": round(flops / ms / 1e9, 1)}
+        print(json.dumps(line), flush=True)
+        del x, w, xq_r, xs_r, wq_r, ws_r, xq_b, xs_b, wq_b, ws_b
+
+
 def make_inputs(cfg, device, seed=0):
     g = torch.Generator(device=device).manual_seed(seed)
     t, h, i, e = cfg["tokens"], cfg["hidden"], cfg["inter"], cfg["experts"]
@@ -250,6 +303,9 @@ def main():
     parser.add_argument("--calibration-copy-mib", type=int, default=0,
                         help="after the timed steps, run one device copy of this many MiB "
                              "(the known-size kernel that calibrates rocprofv3 byte counters)")
+    parser.add_argument("--vendor-gemm", action="store_true",
+                        help="instead of the benchmark line, time the layer's four GEMM shapes "
+                             "as dense problems through hipBLASLt and this package's kernels")
     args = parser.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
@@ -260,6 +316,9 @@ def main():
     from mlops_amd import kernels
 
     cfg = CONFIGS[args.config]
+    if args.vendor_gemm:
+        vendor_gemm_main(args, cfg)
+        return
     if cfg.get("gemm_only"):
         gemm_main(args, cfg)
         return
