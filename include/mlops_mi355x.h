@@ -302,7 +302,8 @@ int mi355x_quantize_weights_current_fp8(const void* w, int is_fp32, int experts,
                                         float* scales_t, void* workspace, size_t workspace_bytes,
                                         void* stream);
 /* Bytes of device workspace mi355x_quantize_weights_current_fp8 needs (the
- * column maxima of each 128-row tile). */
+ * row and column maxima of each 128 x 128 tile, and the reciprocals of both
+ * scale vectors). */
 size_t mi355x_quantize_weights_current_workspace_size(int experts, int out, int in);
 
 /* Thin grouped product of expert LoRA: out[r, 0:R] = sum_k a[r, k] *

@@ -146,14 +146,14 @@ __device__ __forceinline__ void unpack_bf16x8(uint4 r, float* v) {
   }
 }
 
-__device__ __forceinline__ uint2 quant8(const float* v, float s) {
-  const float inv = 1.0f / s;
+__device__ __forceinline__ uint2 quant8(const float* v, float s, float inv) {
   uint32_t lo = f32x4_to_e4m3(quant_div_inv(v[0], s, inv), quant_div_inv(v[1], s, inv),
                               quant_div_inv(v[2], s, inv), quant_div_inv(v[3], s, inv));
   uint32_t hi = f32x4_to_e4m3(quant_div_inv(v[4], s, inv), quant_div_inv(v[5], s, inv),
                               quant_div_inv(v[6], s, inv), quant_div_inv(v[7], s, inv));
   return make_uint2(lo, hi);
 }
+__device__ __forceinline__ uint2 quant8(const float* v, float s) { return quant8(v, s, 1.0f / s); }
 
 // ---------------------------------------------------------------- waves
 __device__ __forceinline__ float wave_max(float v) {

@@ -192,11 +192,13 @@ __global__ void __launch_bounds__(256) swiglu_rows_current_kernel(
 }
 
 // Both orientations of weights w [E, out, in] in two passes over w:
-//  1. weight_amax_kernel: one block per (64 stored rows, expert). It writes
-//     each row's scale (a wave reduces a whole row), and the maxima of its
-//     rows per column to colpart[e][tile][c] in the workspace.
-//  2. col_scale_kernel reduces colpart over the row tiles into the column
-//     scales.
+//  1. weight_amax_kernel: one block per (128 x 128 tile, expert), in the
+//     tiling and thread layout of the quantize pass. It writes the tile's
+//     maxima per stored row to rowpart[e][column tile][row] and per column
+//     to colpart[e][row tile][column] in the workspace.
+//  2. scale_reduce_kernel reduces the partials into the row scales and the
+//     column scales (a maximum, so the order does not matter), and writes
+//     each scale's reciprocal to the workspace for the quantize pass.
 //  3. weight_quantize_kernel: one block per (128 x 128 tile, expert). It
 //     quantizes the tile with its rows' scales into q, and with its columns'
 //     scales into qt through an LDS transpose.
@@ -206,144 +208,151 @@ __device__ __forceinline__ int logical_row(int p, int out, int interleave) {
   return interleave ? ((p & 1) ? out / 2 + (p >> 1) : (p >> 1)) : p;
 }
 
-constexpr int kAmaxRows = 64;  // 3 x 256 blocks fill the GPU evenly for E = 128, out = 1536
 constexpr int kQTile = 128;
 
-template <typename T>
-__global__ void __launch_bounds__(256) weight_amax_kernel(
-    const T* __restrict__ w, int out, int in, int interleave, float* __restrict__ scales,
-    float* __restrict__ colpart) {
-  __shared__ float colmax[4][2048 + 8];  // per-wave column maxima of a 2048-column chunk
-  const int e = blockIdx.y, tile = blockIdx.x, p0 = tile * kAmaxRows;
-  const int tiles = gridDim.x;
-  const int wave = threadIdx.x >> 6, lane = lane_id();
-  const T* we = w + (size_t)e * out * in;
-  const int prows = min(kAmaxRows, out - p0);
-  for (int c0 = 0; c0 < in; c0 += 2048) {
-    const int cw = min(2048, in - c0);
-    float cm[32];
+// Thread t of a 128 x 128 tile block holds the tile's stored rows
+// rg * R + i (i < R) at the 8 columns cg * 8 + j, rg = t / 16, cg = t % 16:
+// a wave's load instruction reads 4 rows x 256 contiguous bytes. All R
+// loads are issued before any use.
+template <int R, typename T>
+__device__ __forceinline__ void load_tile(const T* __restrict__ we, int out, int in,
+                                          int interleave, int p0, int col, int rg,
+                                          float (&v)[R][8]) {
 #pragma unroll
-    for (int i = 0; i < 32; ++i) cm[i] = 0.0f;
-    // Wave w takes rows w, w + 4, ..., two at a time (all eight loads of a
-    // pair issued before the maxima); lane l takes 8 columns per 512.
-    for (int pr = wave; pr < prows; pr += 8) {
-      float rmax[2] = {0.0f, 0.0f};
-      float v[2][4][8];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int p = p0 + pr + 4 * h;
-        const T* row = we + (size_t)logical_row(p, out, interleave) * in + c0;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int col = u * 512 + lane * 8;
-          if (pr + 4 * h < prows && col < cw) {
-            load8(row + col, v[h][u]);
-          } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[h][u][i] = 0.0f;
-          }
-        }
-      }
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float a = fabsf(v[h][u][i]);
-            rmax[h] = fmaxf(rmax[h], a);
-            cm[u * 8 + i] = fmaxf(cm[u * 8 + i], a);
-          }
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const float m_row = wave_max(rmax[h]);
-        // The row's running maximum over the column chunks lives in scales[]
-        // (this block is the row's only writer), finished after the last chunk.
-        if (lane == 0 && pr + 4 * h < prows) {
-          const size_t at = (size_t)e * out + p0 + pr + 4 * h;
-          const float prev = c0 == 0 ? 0.0f : scales[at];
-          const float m = fmaxf(prev, m_row);
-          scales[at] = c0 + 2048 >= in ? fmaxf(m * kInv448, kMinScale) : m;
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) colmax[wave][u * 512 + lane * 8 + i] = cm[u * 8 + i];
-    __syncthreads();
-    float* part = colpart + ((size_t)e * tiles + tile) * in + c0;
-    for (int c = threadIdx.x; c < cw; c += 256)
-      part[c] = fmaxf(fmaxf(colmax[0][c], colmax[1][c]), fmaxf(colmax[2][c], colmax[3][c]));
-    __syncthreads();
-  }
-}
-
-__global__ void __launch_bounds__(256) col_scale_kernel(const float* __restrict__ colpart,
-                                                        int experts, int tiles, int in,
-                                                        float* __restrict__ scales_t) {
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // e * in + c
-  if (i >= (size_t)experts * in) return;
-  const size_t e = i / in, c = i - e * in;
-  const float* part = colpart + e * tiles * in + c;
-  float m = 0.0f;
-  for (int k = 0; k < tiles; ++k) m = fmaxf(m, part[(size_t)k * in]);
-  scales_t[i] = fmaxf(m * kInv448, kMinScale);
-}
-
-template <typename T>
-__global__ void __launch_bounds__(256) weight_quantize_kernel(
-    const T* __restrict__ w, int out, int in, int interleave, const float* __restrict__ scales,
-    const float* __restrict__ scales_t, uint8_t* __restrict__ q, uint8_t* __restrict__ qt) {
-  __shared__ uint8_t tile[kQTile][kQTile + 8];  // [column][stored row]
-  __shared__ float colscale[kQTile];
-  const int e = blockIdx.z, p0 = blockIdx.y * kQTile, c0 = blockIdx.x * kQTile;
-  const int t = threadIdx.x, cg = t & 15, rg = t >> 4;  // 16 column groups x 16 row groups
-  const int col = c0 + cg * 8;
-  const bool col_ok = col < in;
-  const T* we = w + (size_t)e * out * in;
-  // The thread's 8 consecutive rows rg * 8 + i, all loads issued first.
-  float v[8][8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int p = p0 + rg * 8 + i;
-    if (p < out && col_ok) {
+  for (int i = 0; i < R; ++i) {
+    const int p = p0 + rg * R + i;
+    if (p < out && col < in) {
       load8(we + (size_t)logical_row(p, out, interleave) * in + col, v[i]);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[i][j] = 0.0f;
     }
   }
-  if (t < kQTile) colscale[t] = c0 + t < in ? scales_t[(size_t)e * in + c0 + t] : 1.0f;
-  __syncthreads();
-  float cs[8], ci[8];
+}
+
+template <typename T>
+__global__ void __launch_bounds__(512) weight_amax_kernel(
+    const T* __restrict__ w, int out, int in, int interleave, float* __restrict__ rowpart,
+    float* __restrict__ colpart) {
+  __shared__ float colmax[8][kQTile];  // per-wave column maxima
+  const int e = blockIdx.z, p0 = blockIdx.y * kQTile, c0 = blockIdx.x * kQTile;
+  const int t = threadIdx.x, cg = t & 15, rg = t >> 4, wave = t >> 6;
+  float v[4][8];
+  load_tile<4>(w + (size_t)e * out * in, out, in, interleave, p0, c0 + cg * 8, rg, v);
+  float rm[4], cm[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    cs[j] = colscale[cg * 8 + j];
-    ci[j] = 1.0f / cs[j];
-  }
-  uint32_t lo[8], hi[8];  // column j's bytes of the thread's 8 rows
+  for (int j = 0; j < 8; ++j) cm[j] = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) lo[j] = hi[j] = 0u;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int p = p0 + rg * 8 + i;
-    if (p < out && col_ok)
-      *(uint2*)(q + ((size_t)e * out + p) * in + col) = quant8(v[i], scales[(size_t)e * out + p]);
+  for (int i = 0; i < 4; ++i) {
+    rm[i] = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const uint32_t b = f32x2_to_e4m3(quant_div_inv(v[i][j], cs[j], ci[j]), 0.0f) & 0xffu;
-      if (i < 4) lo[j] |= b << (8 * i);
-      else hi[j] |= b << (8 * (i - 4));
+      const float a = fabsf(v[i][j]);
+      rm[i] = fmaxf(rm[i], a);
+      cm[j] = fmaxf(cm[j], a);
     }
   }
+  // Rows over the 16 column groups (lanes 16 apart share rows: xor 1..8);
+  // columns over the wave's 4 row groups (xor 16, 32), then over the waves.
 #pragma unroll
-  for (int j = 0; j < 8; ++j) *(uint2*)&tile[cg * 8 + j][rg * 8] = make_uint2(lo[j], hi[j]);
+  for (int o = 1; o < 16; o <<= 1)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rm[i] = fmaxf(rm[i], __shfl_xor(rm[i], o, 64));
+#pragma unroll
+  for (int o = 16; o < 64; o <<= 1)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cm[j] = fmaxf(cm[j], __shfl_xor(cm[j], o, 64));
+  const int p = p0 + rg * 4;
+  if (cg == 0 && p < out)  // out % 16 == 0: all 4 rows exist
+    *(float4*)(rowpart + ((size_t)e * gridDim.x + blockIdx.x) * out + p) =
+        make_float4(rm[0], rm[1], rm[2], rm[3]);
+  if ((t & 63) < 16) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) colmax[wave][cg * 8 + j] = cm[j];
+  }
   __syncthreads();
-  // 128 qt rows x 128 bytes, four passes of 32 rows: thread t writes 16 bytes.
+  if (t < kQTile && c0 + t < in) {
+    float m = colmax[0][t];
 #pragma unroll
-  for (int pass = 0; pass < 4; ++pass) {
-    const int cc = pass * 32 + (t >> 3), seg = (t & 7) * 16;
+    for (int k = 1; k < 8; ++k) m = fmaxf(m, colmax[k][t]);
+    colpart[((size_t)e * gridDim.y + blockIdx.y) * in + c0 + t] = m;
+  }
+}
+
+// Thread i < experts * out: row scale i from its ctiles partials; the next
+// experts * in threads: column scale from its rtiles partials.
+__global__ void __launch_bounds__(256) scale_reduce_kernel(
+    const float* __restrict__ rowpart, const float* __restrict__ colpart, int experts, int out,
+    int in, int ctiles, int rtiles, float* __restrict__ scales, float* __restrict__ scales_t,
+    float* __restrict__ inverse) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t nrow = (size_t)experts * out;
+  float m = 0.0f;
+  if (i < nrow) {
+    const size_t e = i / out, p = i - e * out;
+    const float* part = rowpart + e * ctiles * out + p;
+    for (int k = 0; k < ctiles; ++k) m = fmaxf(m, part[(size_t)k * out]);
+    const float sc = fmaxf(m * kInv448, kMinScale);
+    scales[i] = sc;
+    inverse[i] = 1.0f / sc;
+  } else if (i - nrow < (size_t)experts * in) {
+    const size_t j = i - nrow, e = j / in, c = j - e * in;
+    const float* part = colpart + e * rtiles * in + c;
+    for (int k = 0; k < rtiles; ++k) m = fmaxf(m, part[(size_t)k * in]);
+    const float sc = fmaxf(m * kInv448, kMinScale);
+    scales_t[j] = sc;
+    inverse[i] = 1.0f / sc;
+  }
+}
+
+// 512 threads, 4 rows x 8 columns each: the two quantizations of every
+// element (row scale for q, column scale for qt) make this pass ALU-heavy,
+// and the small per-thread tile keeps ~8 waves per SIMD to hide the loads.
+template <typename T>
+__global__ void __launch_bounds__(512) weight_quantize_kernel(
+    const T* __restrict__ w, int out, int in, int interleave, const float* __restrict__ scales,
+    const float* __restrict__ scales_t, const float* __restrict__ inverse, uint8_t* __restrict__ q,
+    uint8_t* __restrict__ qt) {
+  __shared__ uint8_t tile[kQTile][kQTile + 8];  // [column][stored row]
+  __shared__ float colscale[2][kQTile];         // column scales and their reciprocals
+  const int e = blockIdx.z, p0 = blockIdx.y * kQTile, c0 = blockIdx.x * kQTile;
+  const int t = threadIdx.x, cg = t & 15, rg = t >> 4;  // 16 column groups x 32 row groups
+  const int col = c0 + cg * 8;
+  const bool col_ok = col < in;
+  float v[4][8];
+  load_tile<4>(w + (size_t)e * out * in, out, in, interleave, p0, col, rg, v);
+  // The row scales and the column scales are loaded before any store:
+  // loads and stores complete in order, so a load behind a store waits.
+  const int pr = min(p0 + rg * 4, out - 4);  // out % 16 == 0
+  const float4 rs = *(const float4*)(scales + (size_t)e * out + pr);
+  const float4 ri = *(const float4*)(inverse + (size_t)e * out + pr);
+  if (t < 2 * kQTile) {
+    const int c = t & (kQTile - 1);
+    const float* src = t < kQTile ? scales_t + (size_t)e * in
+                                  : inverse + (size_t)gridDim.z * out + (size_t)e * in;
+    colscale[t >> 7][c] = c0 + c < in ? src[c0 + c] : 1.0f;
+  }
+  __syncthreads();
+  const float rsv[4] = {rs.x, rs.y, rs.z, rs.w}, riv[4] = {ri.x, ri.y, ri.z, ri.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p = p0 + rg * 4 + i;
+    if (p < out && col_ok)
+      *(uint2*)(q + ((size_t)e * out + p) * in + col) = quant8(v[i], rsv[i], riv[i]);
+  }
+  // Column j's bytes of the thread's 4 rows, one conversion pair each.
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float cs = colscale[0][cg * 8 + j], ci = colscale[1][cg * 8 + j];
+    *(uint32_t*)&tile[cg * 8 + j][rg * 4] =
+        f32x4_to_e4m3(quant_div_inv(v[0][j], cs, ci), quant_div_inv(v[1][j], cs, ci),
+                      quant_div_inv(v[2][j], cs, ci), quant_div_inv(v[3][j], cs, ci));
+  }
+  __syncthreads();
+  // 128 qt rows x 128 bytes, two passes of 64 rows: thread t writes 16 bytes.
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int cc = pass * 64 + (t >> 3), seg = (t & 7) * 16;
     if (c0 + cc < in && p0 + seg < out) {
       const uint2 a = *(const uint2*)&tile[cc][seg], b = *(const uint2*)&tile[cc][seg + 8];
       *(uint4*)(qt + ((size_t)e * in + c0 + cc) * out + p0 + seg) = make_uint4(a.x, a.y, b.x, b.y);
@@ -385,7 +394,8 @@ extern "C" int mi355x_swiglu_quantize_rows_current_fp8(const void* h, int rows, 
 
 extern "C" size_t mi355x_quantize_weights_current_workspace_size(int experts, int out, int in) {
   if (experts <= 0 || out <= 0 || in <= 0) return 0;
-  return (size_t)experts * ((out + kAmaxRows - 1) / kAmaxRows) * in * sizeof(float);
+  const size_t rtiles = (out + kQTile - 1) / kQTile, ctiles = (in + kQTile - 1) / kQTile;
+  return (size_t)experts * (ctiles * out + rtiles * in + out + in) * sizeof(float);
 }
 
 extern "C" int mi355x_quantize_weights_current_fp8(const void* w, int is_fp32, int experts,
@@ -400,26 +410,28 @@ extern "C" int mi355x_quantize_weights_current_fp8(const void* w, int is_fp32, i
                      workspace_bytes >= mi355x_quantize_weights_current_workspace_size(experts, out, in),
                  "quantize_weights_current: workspace too small");
   hipStream_t s = (hipStream_t)stream;
-  const int tiles = (out + kAmaxRows - 1) / kAmaxRows;
-  float* colpart = (float*)workspace;
-  const dim3 amax_grid(tiles, experts);
   const dim3 tile_grid((in + kQTile - 1) / kQTile, (out + kQTile - 1) / kQTile, experts);
+  float* rowpart = (float*)workspace;
+  float* colpart = rowpart + (size_t)experts * tile_grid.x * out;
+  // Reciprocals of the row scales [E, out], then of the column scales [E, in].
+  float* inverse = colpart + (size_t)experts * tile_grid.y * in;
   if (is_fp32) {
-    hipLaunchKernelGGL(weight_amax_kernel<float>, amax_grid, dim3(256), 0, s, (const float*)w,
-                       out, in, interleave, scales, colpart);
+    hipLaunchKernelGGL(weight_amax_kernel<float>, tile_grid, dim3(512), 0, s, (const float*)w,
+                       out, in, interleave, rowpart, colpart);
   } else {
-    hipLaunchKernelGGL(weight_amax_kernel<uint16_t>, amax_grid, dim3(256), 0, s,
-                       (const uint16_t*)w, out, in, interleave, scales, colpart);
+    hipLaunchKernelGGL(weight_amax_kernel<uint16_t>, tile_grid, dim3(512), 0, s,
+                       (const uint16_t*)w, out, in, interleave, rowpart, colpart);
   }
-  const size_t ncol = (size_t)experts * in;
-  hipLaunchKernelGGL(col_scale_kernel, dim3((unsigned)((ncol + 255) / 256)), dim3(256), 0, s,
-                     colpart, experts, tiles, in, scales_t);
+  const size_t n = (size_t)experts * (out + in);
+  hipLaunchKernelGGL(scale_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                     rowpart, colpart, experts, out, in, (int)tile_grid.x, (int)tile_grid.y,
+                     scales, scales_t, inverse);
   if (is_fp32) {
-    hipLaunchKernelGGL(weight_quantize_kernel<float>, tile_grid, dim3(256), 0, s, (const float*)w,
-                       out, in, interleave, scales, scales_t, q, qt);
+    hipLaunchKernelGGL(weight_quantize_kernel<float>, tile_grid, dim3(512), 0, s, (const float*)w,
+                       out, in, interleave, scales, scales_t, inverse, q, qt);
   } else {
-    hipLaunchKernelGGL(weight_quantize_kernel<uint16_t>, tile_grid, dim3(256), 0, s,
-                       (const uint16_t*)w, out, in, interleave, scales, scales_t, q, qt);
+    hipLaunchKernelGGL(weight_quantize_kernel<uint16_t>, tile_grid, dim3(512), 0, s,
+                       (const uint16_t*)w, out, in, interleave, scales, scales_t, inverse, q, qt);
   }
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
