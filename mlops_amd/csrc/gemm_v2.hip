@@ -16,20 +16,34 @@ struct Tile {
 };
 
 __device__ __forceinline__ Tile describe(const int* prefix, const int32_t* __restrict__ offsets,
-                                         int experts, int n_tiles, int tile, int nk) {
+                                         int experts, int n_tiles, int tile, int nk, int n_group,
+                                         int rotate) {
   // Every field is wave-uniform; readfirstlane lets the compiler keep them
   // (and everything derived: weight bases, scale addresses) in SGPRs.
   Tile t;
-  const int mt = tile / n_tiles;
+  int mt = tile / n_tiles;
   t.nt = tile % n_tiles;
   t.e = __builtin_amdgcn_readfirstlane(find_expert(prefix, experts, mt));
+  if (n_group > 0) {
+    // Inside the expert: groups of n_group N tiles (the last may be
+    // narrower), each walked over all the expert's row blocks, N fastest.
+    // An expert that owns a tile has at least one row block.
+    const int blocks = prefix[t.e + 1] - prefix[t.e];
+    const int local = tile - prefix[t.e] * n_tiles;
+    const int g = local / (blocks * n_group);
+    const int gs = min(n_group, n_tiles - g * n_group);
+    const int idx = local - g * blocks * n_group;
+    mt = __builtin_amdgcn_readfirstlane(prefix[t.e] + idx / gs);
+    t.nt = __builtin_amdgcn_readfirstlane(g * n_group + idx % gs);
+  }
   t.row0 = __builtin_amdgcn_readfirstlane(offsets[t.e] + (mt - prefix[t.e]) * BM);
   t.nvalid = __builtin_amdgcn_readfirstlane(min(BM, offsets[t.e + 1] - t.row0));
   // Tiles that share an operand panel run at the same time on neighbouring
   // CUs of one XCD; starting each at a different K step means one of them
   // takes a panel step's L2 miss and the others find it in L2 later,
-  // instead of all of them waiting on the same miss together.
-  t.rot = __builtin_amdgcn_readfirstlane((tile * 7) % nk);
+  // instead of all of them waiting on the same miss together. The grouped
+  // order runs unrotated: there the CUs sharing a panel read it together.
+  t.rot = rotate ? __builtin_amdgcn_readfirstlane((tile * 7) % nk) : 0;
   return t;
 }
 
@@ -60,7 +74,8 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     int N, int K, const int32_t* __restrict__ offsets, int interleave,
     const uint16_t* __restrict__ addend, uint16_t* __restrict__ out,
     uint8_t* __restrict__ act_q, float* __restrict__ act_scales, float limit,
-    const uint16_t* __restrict__ lora_z, const uint16_t* __restrict__ lora_b, int lora_rank) {
+    const uint16_t* __restrict__ lora_z, const uint16_t* __restrict__ lora_b, int lora_rank,
+    int n_group, int rotate) {
   __shared__ __align__(1024) uint8_t smem[kStages * STAGE_BYTES];
   __shared__ float act_amax[2][BM];  // per-row amax of each wave column's 64 act columns
   __shared__ int prefix[kMaxExperts + 1];
@@ -131,7 +146,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
   int round = 0;
   int tile = tile_at(0);
   if (tile >= total) return;
-  Tile ct = describe(prefix, offsets, experts, n_tiles, tile, nk);
+  Tile ct = describe(prefix, offsets, experts, n_tiles, tile, nk, n_group, rotate);
   issue(ct, 0, 0);
   int stage = 0;
   for (;;) {
@@ -195,7 +210,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       if (kb + 1 < nk) {
         issue(ct, kb + 1, stage ^ 1);
       } else if (next_tile < total) {
-        const Tile nt = describe(prefix, offsets, experts, n_tiles, next_tile, nk);
+        const Tile nt = describe(prefix, offsets, experts, n_tiles, next_tile, nk, n_group, rotate);
         issue(nt, 0, stage ^ 1);
       }
       const uint8_t* base = smem + stage * STAGE_BYTES;
@@ -387,7 +402,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     if (next_tile >= total) break;
     ++round;
     tile = next_tile;
-    ct = describe(prefix, offsets, experts, n_tiles, tile, nk);
+    ct = describe(prefix, offsets, experts, n_tiles, tile, nk, n_group, rotate);
   }
 }
 
@@ -407,6 +422,23 @@ int cu_count() {
 
 }  // namespace
 
+// Tile order by the size of one expert's weight (N x K bytes). Up to a few
+// L2s' worth, tiles go row-block-major with the K rotation: an XCD's CUs
+// sweep one row block's N tiles, and the whole weight stays cached across
+// row blocks. Beyond that, each row block would stream the weight again
+// from HBM, so tiles go in groups of 8 N tiles x all the expert's row
+// blocks, unrotated, and the CUs that share a weight panel read it
+// together. Measured on MI355X: Mixtral's four GEMMs (58-117 MB per
+// expert) +6-14%, DeepSeek-shard up/dgrad-up (29 MB) +5-7%; the 3-15 MB
+// weights of the other shapes lose 1-7% in that order.
+struct Order {
+  int n_group, rotate;
+};
+Order tile_order(int n, int k) {
+  if ((size_t)n * (size_t)k >= ((size_t)24 << 20)) return {8, 0};
+  return {0, 1};
+}
+
 // Launches the pipelined kernel; returns 1 if the shape is not its form
 // (N % 256 != 0), in which case the caller uses the general kernel.
 int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, const uint8_t* w,
@@ -417,11 +449,13 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
   if (n % BN != 0 || experts > kMaxExperts || (interleave && (n / 2) % 128 != 0)) return 1;
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   const int grid = upper < cu_count() ? upper : cu_count();
+  const Order order = tile_order(n, k);
   auto launch = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream, a, a_scale,
                        rows, w, w_scale, w_scale_t, experts, n, k, offsets, interleave,
                        (const uint16_t*)addend, (uint16_t*)out, act_q, act_scales, limit,
-                       (const uint16_t*)lora_z, (const uint16_t*)lora_b, lora_rank);
+                       (const uint16_t*)lora_z, (const uint16_t*)lora_b, lora_rank,
+                       order.n_group, order.rotate);
   };
   if (lora_z != nullptr) {
     if (act_q != nullptr || addend != nullptr) return 1;  // not a form of this kernel
@@ -446,11 +480,13 @@ int mi355x_gemm_v2_rowwise_launch(const uint8_t* a, const float* a_scale, int ro
   if (n % BN != 0 || experts > kMaxExperts) return 1;
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   const int grid = upper < cu_count() ? upper : cu_count();
+  const Order order = tile_order(n, k);
   auto launch = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream, a, a_scale,
                        rows, w, w_scale, 0, experts, n, k, offsets, 0, (const uint16_t*)nullptr,
                        (uint16_t*)out, (uint8_t*)nullptr, (float*)nullptr, 0.0f,
-                       (const uint16_t*)lora_z, (const uint16_t*)lora_b, lora_rank);
+                       (const uint16_t*)lora_z, (const uint16_t*)lora_b, lora_rank,
+                       order.n_group, order.rotate);
   };
   if (lora_z != nullptr) launch(grouped_gemm_v2_kernel<false, false, true, true>);
   else launch(grouped_gemm_v2_kernel<false, false, false, true>);
