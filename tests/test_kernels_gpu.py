@@ -296,6 +296,55 @@ def test_grouped_gemm_baseline_config2_sampled(device):
         assert max_rel(out[sample], want) < 1e-2, e
 
 
+@pytest.mark.parametrize("interleave", [False, True])
+def test_grouped_gemm_large_weight_tile_order(device, interleave):
+    """Experts whose weight is 24 MB or more (N x K e4m3 bytes) run in the
+    grouped tile order: 8 N tiles x all the expert's row blocks, unrotated.
+    N = 6400 gives groups of 8, 8, 8 and 1 N tiles; an empty expert and
+    partial row blocks are included. Every output element is checked
+    against the dequantized oracle operands multiplied in fp32."""
+    counts, n, k = [300, 0, 520, 45], 6400, 4096
+    assert n * k >= 24 << 20
+    g = torch.Generator().manual_seed(17)
+    offsets = _ragged(counts)
+    rows = int(offsets[-1])
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16).to(device)
+    w = (torch.randn(len(counts), n, k, generator=g) * 0.02).to(torch.bfloat16).to(device)
+    xq, xs = K.quantize_rows(x)
+    wq, ws = K.quantize_weight_blocks(w)
+    out = K.gemm(xq, xs, wq, ws, offsets.to(device), interleave=interleave)
+    a = O.dequantize_rows(xq.cpu(), xs.cpu()).float().to(device)
+    for e, count in enumerate(counts):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi == lo:
+            continue
+        wd = O.dequantize_blocks(wq[e:e + 1].cpu(), ws[e:e + 1].cpu())[0].float().to(device)
+        want = a[lo:hi] @ wd.t()
+        if interleave:  # output columns 2j, 2j + 1 = gate j, up j
+            want = want.view(hi - lo, 2, n // 2).transpose(1, 2).reshape(hi - lo, n)
+        assert max_rel(out[lo:hi].float(), want) < 1e-2, e
+
+
+def test_rowwise_gemm_large_weight_tile_order(device):
+    """The row-scaled kernel in the grouped tile order (same shape rule)."""
+    counts, n, k = [0, 260, 700], 6400, 4096
+    g = torch.Generator().manual_seed(19)
+    offsets = _ragged(counts)
+    rows = int(offsets[-1])
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16).to(device)
+    w = (torch.randn(len(counts), n, k, generator=g) * 0.02).to(torch.bfloat16).to(device)
+    xq, xs = K.quantize_rows_current(x)
+    wq, _, wsc, _ = K.quantize_weights_current(w)
+    out = K.gemm_rowwise(xq, xs, wq, wsc, offsets.to(device))
+    a = xq.float() * xs[:, None]
+    for e, count in enumerate(counts):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi == lo:
+            continue
+        want = a[lo:hi] @ (wq[e].float() * wsc[e][:, None]).t()
+        assert max_rel(out[lo:hi].float(), want) < 1e-2, e
+
+
 # (256, 384): general kernel; (512, 768): the pipelined hardware-scaled one.
 @pytest.mark.parametrize("features", [(256, 384), (512, 768)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
