@@ -9,7 +9,15 @@
 // values of its row or factor column), keep 4 K steps (8 at rank 16) of
 // loads in flight, and meet in LDS. A 16-row block that spans an expert boundary is run once
 // per expert present, storing only that expert's rows.
-#include "common.h"
+//
+// That register-operand form loads in the MFMA operand layout: a 16-lane
+// quarter-wave reads 16 rows x 16 bytes, so each load instruction touches
+// 16 cache lines at half use, and every wave reloads the factor. For K a
+// multiple of 128 the staged form below is used instead: rows and factor
+// are copied to LDS with direct loads (16 lanes per 256-byte row slice, so
+// whole lines), three stages deep, and each wave reads its MFMA fragments
+// from there.
+#include "gemm_pipe.h"
 
 namespace {
 
@@ -111,6 +119,94 @@ __global__ void __launch_bounds__(64 * kRankWaves) rank_product_kernel(
   }
 }
 
+// Staged form: a block of 2 waves takes 32 rows, a wave 16 rows over all of
+// K, in chunks of 128 K (256 bytes per row). A chunk's row slices and the
+// factor's R slices go to LDS with direct loads; chunk c of a row r sits at
+// 16-byte position c ^ (r % 16), so the 16 rows of a fragment read fall in
+// distinct banks. R is a template parameter so that each wave's loads per
+// stage, 4 + R / 8, is a compile-time count for the wait.
+constexpr int kStRows = 32;
+constexpr int kStSlice = 256;  // bytes of one row per K chunk
+constexpr int kStStages = 3;
+
+template <int R>
+__global__ void __launch_bounds__(128) rank_product_staged_kernel(
+    const uint16_t* __restrict__ a, int rows, int K, const uint16_t* __restrict__ bt,
+    const int32_t* __restrict__ offsets, int experts, uint16_t* __restrict__ out) {
+  constexpr int A_BYTES = kStRows * kStSlice;              // 8 KB
+  constexpr int B_BYTES = R * kStSlice;                    // 4-16 KB
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int A_PER_WAVE = A_BYTES / 1024 / 2, B_PER_WAVE = B_BYTES / 1024 / 2;
+  constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;           // direct loads per wave per stage
+  __shared__ __align__(1024) uint8_t smem[kStStages * STAGE];
+  const int row0 = blockIdx.x * kStRows;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
+  const int last = min(row0 + kStRows - 1, rows - 1);
+  const int e_lo = __builtin_amdgcn_readfirstlane(expert_of(offsets, experts, row0));
+  const int e_hi = __builtin_amdgcn_readfirstlane(expert_of(offsets, experts, last));
+  const int nch = K / 128;
+  const uint32_t pitch = (uint32_t)K * 2u;
+  // Slice position of this lane's 16 bytes and the 16-byte chunk it holds.
+  const int pos = lane & 15;
+  for (int e = e_lo; e <= e_hi; ++e) {
+    if (offsets[e + 1] <= offsets[e]) continue;  // an empty expert inside the block's span
+    const uint8_t* fbase = (const uint8_t*)(bt + (size_t)e * R * K);
+    auto issue = [&](int ch, int st) {
+      uint8_t* base = smem + st * STAGE;
+      const uint8_t* ab = (const uint8_t*)a + (size_t)ch * kStSlice;
+      const uint8_t* bb = fbase + (size_t)ch * kStSlice;
+#pragma unroll
+      for (int i = 0; i < A_PER_WAVE; ++i) {  // 4 rows per copy
+        const int j = wave * A_PER_WAVE + i, r = j * 4 + (lane >> 4);
+        const uint32_t src = (uint32_t)min(row0 + r, rows - 1) * pitch + 16u * (uint32_t)(pos ^ (r & 15));
+        pipe::dma16(ab, src, base + j * 1024);
+      }
+#pragma unroll
+      for (int i = 0; i < B_PER_WAVE; ++i) {
+        const int j = wave * B_PER_WAVE + i, r = j * 4 + (lane >> 4);
+        const uint32_t src = (uint32_t)r * pitch + 16u * (uint32_t)(pos ^ (r & 15));
+        pipe::dma16(bb, src, base + A_BYTES + j * 1024);
+      }
+    };
+    v4f acc[R / 16];
+#pragma unroll
+    for (int c = 0; c < R / 16; ++c) acc[c] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
+    issue(0, 0);
+    if (nch > 1) issue(1, 1);
+    for (int ch = 0; ch < nch; ++ch) {
+      // This chunk's copies; the next chunk's may stay in flight.
+      if (ch + 1 < nch) pipe::wait_and_sync<LOADS>();
+      else pipe::wait_and_sync<0>();
+      // Into the stage every wave finished reading before this barrier.
+      if (ch + 2 < nch) issue(ch + 2, (ch + 2) % kStStages);
+      const uint8_t* ta = smem + (ch % kStStages) * STAGE;
+      const uint8_t* tb = ta + A_BYTES;
+      const int ar = wave * 16 + (lane & 15);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int c = ks * 4 + (lane >> 4);  // this lane's 8 K values of the 32-K step
+        const int at = (c ^ (lane & 15)) * 16;
+        const bf16x8_t af = *(const bf16x8_t*)(ta + ar * kStSlice + at);
+#pragma unroll
+        for (int cb = 0; cb < R / 16; ++cb) {
+          const bf16x8_t bf = *(const bf16x8_t*)(tb + (cb * 16 + (lane & 15)) * kStSlice + at);
+          acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf, acc[cb], 0, 0, 0);
+        }
+      }
+    }
+    // acc[cb][i] is row 4 * (lane / 16) + i of the wave's 16, column cb * 16 + lane % 16.
+    const int lo = max(offsets[e], row0), hi = min(offsets[e + 1], row0 + kStRows);
+#pragma unroll
+    for (int cb = 0; cb < R / 16; ++cb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = row0 + wave * 16 + 4 * (lane >> 4) + i;
+        if (r >= lo && r < hi) out[(size_t)r * R + cb * 16 + (lane & 15)] = f32_to_bf16(acc[cb][i]);
+      }
+    __syncthreads();  // the stages are refilled for the next expert
+  }
+}
+
 }  // namespace
 
 extern "C" int mi355x_rank_product(const void* a, int rows, int k, const void* bt, int rank,
@@ -120,6 +216,24 @@ extern "C" int mi355x_rank_product(const void* a, int rows, int k, const void* b
                  "rank_product: rank must be a multiple of 16 up to %d, got %d", kMaxRank, rank);
   MI355X_REQUIRE(experts > 0, "rank_product: experts must be positive");
   if (rows == 0) return MI355X_OK;
+  // The staged form: K in 128-wide chunks, and per-lane 32-bit byte offsets
+  // into the rows and the factor.
+  if (k % 128 == 0 && (uint64_t)rows * (uint64_t)k * 2u < (1ull << 32) &&
+      (uint64_t)rank * (uint64_t)k * 2u < (1ull << 32)) {
+    const dim3 grid((rows + kStRows - 1) / kStRows);
+    auto launch = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, grid, dim3(128), 0, (hipStream_t)stream, (const uint16_t*)a, rows,
+                         k, (const uint16_t*)bt, offsets, experts, (uint16_t*)out);
+    };
+    switch (rank) {
+      case 16: launch(rank_product_staged_kernel<16>); break;
+      case 32: launch(rank_product_staged_kernel<32>); break;
+      case 48: launch(rank_product_staged_kernel<48>); break;
+      default: launch(rank_product_staged_kernel<64>); break;
+    }
+    MI355X_LAUNCH_CHECK();
+    return MI355X_OK;
+  }
   hipLaunchKernelGGL(rank_product_kernel, dim3((rows + 15) / 16), dim3(64 * kRankWaves), 0,
                      (hipStream_t)stream, (const uint16_t*)a, rows, k, (const uint16_t*)bt, rank,
                      offsets, experts, (uint16_t*)out);

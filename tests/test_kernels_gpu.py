@@ -479,7 +479,9 @@ def test_gemm_swiglu_fused_matches_separate_pass(device, limit, inter):
 @pytest.mark.parametrize("counts,k,rank", [
     ([0, 37, 5, 0, 150, 16], 512, 16),   # empty experts, blocks spanning boundaries
     ([300, 1, 200], 1536, 32),
-    ([64], 96, 48),
+    ([64], 96, 48),                      # K % 128 != 0: the register-operand form
+    ([64, 129, 0, 31], 384, 48),         # the LDS-staged form at each rank
+    ([1000, 0, 33, 700], 1024, 64),
 ])
 def test_rank_product_matches_fp32(device, counts, k, rank):
     g = torch.Generator().manual_seed(sum(counts) + k)
