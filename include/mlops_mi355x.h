@@ -201,6 +201,19 @@ int mi355x_swiglu_bwd_quantize(const void* r, const void* h, const float* weight
                                uint8_t* ap_t, float* ap_t_scales, float* dscore,
                                void* workspace, size_t workspace_bytes, void* stream);
 
+/* mi355x_swiglu_bwd_quantize with bf16 dh [rows, 2I] in h's interleaved
+ * order (2j = gate j, 2j + 1 = up j) in place of dhq / dh_scales, the
+ * values mi355x_routed_swiglu_bwd writes; dh_t / ap_t and dscore as there.
+ * The fp8_current backward needs dh in bf16 for its per-row quantizer
+ * (quantize_rows.py:35-207) and the transposed operands for the weight
+ * gradients (sonicmoe/moe.py:346-358, 408-419); this is one read of r and h
+ * for all three instead of the SwiGLU backward plus two transposing passes. */
+int mi355x_swiglu_bwd_bf16(const void* r, const void* h, const float* weights,
+                           const int32_t* order, const int32_t* row_blocks, int rows, int width,
+                           int padded, float limit, void* dh, uint8_t* dh_t, float* dh_t_scales,
+                           uint8_t* ap_t, float* ap_t_scales, float* dscore, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------- GEMMs ---- */
 
 /* Ragged grouped block-FP8 GEMM, fp8 MFMA with fp32 accumulation:

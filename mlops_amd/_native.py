@@ -50,6 +50,10 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _P, _S, _P],
     ),
+    "mi355x_swiglu_bwd_bf16": (
+        _I,
+        [_P, _P, _P, _P, _P, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _S, _P],
+    ),
     "mi355x_gemm_fp8_block": (
         _I,
         [_P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _P],

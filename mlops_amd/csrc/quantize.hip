@@ -494,7 +494,7 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
     const int32_t* __restrict__ row_blocks, int rows, int width, int padded, float limit,
     uint8_t* __restrict__ dhq, float* __restrict__ dhs, uint8_t* __restrict__ dht,
     float* __restrict__ dhts, uint8_t* __restrict__ apt, float* __restrict__ apts,
-    float* __restrict__ dsp) {
+    float* __restrict__ dsp, uint16_t* __restrict__ dh) {
   // dgate and dup tiles (a' is staged through tile 0 afterwards): ~74 KB,
   // two blocks per CU.
   __shared__ __align__(16) uint16_t tiles[2][128 * kQtPitch];
@@ -574,6 +574,22 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
                       pack_bf16x2(du[4], du[5]), pack_bf16x2(du[6], du[7]));
       oa = make_uint4(pack_bf16x2(ap[0], ap[1]), pack_bf16x2(ap[2], ap[3]),
                       pack_bf16x2(ap[4], ap[5]), pack_bf16x2(ap[6], ap[7]));
+      dot = group_sum<16>(dot);
+      if (lane16 == 0) dsp[(size_t)cb * rows + row] = dot;
+      if (dh != nullptr) {
+        // bf16 dh in h's interleaved order (2j' = gate j', 2j' + 1 = up j').
+        const uint32_t g4[4] = {og.x, og.y, og.z, og.w}, u4[4] = {ou.x, ou.y, ou.z, ou.w};
+        uint32_t wv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t gb = (g4[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+          const uint32_t ub = (u4[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+          wv[i] = gb | (ub << 16);
+        }
+        uint16_t* dp = dh + (size_t)row * 2 * width + 2 * j;
+        *(uint4*)dp = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+        *(uint4*)(dp + 8) = make_uint4(wv[4], wv[5], wv[6], wv[7]);
+      } else {
       // Row quantization of the bf16 values (gate-first 1x128 layout).
       float gq[8], uq[8];
       unpack_bf16x8(og, gq);
@@ -586,14 +602,13 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
       }
       ga = group_max<16>(ga);
       ua = group_max<16>(ua);
-      dot = group_sum<16>(dot);
       const float sg = fmaxf(ga * kInv448, kMinScale), su = fmaxf(ua * kInv448, kMinScale);
       *(uint2*)(dhq + (size_t)row * 2 * width + j) = quant8(gq, sg);
       *(uint2*)(dhq + (size_t)row * 2 * width + width + j) = quant8(uq, su);
       if (lane16 == 0) {
         dhs[(size_t)cb * rows + row] = sg;
         dhs[(size_t)(nblk + cb) * rows + row] = su;
-        dsp[(size_t)cb * rows + row] = dot;
+      }
       }
     }
     *(uint4*)&tiles[0][rr * kQtPitch + jl] = og;
@@ -760,13 +775,12 @@ extern "C" size_t mi355x_swiglu_bwd_quantize_workspace_size(int rows, int width)
   return (size_t)rows * (size_t)(width / 128) * sizeof(float);
 }
 
-extern "C" int mi355x_swiglu_bwd_quantize(const void* r, const void* h, const float* weights,
-                                          const int32_t* order, const int32_t* row_blocks,
-                                          int rows, int width, int padded, float limit,
-                                          uint8_t* dhq, float* dh_scales, uint8_t* dh_t,
-                                          float* dh_t_scales, uint8_t* ap_t, float* ap_t_scales,
-                                          float* dscore, void* workspace, size_t workspace_bytes,
-                                          void* stream) {
+namespace {
+int swiglu_bwd_launch(const void* r, const void* h, const float* weights, const int32_t* order,
+                      const int32_t* row_blocks, int rows, int width, int padded, float limit,
+                      uint8_t* dhq, float* dh_scales, void* dh, uint8_t* dh_t, float* dh_t_scales,
+                      uint8_t* ap_t, float* ap_t_scales, float* dscore, void* workspace,
+                      size_t workspace_bytes, void* stream) {
   MI355X_REQUIRE(width > 0 && width % 128 == 0, "swiglu_bwd_quantize: I must be a multiple of 128");
   MI355X_REQUIRE(padded >= 0 && padded % 128 == 0 && (size_t)padded >= (size_t)rows,
                  "swiglu_bwd_quantize: padded must be a multiple of 128 covering the rows");
@@ -781,10 +795,36 @@ extern "C" int mi355x_swiglu_bwd_quantize(const void* r, const void* h, const fl
   hipLaunchKernelGGL(swiglu_bwd_quantize_kernel, dim3(padded / 128, width / 128), dim3(kSbThreads),
                      0, s, (const uint16_t*)r, (const uint16_t*)h, weights, order, row_blocks,
                      rows, width, padded, limit, dhq, dh_scales, dh_t, dh_t_scales, ap_t,
-                     ap_t_scales, dsp);
+                     ap_t_scales, dsp, (uint16_t*)dh);
   MI355X_LAUNCH_CHECK();
   hipLaunchKernelGGL(dscore_reduce_kernel, dim3((rows + 255) / 256), dim3(256), 0, s, dsp, rows,
                      width / 128, dscore);
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
+}
+}  // namespace
+
+extern "C" int mi355x_swiglu_bwd_quantize(const void* r, const void* h, const float* weights,
+                                          const int32_t* order, const int32_t* row_blocks,
+                                          int rows, int width, int padded, float limit,
+                                          uint8_t* dhq, float* dh_scales, uint8_t* dh_t,
+                                          float* dh_t_scales, uint8_t* ap_t, float* ap_t_scales,
+                                          float* dscore, void* workspace, size_t workspace_bytes,
+                                          void* stream) {
+  MI355X_REQUIRE(dhq != nullptr && dh_scales != nullptr, "swiglu_bwd_quantize: dhq is required");
+  return swiglu_bwd_launch(r, h, weights, order, row_blocks, rows, width, padded, limit, dhq,
+                           dh_scales, nullptr, dh_t, dh_t_scales, ap_t, ap_t_scales, dscore,
+                           workspace, workspace_bytes, stream);
+}
+
+extern "C" int mi355x_swiglu_bwd_bf16(const void* r, const void* h, const float* weights,
+                                      const int32_t* order, const int32_t* row_blocks, int rows,
+                                      int width, int padded, float limit, void* dh, uint8_t* dh_t,
+                                      float* dh_t_scales, uint8_t* ap_t, float* ap_t_scales,
+                                      float* dscore, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+  MI355X_REQUIRE(dh != nullptr, "swiglu_bwd_bf16: dh is required");
+  return swiglu_bwd_launch(r, h, weights, order, row_blocks, rows, width, padded, limit, nullptr,
+                           nullptr, dh, dh_t, dh_t_scales, ap_t, ap_t_scales, dscore, workspace,
+                           workspace_bytes, stream);
 }

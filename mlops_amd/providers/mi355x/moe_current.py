@@ -139,17 +139,21 @@ def backward_routed(grad_output, grad_aux, grad_probability_sum, h2, router_weig
             dy = dy.to(torch.bfloat16)
         dyq, dys = kernels.permute_quantize_current(dy, slots)
         r = kernels.gemm_rowwise(dyq, dys, w2[1], w2[3], offsets)
-        dh, a_prime, dscore = kernels.routed_swiglu_backward(
-            r, h13, route_weights.reshape(-1), order, swiglu_limit)
         if need_w2 or need_w13:
+            # One pass for bf16 dh and the transposed dh and a' of the weight
+            # gradients (equal to the SwiGLU backward then quantize_transpose).
             padded = kernels.wgrad_padded_rows(assignments, experts)
             blocks = kernels.padded_row_blocks(offsets, padded)
+            dh, dh_t, dh_ts, ap_t, ap_ts, dscore = kernels.swiglu_bwd_bf16(
+                r, h13, route_weights.reshape(-1), order, offsets, padded=padded,
+                row_blocks=blocks, limit=swiglu_limit)
+        else:
+            dh, _, dscore = kernels.routed_swiglu_backward(
+                r, h13, route_weights.reshape(-1), order, swiglu_limit)
         if need_w2:
             dy_t, dy_ts, _ = kernels.quantize_transpose(
                 dy, offsets, assignments, gather=order, gather_div=int(top_k), padded=padded,
                 row_blocks=blocks)
-            ap_t, ap_ts, _ = kernels.quantize_transpose(
-                a_prime, offsets, assignments, padded=padded, row_blocks=blocks)
             grad_w2 = fused._grad_at(
                 kernels.wgrad(dy_t, dy_ts, ap_t, ap_ts, offsets, out_dtype=direct,
                               rows=assignments), expert_dtype)
@@ -158,8 +162,6 @@ def backward_routed(grad_output, grad_aux, grad_probability_sum, h2, router_weig
         dhq, dhs = kernels.quantize_rows_current(dh)
         dx = kernels.gemm_rowwise(dhq, dhs, w13[1], w13[3], offsets)
         if need_w13:
-            dh_t, dh_ts, _ = kernels.quantize_transpose(
-                dh, offsets, assignments, gate_up=True, padded=padded, row_blocks=blocks)
             x_t, x_ts, _ = kernels.quantize_transpose(
                 x, offsets, assignments, gather=order, gather_div=int(top_k), padded=padded,
                 row_blocks=blocks)

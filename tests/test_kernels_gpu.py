@@ -437,6 +437,18 @@ def test_swiglu_bwd_quantize_matches_unfused(device, limit):
         r, h, weights, order_d, offsets_d, limit=limit, transposed_dh=False, transposed_ap=False)
     assert dht2 is None and apt2 is None
     assert torch.equal(_bytes(dhq2), _bytes(dhq)) and torch.equal(dhs2, dhs)
+    # The bf16 form (fp8_current's backward): dh exactly as the routed SwiGLU
+    # backward writes it (h's interleaved order), the same transposed
+    # operands and dscore.
+    blocks = K.padded_row_blocks(offsets_d, padded)
+    dh3, dht3, dhts3, apt3, apts3, ds3 = K.swiglu_bwd_bf16(
+        r, h, weights, order_d, offsets_d, padded=padded, row_blocks=blocks, limit=limit)
+    assert torch.equal(dh3, dh)
+    assert torch.equal(_bytes(dht3)[:, :total], _bytes(t_ref)[:, :total])
+    assert torch.equal(dhts3[: total // 128], ts_ref[: total // 128])
+    assert torch.equal(_bytes(apt3)[:, :total], _bytes(a_ref)[:, :total])
+    assert torch.equal(apts3[: total // 128], as_ref[: total // 128])
+    assert torch.equal(ds3, ds_ref)
 
 
 def test_padded_row_blocks_table(device):
