@@ -431,6 +431,7 @@ int cu_count() {
 // together. Measured on MI355X: Mixtral's four GEMMs (58-117 MB per
 // expert) +6-14%, DeepSeek-shard up/dgrad-up (29 MB) +5-7%; the 3-15 MB
 // weights of the other shapes lose 1-7% in that order.
+namespace {
 struct Order {
   int n_group, rotate;
 };
@@ -438,6 +439,7 @@ Order tile_order(int n, int k) {
   if ((size_t)n * (size_t)k >= ((size_t)24 << 20)) return {8, 0};
   return {0, 1};
 }
+}  // namespace
 
 // Launches the pipelined kernel; returns 1 if the shape is not its form
 // (N % 256 != 0), in which case the caller uses the general kernel.
