@@ -202,35 +202,49 @@ __global__ void __launch_bounds__(256) router_stats_partial_kernel(
   const int per_lane = (experts + 63) / 64;
   float acc[kMaxPerLane];
   _Pragma("unroll") for (int i = 0; i < kMaxPerLane; ++i) acc[i] = 0.0f;
-  for (int t = start + wave; t < end; t += 4) {
-    const float* row = logits + (size_t)t * experts;
-    float l[kMaxPerLane];
-    SLOTS(i) {
-      int e = lane + 64 * i;
-      l[i] = e < experts ? row[e] : -INFINITY;
-    }
-    if (mode == MI355X_ROUTE_SIGMOID_NOAUX_TC) {
-      float s = 0.0f;
+  // The wave's tokens t = start + wave + 4u, four at a time: the four rows'
+  // logits and route ids are loaded before any of them is used, then the
+  // tokens are summed in order (the same order as one at a time).
+  constexpr int kBatch = 4;
+  for (int t0 = start + wave; t0 < end; t0 += 4 * kBatch) {
+    float l[kBatch][kMaxPerLane];
+    int id[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int t = t0 + 4 * u;
+      const float* row = logits + (size_t)t * experts;
       SLOTS(i) {
         int e = lane + 64 * i;
-        l[i] = e < experts ? sigmoid_f(l[i]) : 0.0f;
-        s += l[i];
+        l[u][i] = (t < end && e < experts) ? row[e] : -INFINITY;
       }
-      s = wave_sum(s);
-      SLOTS(i) acc[i] += l[i] / s;
-    } else {
-      float m = -INFINITY;
-      SLOTS(i) m = fmaxf(m, l[i]);
-      m = wave_max(m);
-      float s = 0.0f;
-      SLOTS(i) {
-        l[i] = (lane + 64 * i) < experts ? __expf(l[i] - m) : 0.0f;
-        s += l[i];
-      }
-      s = wave_sum(s);
-      SLOTS(i) acc[i] += l[i] / s;
+      id[u] = (t < end && lane < top_k) ? ids[(size_t)t * top_k + lane] : -1;
     }
-    if (lane < top_k) atomicAdd(&counts[ids[(size_t)t * top_k + lane]], 1);
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (t0 + 4 * u >= end) break;  // wave-uniform
+      if (mode == MI355X_ROUTE_SIGMOID_NOAUX_TC) {
+        float s = 0.0f;
+        SLOTS(i) {
+          int e = lane + 64 * i;
+          l[u][i] = e < experts ? sigmoid_f(l[u][i]) : 0.0f;
+          s += l[u][i];
+        }
+        s = wave_sum(s);
+        SLOTS(i) acc[i] += l[u][i] / s;
+      } else {
+        float m = -INFINITY;
+        SLOTS(i) m = fmaxf(m, l[u][i]);
+        m = wave_max(m);
+        float s = 0.0f;
+        SLOTS(i) {
+          l[u][i] = (lane + 64 * i) < experts ? __expf(l[u][i] - m) : 0.0f;
+          s += l[u][i];
+        }
+        s = wave_sum(s);
+        SLOTS(i) acc[i] += l[u][i] / s;
+      }
+      if (id[u] >= 0) atomicAdd(&counts[id[u]], 1);
+    }
   }
   SLOTS(i) {
     int e = lane + 64 * i;
@@ -333,6 +347,8 @@ __global__ void __launch_bounds__(kReduceThreads) router_stats_reduce_kernel(
     int sc = 0;
     if (pair < pairs) {
       const int seg = pair / experts, e = pair % experts;
+      // Unrolled so the loads run ahead of the in-order sums.
+#pragma unroll 8
       for (int c = seg_start[seg] + part; c < seg_start[seg + 1]; c += G) {
         sp += part_p[(size_t)c * experts + e];
         sc += part_c[(size_t)c * experts + e];
