@@ -92,6 +92,19 @@ int mi355x_permute_plan(const int32_t* ids, int assignments, int experts, int64_
                         int32_t* offsets, int32_t* order, int32_t* slots, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of mi355x_permute_plan, with the same outputs. It
+ * has no counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Its histogram scratch is a fixed 4 MiB file-scope
+ * device array, one per GPU, held until the process ends, so it never calls
+ * hipMalloc/hipFree. Sizes beyond that scratch (chunks of 4096 assignments x
+ * experts above 2^20 - 64 int32) are refused with MI355X_EINVAL;
+ * mi355x_permute_plan_noalloc_max_assignments(E) gives the largest A for E.
+ * Calls that overlap on one GPU share the scratch and race. */
+size_t mi355x_permute_plan_noalloc_max_assignments(int experts);
+int mi355x_permute_plan_noalloc(const int32_t* ids, int assignments, int experts, int64_t* counts,
+                                int32_t* offsets, int32_t* order, int32_t* slots, void* stream);
+
 /* Dispatch + quantize: token rows x bf16 [T,H] read once, written as e4m3 to
  * each of their k routed rows slots[t,j] with one fp32 descale per 1x128
  * block: s = max(amax * (1/448), 1e-12), q = e4m3(clip(x / s, +-448)).

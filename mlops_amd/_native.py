@@ -34,6 +34,8 @@ SIGNATURES = {
     ),
     "mi355x_permute_plan_workspace_size": (_S, [_I, _I]),
     "mi355x_permute_plan": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _S, _P]),
+    "mi355x_permute_plan_noalloc_max_assignments": (_S, [_I]),
+    "mi355x_permute_plan_noalloc": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
     "mi355x_permute_quantize_fp8": (_I, [_P, _I, _I, _I, _P, _P, _P, _P]),
     "mi355x_quantize_rows_fp8": (_I, [_P, _I, _I, _I64, _I, _P, _P, _P]),
     "mi355x_swiglu_quantize_fp8": (_I, [_P, _I, _I, _F, _P, _P, _P, _P]),

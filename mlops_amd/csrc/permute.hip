@@ -1,6 +1,8 @@
 // Token permutation: the stable counting sort that groups routed rows by
 // expert, the dispatch that quantizes each token once and writes its k routed
 // copies, and the token-parallel combine / token-sum of the way back.
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -209,6 +211,39 @@ __global__ void __launch_bounds__(256) combine_kernel(
   }
 }
 
+// ------------------------------------------------ allocation-free variant
+// The plan's only scratch is the per-chunk histogram (chunks x experts int32).
+// The allocation-free entry point keeps it in this file-scope device array, one
+// copy per GPU, held until the process ends. The histogram pass writes every
+// entry the later passes read, so nothing needs clearing between calls; calls
+// that overlap on one GPU share the array and race.
+constexpr size_t kPlanScratchInts = size_t(1) << 20;  // 4 MiB
+__device__ __align__(256) int32_t scratch[kPlanScratchInts];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+int32_t* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this GPU's copy of `scratch`, looked up once per device
+// with that device current. The array's name is only a host-side stand-in and
+// is never passed to a kernel or a copy.
+int plan_scratch(int32_t** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  MI355X_REQUIRE(e == hipSuccess && dev >= 0 && dev < kMaxDevices,
+                 "permute_plan_noalloc: no current device (%s)", hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    MI355X_REQUIRE(e == hipSuccess && p != nullptr,
+                   "permute_plan_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = (int32_t*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MI355X_OK;
+}
+
 }  // namespace
 
 extern "C" size_t mi355x_permute_plan_workspace_size(int assignments, int experts) {
@@ -242,6 +277,33 @@ extern "C" int mi355x_permute_plan(const int32_t* ids, int assignments, int expe
     MI355X_LAUNCH_CHECK();
   }
   return MI355X_OK;
+}
+
+extern "C" size_t mi355x_permute_plan_noalloc_max_assignments(int experts) {
+  if (experts <= 0 || experts > kMaxExperts) return 0;
+  // the plan needs ceil(A / chunk) * experts ints plus 256 bytes of slack
+  const size_t chunks = (kPlanScratchInts - 64) / (size_t)experts;
+  return chunks * (size_t)kPlanChunk;
+}
+
+extern "C" int mi355x_permute_plan_noalloc(const int32_t* ids, int assignments, int experts,
+                                           int64_t* counts, int32_t* offsets, int32_t* order,
+                                           int32_t* slots, void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= kMaxExperts,
+                 "permute_plan_noalloc: experts must be in [1, %d]", kMaxExperts);
+  MI355X_REQUIRE(assignments >= 0, "permute_plan_noalloc: negative assignments");
+  const size_t need = mi355x_permute_plan_workspace_size(assignments, experts);
+  const size_t have = kPlanScratchInts * sizeof(int32_t);
+  MI355X_REQUIRE(need <= have,
+                 "permute_plan_noalloc: %d assignments x %d experts need %zu scratch bytes, "
+                 "above the fixed %zu (at most %zu assignments at this expert count)",
+                 assignments, experts, need, have,
+                 mi355x_permute_plan_noalloc_max_assignments(experts));
+  int32_t* hist = nullptr;
+  const int rc = plan_scratch(&hist);
+  if (rc != MI355X_OK) return rc;
+  return mi355x_permute_plan(ids, assignments, experts, counts, offsets, order, slots, hist, have,
+                             stream);
 }
 
 extern "C" int mi355x_permute_quantize_fp8(const void* x, int tokens, int width, int top_k,
