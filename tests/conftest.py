@@ -38,3 +38,20 @@ def frob_rel(actual, expected):
     a = actual.double().cpu()
     e = expected.double().cpu()
     return float((a - e).norm() / e.norm().clamp_min(1e-30))
+
+
+def worst_cell_rel(actual, expected, row_bounds, block=128):
+    """Largest relative Frobenius error over the output's cells: the rows of
+    each group (between consecutive ``row_bounds``) by each ``block``-column
+    slice; empty groups are skipped. This is the reference's GEMM metric
+    (tests/test_block_fp8_transpose_gemm.py:390-406)."""
+    a = actual.double().cpu().reshape(-1, actual.shape[-1])
+    e = expected.double().cpu().reshape(-1, expected.shape[-1])
+    worst = 0.0
+    for lo, hi in zip(row_bounds[:-1], row_bounds[1:]):
+        if hi <= lo:
+            continue
+        for col in range(0, e.shape[1], block):
+            ac, ec = a[lo:hi, col:col + block], e[lo:hi, col:col + block]
+            worst = max(worst, float((ac - ec).norm() / ec.norm().clamp_min(1e-6)))
+    return worst

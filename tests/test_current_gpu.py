@@ -28,7 +28,7 @@ from mlops_amd import kernels as K
 from mlops_amd.dispatch import use_implementation, weight_gradients_at
 from mlops_amd.explicit import moe as explicit
 from oracle import moe_oracle as O
-from tests.conftest import frob_rel, max_rel
+from tests.conftest import frob_rel, max_rel, worst_cell_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -149,6 +149,7 @@ def test_gemm_rowwise_matches_fp64(device, counts, n, k):
         lo, hi = int(offsets[e]), int(offsets[e + 1])
         if hi > lo:
             assert max_rel(out[lo:hi].double(), want[lo:hi]) < 1e-2, e
+    assert worst_cell_rel(out, want, offsets.tolist()) < 1e-2
     # The input-gradient orientation: rows [rows, N] against the transposed copy.
     y = torch.randn(rows, n, generator=g).to(torch.bfloat16)
     yq, ys = K.quantize_rows_current(y.to(device))

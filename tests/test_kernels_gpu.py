@@ -14,7 +14,7 @@ import torch
 
 from mlops_amd import kernels as K
 from oracle import moe_oracle as O
-from tests.conftest import frob_rel, max_rel
+from tests.conftest import frob_rel, max_rel, worst_cell_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -210,20 +210,32 @@ def _ragged(counts):
     return torch.tensor(offs, dtype=torch.int32)
 
 
-def _gemm_case(device, counts, n, k, *, seed, transposed=False, interleave=False, extreme=False,
-               addend=False, lora_rank=0):
+def _block_factors(g, shape, exponents):
+    """A power of two per 128x128 block of a ``[E, R, C]`` weight, 2**e with e
+    uniform over ``exponents``, and one all-zero block (the last expert's
+    last block row, first block column), as the reference's block-weight
+    helper builds them (tests/test_block_fp8_transpose_gemm.py:431-444)."""
+    experts, r, c = shape
+    lo, hi = exponents
+    blocks = (experts, -(-r // 128), -(-c // 128))
+    e = torch.randint(lo, hi + 1, blocks, generator=g).double()
+    f = torch.exp2(e).float()
+    if f.numel() > 1:
+        f[-1, -1, 0] = 0.0
+    return f.repeat_interleave(128, 1).repeat_interleave(128, 2)[:, :r, :c]
+
+
+def _gemm_case(device, counts, n, k, *, seed, transposed=False, interleave=False,
+               exponents=(-3, 3), addend=False, lora_rank=0):
     g = torch.Generator().manual_seed(seed)
     experts = len(counts)
     offsets = _ragged(counts)
     rows = int(offsets[-1])
     x = torch.randn(rows, k, generator=g).to(torch.bfloat16)
     wshape = (experts, k, n) if transposed else (experts, n, k)
-    w = torch.randn(*wshape, generator=g) * 0.02
-    if extreme:
-        # block scales at 2^+-14 and a zero block (test_block_fp8_transpose_gemm.py:495-500)
-        w[0, :128, :128] *= 2.0 ** 14
-        w[-1, -128:, -128:] *= 2.0 ** -14
-        w[experts // 2, :128, -128:] = 0
+    # Block scales a few powers of two apart (or 2^-14..2^14), so every
+    # block's scale shows in every output cell.
+    w = torch.randn(*wshape, generator=g) * 0.02 * _block_factors(g, wshape, exponents)
     xq, xs = K.quantize_rows(x.to(device))
     if transposed:
         wd, ws, wt = K.quantize_weight_blocks(w.to(device), transposed=True)
@@ -256,22 +268,29 @@ def _gemm_case(device, counts, n, k, *, seed, transposed=False, interleave=False
     return out.cpu(), want, offsets
 
 
+COUNTS = [0, 70, 131, 15, 260]  # an empty expert, partial row tiles (reference COUNTS)
+
+
 @pytest.mark.parametrize("case", [
-    dict(counts=[0, 70, 131, 15, 260], n=256, k=512),              # empty expert, partial tiles
-    dict(counts=[300, 0, 0, 128, 1], n=384, k=256, extreme=True),   # extreme scales, zero block
-    dict(counts=[129, 64, 257], n=256, k=384, interleave=True),     # gate/up interleaved output
-    dict(counts=[100, 200, 0, 33], n=256, k=512, transposed=True),  # input-gradient orientation
-    dict(counts=[90, 190], n=128, k=256, addend=True),              # LoRA-style addend
-    dict(counts=[0, 70, 131, 15, 260], n=256, k=512, lora_rank=16),  # rank term, empty expert
+    dict(counts=COUNTS, n=256, k=512),                                  # block scales 2^-3..2^3
+    dict(counts=COUNTS, n=384, k=1024, exponents=(-14, 14)),            # extreme scales, zero block
+    dict(counts=COUNTS, n=256, k=1024, exponents=(-14, 14), transposed=True),
+    dict(counts=COUNTS, n=512, k=1024, exponents=(-14, 14), interleave=True),
+    dict(counts=[129, 64, 257], n=256, k=384, interleave=True),         # gate/up interleaved output
+    dict(counts=[100, 200, 0, 33], n=256, k=512, transposed=True),      # input-gradient orientation
+    dict(counts=[90, 190], n=128, k=256, addend=True),                  # LoRA-style addend
+    dict(counts=COUNTS, n=256, k=512, lora_rank=16),                    # rank term, empty expert
     dict(counts=[129, 64, 257], n=512, k=384, interleave=True, lora_rank=32),  # gate/up order
     dict(counts=[100, 200, 0, 33], n=256, k=512, transposed=True, lora_rank=16),  # input gradient
 ])
 def test_grouped_gemm_matches_fp64(device, case):
-    out, want, offsets = _gemm_case(device, seed=sum(case["counts"]), **case)
-    for e in range(len(case["counts"])):
-        lo, hi = int(offsets[e]), int(offsets[e + 1])
-        if hi > lo:
-            assert max_rel(out[lo:hi], want[lo:hi]) < 1e-2, e
+    """Worst relative Frobenius error over (expert, 128-column) cells < 1e-2,
+    the reference's GEMM metric (tests/test_block_fp8_transpose_gemm.py:
+    390-406), so a block 2^28 times smaller than its neighbours is still
+    checked at its own magnitude."""
+    out, want, offsets = _gemm_case(device, seed=sum(case["counts"]) + case["k"], **case)
+    assert torch.isfinite(out).all()
+    assert worst_cell_rel(out, want, offsets.tolist()) < 1e-2
 
 
 def test_grouped_gemm_baseline_config2_sampled(device):
@@ -323,6 +342,7 @@ def test_grouped_gemm_large_weight_tile_order(device, interleave):
         if interleave:  # output columns 2j, 2j + 1 = gate j, up j
             want = want.view(hi - lo, 2, n // 2).transpose(1, 2).reshape(hi - lo, n)
         assert max_rel(out[lo:hi].float(), want) < 1e-2, e
+        assert worst_cell_rel(out[lo:hi], want, [0, hi - lo]) < 1e-2, e
 
 
 def test_rowwise_gemm_large_weight_tile_order(device):
@@ -365,6 +385,8 @@ def test_wgrad_matches_fp64(device, out_dtype, features):
     tol = 1e-4 if out_dtype == torch.float32 else 1e-2  # fp32 accumulation order
     for e in range(1, 4):
         assert max_rel(out[e], want[e]) < tol, e
+        # per (128-row, 128-column) cell, as the reference measures GEMMs
+        assert worst_cell_rel(out[e], want[e], list(range(0, features[0] + 1, 128))) < tol, e
 
 
 def test_combine_and_token_sum(device):

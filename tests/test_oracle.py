@@ -522,3 +522,92 @@ def test_current_forward_is_the_layer_when_quantizers_are_identities(monkeypatch
                                      routing_mode="softmax_then_topk", swiglu_limit=0.05)
     assert torch.equal(fwd["counts"], counts)
     assert frob_rel(fwd["out"].float(), out.detach().float()) < 1e-2
+
+
+def test_fp8_layer_is_the_native_layer_when_quantizers_are_identities(monkeypatch):
+    """With the e4m3 rounding replaced by the identity, the block-FP8 forward
+    and backward are the native layer up to their bf16 roundings: a wrong
+    gather, slot, gate/up order, scale layout, padding or orientation in any
+    of the layer's products (forward, both input gradients, both weight
+    gradients, router) fails this."""
+    monkeypatch.setattr(O, "_e4m3", lambda values: values)
+    x, res, wr, w13, w2 = _layer_inputs(tokens=96, seed=31)
+    res = torch.zeros_like(res)  # the routed part alone, without bf16 residual rounding
+    w13q, w13s = O.quantize_blocks(w13)
+    w2q, w2s = O.quantize_blocks(w2)
+    for mode, limit in (("topk_then_softmax", None), ("softmax_then_topk", 0.3)):
+        fwd = O.fp8_moe_forward(x, res, wr, w13q, w13s, w2q, w2s, top_k=2, routing_mode=mode,
+                                swiglu_limit=limit)
+        xr = x.float().requires_grad_(True)
+        w13r = w13.float().requires_grad_(True)
+        w2r = w2.float().requires_grad_(True)
+        wrr = wr.clone().requires_grad_(True)
+        out, aux, counts, _ = O.native_moe(xr, res.float(), wrr, w13r, w2r, top_k=2,
+                                           routing_mode=mode, swiglu_limit=limit)
+        assert torch.equal(fwd["counts"], counts)
+        assert frob_rel(fwd["out"].float(), out.detach().float()) < 1e-2
+        g = torch.Generator().manual_seed(32)
+        gy = torch.randn(out.shape, generator=g).to(torch.bfloat16)
+        out.backward(gy.float())
+        bwd = O.fp8_moe_backward(fwd, x, gy, wr, w13q, w13s, w2q, w2s, top_k=2,
+                                 routing_mode=mode, swiglu_limit=limit)
+        assert frob_rel(bwd["dw2"], w2r.grad) < 1e-2, mode
+        assert frob_rel(bwd["dw13"], w13r.grad) < 1e-2, mode
+        assert frob_rel(bwd["grad_x"].float(), xr.grad) < 1e-2, mode
+        assert frob_rel(bwd["grad_router"], wrr.grad) < 1e-2, mode
+
+
+def test_wgrad_is_a_sum_of_row_outer_products(monkeypatch):
+    """``O.wgrad`` against a row-by-row outer-product accumulation over each
+    expert's own (unpadded) rows. With identity e4m3 rounding the power-of-two
+    descales make the dequantized operands equal the inputs exactly, so the
+    padded layout, the per-expert starts and the transposition are what is
+    checked; the real rounding is then held within one e4m3 step."""
+    g = torch.Generator().manual_seed(33)
+    counts = [3, 0, 130, 1]
+    offsets = torch.tensor([0, *np.cumsum(counts)], dtype=torch.int32)
+    rows = int(offsets[-1])
+    p = torch.randn(rows, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(rows, 256, generator=g).to(torch.bfloat16)
+    _, padded = O.padded_layout(offsets)
+    want = np.zeros((len(counts), 128, 256))
+    pn, qn = p.double().numpy(), q.double().numpy()
+    for e in range(len(counts)):
+        for r in range(int(offsets[e]), int(offsets[e + 1])):
+            want[e] += np.outer(pn[r], qn[r])
+    with monkeypatch.context() as m:
+        m.setattr(O, "_e4m3", lambda values: values)
+        pt, pts, _ = O.quantize_transpose_padded(p, offsets, padded)
+        qt, qts, _ = O.quantize_transpose_padded(q, offsets, padded)
+        exact = O.wgrad(pt, pts, qt, qts, offsets).numpy()
+    assert np.abs(exact - want).max() < 1e-9 * np.abs(want).max()
+    assert np.all(exact[1] == 0)
+    pt, pts, _ = O.quantize_transpose_padded(p, offsets, padded)
+    qt, qts, _ = O.quantize_transpose_padded(q, offsets, padded)
+    rounded = O.wgrad(pt, pts, qt, qts, offsets).numpy()
+    assert np.linalg.norm(rounded - want) / np.linalg.norm(want) < 6e-2
+
+
+def test_combine_and_token_sum_by_loops():
+    """``O.combine`` / ``O.unpermute_sum`` against per-token loops in fp64,
+    rounded to bf16 once: every output within one bf16 step."""
+    g = torch.Generator().manual_seed(34)
+    tokens, top_k, width, experts = 40, 3, 256, 5
+    ids = torch.stack([torch.randperm(experts, generator=g)[:top_k] for _ in range(tokens)]).int()
+    _, _, slots = O.sort_assignments(ids, experts)
+    y = torch.randn(tokens * top_k, width, generator=g).to(torch.bfloat16)
+    w = torch.rand(tokens, top_k, generator=g)
+    res = torch.randn(tokens, width, generator=g).to(torch.bfloat16)
+    want = torch.zeros(tokens, width, dtype=torch.float64)
+    want_sum = torch.zeros(tokens, width, dtype=torch.float64)
+    for t in range(tokens):
+        acc = res[t].double().clone()
+        s = torch.zeros(width, dtype=torch.float64)
+        for j in range(top_k):
+            row = y[int(slots[t, j])].double()
+            acc += float(w[t, j]) * row
+            s += row
+        want[t], want_sum[t] = acc, s
+    for got, exp in ((O.combine(y, slots, w, res), want), (O.unpermute_sum(y, slots), want_sum)):
+        step = exp.abs().clamp_min(1e-3) * 2.0 ** -7
+        assert torch.all((got.double() - exp).abs() <= step)
