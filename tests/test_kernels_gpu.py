@@ -516,6 +516,8 @@ def test_gemm_swiglu_fused_matches_separate_pass(device, limit, inter):
     ([64], 96, 48),                      # K % 128 != 0: the register-operand form
     ([64, 129, 0, 31], 384, 48),         # the LDS-staged form at each rank
     ([1000, 0, 33, 700], 1024, 64),
+    ([257, 0, 40, 511, 3, 0, 90, 200], 4096, 16),   # C5's K (hidden) at its rank
+    ([130, 0, 17, 250], 14336, 16),                  # C5's K (intermediate)
 ])
 def test_rank_product_matches_fp32(device, counts, k, rank):
     g = torch.Generator().manual_seed(sum(counts) + k)

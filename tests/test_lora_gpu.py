@@ -218,3 +218,61 @@ def test_cpu_tensors_are_refused_with_the_reason():
         expert_lora(x, x, wr, w13, w2, a, b, torch.zeros(2, 4, 128), torch.zeros(2, 128, 4),
                     top_k=1, routing_mode="softmax_then_topk", scale=1.0,
                     compute_precision="fp8_block")
+
+
+@pytest.mark.gpu
+def test_expert_lora_at_mixtral_widths(device):
+    """C5's widths (H = 4096, I = 14336, E = 8, top-2, rank 16) on a frozen
+    block-FP8 base, with C5's factor scales (A ~ N(0, 0.01), B = 0.1 N(0, 1),
+    bf16) and its +2 logit on expert 0, at 128 tokens so the CPU oracle
+    finishes: every output and gradient against the native form on the
+    dequantized base at the reference's FP8 bounds
+    (tests/test_sonicmoe_lora.py:336-343). K = 4096 and 14336 take the LoRA
+    accumulator-start GEMMs and the routed rank products through their long-K
+    loops."""
+    tokens, width, experts, inter, top_k, rank, scale = 128, 4096, 8, 14336, 2, 16, 2.0
+    g = torch.Generator().manual_seed(55)
+    x = torch.randn(tokens, width, generator=g).to(torch.bfloat16)
+    res = torch.randn(tokens, width, generator=g).to(torch.bfloat16)
+    wr = torch.randn(experts, width, generator=g) / math.sqrt(width)
+    x[:, 0], wr[:, 0], wr[0, 0] = 1.0, 0.0, 2.0  # logits + 2 on expert 0
+    factors = [(torch.randn(*shape, generator=g) * std).to(torch.bfloat16)
+               for shape, std in (((experts, rank, width), 0.01), ((experts, 2 * inter, rank), 0.1),
+                                  ((experts, rank, inter), 0.01), ((experts, width, rank), 0.1))]
+    dy = torch.randn(tokens, width, generator=g).to(torch.bfloat16)
+    gd = torch.Generator(device=device).manual_seed(56)  # 1.4G weight values: drawn on the GPU
+    w13 = (torch.randn(experts, 2 * inter, width, generator=gd, device=device) * 0.02).bfloat16()
+    w2 = (torch.randn(experts, width, inter, generator=gd, device=device) * 0.02).bfloat16()
+    mode = "topk_then_softmax"
+
+    # GPU: frozen containers, gradients for x, the router and the factors.
+    xg, wrg = _leaf(x.to(device)), _leaf(wr.to(device))
+    fg = [_leaf(f.to(device)) for f in factors]
+    w13c, w2c = BlockFP8Weight.quantize(w13), BlockFP8Weight.quantize(w2)
+    del w13, w2
+    out, aux, counts, psum = expert_lora(xg, res.to(device), wrg, w13c, w2c, *fg, top_k=top_k,
+                                         routing_mode=mode, scale=scale)
+    grads = torch.autograd.grad((out.float() * dy.to(device).float()).sum() + 0.3 * aux,
+                                [xg, wrg, *fg])
+    grads = [t.cpu() for t in grads]
+    out, counts = out.detach().cpu(), counts.cpu()
+    assert int(counts[0]) == int(counts.max()) > tokens // 2  # the +2 logit on expert 0
+
+    # Oracle on the CPU, on the base the GPU forward multiplies: the
+    # containers' e4m3 blocks (bit-exact to the oracle's block quantizer,
+    # tested elsewhere) dequantized, as per-expert frozen tensors.
+    comps = [c.components() for c in (w13c, w2c)]
+    w13d, w2d = ([O.dequantize_blocks(d[e:e + 1].cpu(), s[e:e + 1].cpu())[0]
+                  for e in range(experts)] for d, s in comps)
+    del w13c, w2c, comps
+    xl, wrl = _leaf(x), _leaf(wr)
+    fl = [_leaf(f.float()) for f in factors]
+    r_out, r_aux, r_counts, _ = O.native_moe(xl, res, wrl, w13d, w2d, top_k=top_k,
+                                             routing_mode=mode, lora=(*fl, scale))
+    r_grads = torch.autograd.grad((r_out.float() * dy.float()).sum() + 0.3 * r_aux, [xl, wrl, *fl])
+    assert torch.equal(counts, r_counts)
+    assert frob_rel(out.float(), r_out.detach().float()) < 4e-2
+    for name, a, b in zip(["x", "router", "a13", "b13", "a2", "b2"], grads, r_grads, strict=True):
+        assert a.shape == b.shape, name
+        err = frob_rel(a.float(), b.float())
+        assert err < BOUND, f"{name}: relative error {err:.3e}"
