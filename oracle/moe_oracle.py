@@ -38,7 +38,13 @@ PINNED = {
     "grouped_gemm": "fp64 dequantized product vs a per-row dot-product loop",
     "swiglu / routed_swiglu_backward": "torch autograd of silu(min(g,L))*clamp(u,L)",
     "native_moe": "dense-masked (reference) vs sparse-gathered evaluation; autograd gradients",
-    "fp8_moe_forward / fp8_moe_backward": "equals native_moe when the quantizers are identities",
+    "fp8_moe_forward / fp8_moe_backward": "equal native_moe (output, both input gradients, both"
+                                          " weight gradients, router gradient; two routing"
+                                          " modes, a SwiGLU limit) when e4m3 rounding is the"
+                                          " identity",
+    "wgrad": "row-by-row outer-product sums over each expert's unpadded rows (exact under"
+             " identity rounding, since the descales are powers of two)",
+    "combine / unpermute_sum": "per-token fp64 loops, within one bf16 step",
     "quantize_rows_current": "128-wide rows equal the pinned quantize_rows_1x128; per-row closed"
                              " form with numpy; zero row; amax element maps to +-448",
     "quantize_weights_current": "the reference container test's bounds (row-max relative error"

@@ -231,6 +231,54 @@ def test_qwen3_shape_properties(device):
         assert torch.isfinite(gtensor.float()).all()
 
 
+def test_qwen3_full_shape_sampled_tokens_against_oracle(device):
+    """Config 3 at full size (T=16384, H=2048, I=768, E=128, k=8) against the
+    fp8 oracle on a subset S of the tokens: the two least-loaded experts'
+    tokens plus 64 spread tokens. The GPU runs the whole layer; its backward
+    takes the upstream gradient masked to S with zero aux / probability-sum
+    cotangents, so every gradient is a sum over S. The oracle then runs on S
+    alone, with the GPU's fp32 logits of S (routing is per token): its rows of
+    the two experts are exactly the GPU's, in the same order, so their 128-row
+    quantization blocks agree, and it gives the GPU's ``out[S]``,
+    ``grad_x[S]``, the full router gradient and both experts' weight
+    gradients, each within 1e-2 relative Frobenius."""
+    tokens, hidden, inter, experts, top_k = 16384, 2048, 768, 128, 8
+    x, res, wr, w13, w2, dy = _inputs(device, tokens, hidden, experts, inter, seed=12)
+    w13c, w2c = BlockFP8Weight.quantize(w13), BlockFP8Weight.quantize(w2)
+    mode = "topk_then_softmax"
+    fwd = mlops_amd.explicit.moe.forward(x, res, wr, w13c, w2c, top_k=top_k, routing_mode=mode)
+    out, aux, counts, psum, logits, weights, ids, order, offsets, slots, h13 = fwd
+    cnt = counts.cpu().clone()
+    cnt[cnt == 0] = tokens * top_k
+    e1, e2 = (int(e) for e in torch.argsort(cnt, stable=True)[:2])
+    ids_c = ids.cpu()
+    mask = ((ids_c == e1) | (ids_c == e2)).any(1)
+    mask[torch.linspace(0, tokens - 1, 64).long()] = True
+    sample = torch.nonzero(mask).squeeze(1)
+    dy_masked = dy * mask.to(device)[:, None].to(dy.dtype)
+    d_h2, _, d_router, d_w13, d_w2 = mlops_amd.explicit.moe.backward(
+        dy_masked, torch.zeros((), device=device), torch.zeros_like(psum), x, wr, w13c, w2c,
+        logits, weights, ids, order, offsets, slots, h13, top_k=top_k, routing_mode=mode,
+        lengths=(tokens,))
+
+    cpu = lambda t: t.detach().cpu()
+    w13q, w13s = (cpu(t) for t in w13c.components())
+    w2q, w2s = (cpu(t) for t in w2c.components())
+    xs, sl = cpu(x)[sample], cpu(logits)[sample]
+    ofwd = O.fp8_moe_forward(xs, cpu(res)[sample], cpu(wr), w13q, w13s, w2q, w2s, top_k=top_k,
+                             routing_mode=mode, logits=sl)
+    assert torch.equal(ofwd["ids"], ids_c[sample])
+    assert frob_rel(cpu(out)[sample].float(), ofwd["out"].float()) < 1e-2
+    obwd = O.fp8_moe_backward(ofwd, xs, cpu(dy)[sample], cpu(wr), w13q, w13s, w2q, w2s,
+                              top_k=top_k, routing_mode=mode)
+    assert frob_rel(cpu(d_h2)[sample].float(), obwd["grad_x"].float()) < 1e-2
+    assert frob_rel(cpu(d_router).float(), obwd["grad_router"]) < 1e-2
+    for e in (e1, e2):
+        assert int(ofwd["counts"][e]) == int(counts[e]) > 0
+        assert frob_rel(cpu(d_w2[e]).float(), obwd["dw2"][e]) < 1e-2, e
+        assert frob_rel(cpu(d_w13[e]).float(), obwd["dw13"][e]) < 1e-2, e
+
+
 def test_per_call_transposed_weights_match_containers_bitwise(device, monkeypatch):
     """Plain weights quantized per call carry the transposed copies written in
     the same kernel pass (no transpose in backward); the results equal those
