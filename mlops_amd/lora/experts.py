@@ -34,12 +34,11 @@ from __future__ import annotations
 import torch
 
 from .. import kernels, router
-from ..block_fp8 import BlockFP8Weight
 from ..dispatch.context import weight_gradient_dtype
 from ..providers.mi355x import moe as provider
 from ..providers.mi355x import moe_current
 from ..routing import current_route_weight_precision, next_override
-from ..row_fp8 import RowFP8Weight
+from ..weight_formats import is_row_fp8
 
 IMPLEMENTATIONS = ("auto", "mi355x")
 
@@ -130,7 +129,7 @@ class _ExpertLoRA(torch.autograd.Function):
         width = hidden.shape[-1]
         tokens = hidden.numel() // width
         experts = router_weight.shape[0]
-        current = isinstance(w13, RowFP8Weight)
+        current = is_row_fp8(w13)
         if current:  # rows (gate/up-adjacent for w13), transpose, per-row descales
             w13_data, _, w13_scale, _ = w13.components()
             w2_data, _, w2_scale, _ = w2.components()
@@ -213,7 +212,7 @@ class _ExpertLoRA(torch.autograd.Function):
         tokens = hidden.numel() // width
         experts = router_weight.shape[0]
         assignments = order.numel()
-        current = isinstance(ctx.w13, RowFP8Weight)
+        current = is_row_fp8(ctx.w13)
         if current:
             _, w13_t, _, w13_ts = ctx.w13.components()
             w2_data, w2_t, _, w2_ts = ctx.w2.components()
@@ -352,7 +351,7 @@ def expert_lora(
     rows = hidden.numel() // hidden.shape[-1]
     lengths = (rows,) if lengths is None else tuple(int(x) for x in lengths)
     rules = moe_current if (compute_precision == "fp8_current" or (
-        compute_precision is None and any(isinstance(w, RowFP8Weight) for w in (gate_up, down)))
+        compute_precision is None and any(is_row_fp8(w) for w in (gate_up, down)))
     ) else provider
     support = rules.supports(
         hidden, residual, router_weight, gate_up, down, surface="semantic", top_k=top_k,

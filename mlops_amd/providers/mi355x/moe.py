@@ -31,7 +31,8 @@ import torch
 
 from ... import kernels, router
 from ...block_fp8 import BlockFP8Weight
-from ...row_fp8 import RowFP8Weight
+from ...weight_formats import (block_parts, is_block_fp8, is_row_fp8, register_container_class,
+                               route_containers)
 from ...dispatch import logical_costs as logical
 from ...dispatch.context import weight_gradient_dtype
 from ...dispatch.costs import flop_formula
@@ -54,9 +55,9 @@ def _arch(device: torch.device) -> str:
 
 def _precision(compute_precision, w13, w2):
     """``"fp8_block"`` when this implementation serves the request, else a refusal."""
-    if any(isinstance(w, RowFP8Weight) for w in (w13, w2)):
-        return None, "RowFP8Weight weights compute at fp8_current"
-    containers = isinstance(w13, BlockFP8Weight) or isinstance(w2, BlockFP8Weight)
+    if any(is_row_fp8(w) for w in (w13, w2)):
+        return None, "row-FP8 (RowFP8Weight / QuackFP8Weight) weights compute at fp8_current"
+    containers = is_block_fp8(w13) or is_block_fp8(w2)
     if compute_precision == "fp8_block":
         return "fp8_block", None
     if compute_precision is None and containers:
@@ -290,7 +291,7 @@ def routing_backward(grad_h2, x, router_weight, logits, route_weights, route_ids
 
 
 # --------------------------------------------------------------------------
-# Custom operators. Weights arrive as BlockFP8Weight containers; the dispatch
+# Custom operators. Weights arrive as block-FP8 containers; the dispatch
 # rule below replaces each by its e4m3 data and appends its scale to
 # ``weight_components`` (the reference's container protocol,
 # providers/sonicmoe/fp8.py:204-236).
@@ -324,7 +325,7 @@ def transposed_data(container: BlockFP8Weight) -> torch.Tensor:
     carried = getattr(container, "_transposed", None)
     if carried is not None:
         return carried
-    data = container._data
+    data = block_parts(container)[0]
     cached = getattr(container, "_transposed_cache", None)
     if cached is not None and cached[0] == data._version and cached[1] is data:
         return cached[2]
@@ -435,9 +436,10 @@ def _container_rule(cls, func, types, args, kwargs):
     transposed = []
     backward = func is torch.ops.mlops_mi355x.moe_mi355x_block_fp8_bwd.default
     for index, value in enumerate(args):
-        if isinstance(value, BlockFP8Weight):
-            args[index] = value._data
-            components.append(value._scale)
+        parts = block_parts(value)
+        if parts is not None:
+            args[index] = parts[0]
+            components.append(parts[1])
             # The input-gradient GEMMs read the transposed copies.
             transposed.append(transposed_data(value) if backward
                               else getattr(value, "_transposed", None))
@@ -447,8 +449,8 @@ def _container_rule(cls, func, types, args, kwargs):
     return func(*args)
 
 
-_forward_op.register_torch_dispatch(BlockFP8Weight, _container_rule)
-_backward_op.register_torch_dispatch(BlockFP8Weight, _container_rule)
+OPERATORS = (_forward_op, _backward_op)
+register_container_class(OPERATORS, _container_rule, BlockFP8Weight)
 
 
 def _setup_context(ctx, inputs, output):
@@ -519,8 +521,11 @@ class _QuantizePerCall(torch.autograd.Function):
 
 def _containers(w13, w2):
     """Plain weights quantized per call (straight-through); containers as they are."""
-    return tuple(w if isinstance(w, BlockFP8Weight) else _QuantizePerCall.apply(w)
-                 for w in (w13, w2))
+    weights = tuple(w if is_block_fp8(w) else _QuantizePerCall.apply(w) for w in (w13, w2))
+    # Containers of other classes carrying the same components (the
+    # reference's own BlockFP8Weight) reach the operators the same way.
+    route_containers(OPERATORS, _container_rule, *weights)
+    return weights
 
 
 def _shared_base(h2, residual, shared_w13, shared_w2, shared_gate_weight, shared_mode, limit):
@@ -568,8 +573,9 @@ def apply(
 
 
 def _components(weight):
-    if isinstance(weight, BlockFP8Weight):
-        return weight.components()
+    parts = block_parts(weight)
+    if parts is not None:
+        return parts
     data, scale = kernels.quantize_weight_blocks(weight)
     return data, scale
 

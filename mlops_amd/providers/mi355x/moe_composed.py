@@ -38,6 +38,8 @@ from ...dispatch.costs import flop_formula
 from ...dispatch.registry import Implementation, SupportResult, register_implementation
 from ...routing import current_route_weight_precision, next_override
 from ...row_fp8 import RowFP8Weight
+from ...weight_formats import (block_parts, is_row_fp8, register_container_class,
+                               route_containers, row_parts)
 from . import moe as fused
 from . import moe_current as current
 
@@ -47,7 +49,7 @@ PRIORITY = 115  # below mi355x.moe.block_fp8 (120), which is faster
 
 def _is_current(compute_precision, w13, w2) -> bool:
     return compute_precision == "fp8_current" or (
-        compute_precision is None and any(isinstance(w, RowFP8Weight) for w in (w13, w2)))
+        compute_precision is None and any(is_row_fp8(w) for w in (w13, w2)))
 
 
 def _supports(h2, residual, router_weight, w13_experts, w2_experts, *, surface, **kwargs):
@@ -419,7 +421,7 @@ def _finish_backward_flops(grad_output, h13, w2_experts, *_rest, out_val=None, *
 
 
 def _container_rule(cls, func, types, args, kwargs):
-    """Unwraps the one ``BlockFP8Weight`` argument to its data, appending its
+    """Unwraps the one container argument to its data, appending its
     scale and, for the backward operators and wherever the per-call quantizer
     carried it, its transposed data to the ``weight_components`` argument."""
     del cls, types
@@ -432,24 +434,25 @@ def _container_rule(cls, func, types, args, kwargs):
                         torch.ops.mlops_mi355x.moe_mi355x_finish_bwd.default,
                         torch.ops.mlops_mi355x.moe_mi355x_finish_bwd_donate_h13.default)
     for index, value in enumerate(args):
-        if isinstance(value, BlockFP8Weight):
-            args[index] = value._data
-            components.append(value._scale)
+        block, row = block_parts(value), row_parts(value)
+        if block is not None:
+            args[index] = block[0]
+            components.append(block[1])
             transposed = (fused.transposed_data(value) if backward
                           else getattr(value, "_transposed", None))
             if transposed is not None:
                 components.append(transposed)
-        elif isinstance(value, RowFP8Weight):
-            args[index] = value._data
-            components.extend((value._transposed, value._scale, value._transposed_scale))
+        elif row is not None:
+            args[index] = row[0]
+            components.extend(row[1:])
     args[slot] = components
     return func(*args)
 
 
-for _op in (_prepare_op, _prepare_backward_op, _finish_op, _finish_backward_op,
-            _finish_backward_donate_h13_op):
-    _op.register_torch_dispatch(BlockFP8Weight, _container_rule)
-    _op.register_torch_dispatch(RowFP8Weight, _container_rule)
+OPERATORS = (_prepare_op, _prepare_backward_op, _finish_op, _finish_backward_op,
+             _finish_backward_donate_h13_op)
+for _cls in (BlockFP8Weight, RowFP8Weight):
+    register_container_class(OPERATORS, _container_rule, _cls)
 
 
 def _prepare_context(ctx, inputs, output):
@@ -534,6 +537,7 @@ def apply(
     if refusal is not None:
         raise ValueError(refusal)
     w13, w2 = rules._containers(w13_experts, w2_experts)
+    route_containers(OPERATORS, _container_rule, w13, w2)
     rows = h2.numel() // h2.shape[-1]
     normalized = (rows,) if lengths is None else tuple(int(x) for x in lengths)
     bias = (torch.empty(0, dtype=torch.float32, device=h2.device) if router_bias is None

@@ -39,6 +39,8 @@ from ...dispatch.costs import flop_formula
 from ...dispatch.registry import Implementation, SupportResult, register_implementation
 from ...routing import current_route_weight_precision, next_override
 from ...row_fp8 import RowFP8Weight
+from ...weight_formats import (is_block_fp8, is_row_fp8, register_container_class,
+                               route_containers, row_interleaved, row_parts)
 from . import moe as fused
 
 IMPLEMENTATION_ID = "mi355x.moe.fp8_current"
@@ -49,11 +51,11 @@ GEMM_ALIGN = 256  # every N of the four row-scaled GEMMs (2I, H, I, H)
 def _precision(compute_precision, w13, w2):
     """``"fp8_current"`` when this implementation serves the request, else a refusal."""
     weights = (w13, w2)
-    if any(isinstance(w, BlockFP8Weight) for w in weights):
-        return None, "BlockFP8Weight weights compute at fp8_block"
+    if any(is_block_fp8(w) for w in weights):
+        return None, "block-FP8 (BlockFP8Weight) weights compute at fp8_block"
     if compute_precision == "fp8_current":
         return "fp8_current", None
-    if compute_precision is None and any(isinstance(w, RowFP8Weight) for w in weights):
+    if compute_precision is None and any(is_row_fp8(w) for w in weights):
         return "fp8_current", None
     return None, f"compute_precision={compute_precision!r} is not fp8_current"
 
@@ -65,7 +67,7 @@ def supports(h2, residual, router_weight, w13_experts, w2_experts, *, surface, t
     _, refusal = _precision(compute_precision, w13_experts, w2_experts)
     if refusal is not None:
         return SupportResult.no(refusal)
-    if isinstance(w13_experts, RowFP8Weight) and not w13_experts.interleaved:
+    if is_row_fp8(w13_experts) and not row_interleaved(w13_experts):
         return SupportResult.no(
             "an FP8 w13 must be quantized with interleaved=True (gate/up rows adjacent)")
     del surface
@@ -262,7 +264,7 @@ def _backward_flops(grad_output, grad_aux, grad_probability_sum, h2, router_weig
 
 
 def _container_rule(cls, func, types, args, kwargs):
-    """Each `RowFP8Weight` argument becomes its e4m3 rows; its transposed copy
+    """Each row-FP8 container argument becomes its e4m3 rows; its transposed copy
     and the two descale vectors fill ``weight_components``, in weight order
     (reference ``sonicmoe/fp8.py:223-256``)."""
     del cls, types
@@ -272,15 +274,16 @@ def _container_rule(cls, func, types, args, kwargs):
     slot = [a.name for a in func._schema.arguments].index("weight_components")
     components = list(args[slot])
     for index, value in enumerate(args):
-        if isinstance(value, RowFP8Weight):
-            args[index] = value._data
-            components.extend((value._transposed, value._scale, value._transposed_scale))
+        parts = row_parts(value)
+        if parts is not None:
+            args[index] = parts[0]
+            components.extend(parts[1:])
     args[slot] = components
     return func(*args)
 
 
-_forward_op.register_torch_dispatch(RowFP8Weight, _container_rule)
-_backward_op.register_torch_dispatch(RowFP8Weight, _container_rule)
+OPERATORS = (_forward_op, _backward_op)
+register_container_class(OPERATORS, _container_rule, RowFP8Weight)
 
 
 def _setup_context(ctx, inputs, output):
@@ -316,8 +319,10 @@ _forward_op.register_autograd(_autograd_backward, setup_context=_setup_context)
 def _containers(w13, w2):
     """Plain weights quantized per call (straight through, w13 gate/up-adjacent);
     containers as they are."""
-    return (w13 if isinstance(w13, RowFP8Weight) else RowFP8Weight.quantize(w13, interleaved=True),
-            w2 if isinstance(w2, RowFP8Weight) else RowFP8Weight.quantize(w2))
+    weights = (w13 if is_row_fp8(w13) else RowFP8Weight.quantize(w13, interleaved=True),
+               w2 if is_row_fp8(w2) else RowFP8Weight.quantize(w2))
+    route_containers(OPERATORS, _container_rule, *weights)
+    return weights
 
 
 def apply(
@@ -347,8 +352,9 @@ def apply(
 
 
 def _weight(weight, interleaved):
-    if isinstance(weight, RowFP8Weight):
-        return (weight._data, *weight.components()[1:])
+    parts = row_parts(weight)
+    if parts is not None:
+        return parts
     return kernels.quantize_weights_current(weight.detach(), interleaved=interleaved)
 
 

@@ -357,3 +357,39 @@ def test_routing_override_validation():
     with routing_override([ids]):
         with pytest.raises(ValueError, match="shape"):
             next_override(3, 4, 2, "cpu")
+
+
+def test_protocol_containers_are_recognised(monkeypatch):
+    """A container class that only carries the reference's block-FP8
+    component protocol is served by the block-FP8 operator (and refused by
+    the fp8_current one), as the reference's own BlockFP8Weight would be."""
+    from mlops_amd.providers.mi355x import moe_current
+    from mlops_amd.weight_formats import block_parts, is_row_fp8
+    from tests.foreign_container import ProtocolBlockWeight
+
+    monkeypatch.setattr(torch.version, "hip", "7.0", raising=False)
+    monkeypatch.setattr(provider, "_arch", lambda device: "gfx950:sramecc+:xnack-")
+
+    class FakeCuda(torch.Tensor):
+        pass
+
+    monkeypatch.setattr(FakeCuda, "is_cuda", property(lambda self: True))
+    gpu = lambda t: t.as_subclass(FakeCuda)
+    x, res, wr, w13, w2 = _args()
+    fp8 = torch.float8_e4m3fn
+
+    def foreign(w):
+        e, out, inner = w.shape
+        return ProtocolBlockWeight(torch.zeros(e, out, inner, dtype=fp8),
+                                   torch.ones(e, -(-out // 128), -(-inner // 128)))
+
+    c13, c2 = foreign(w13), foreign(w2)
+    assert block_parts(c13) is not None and not is_row_fp8(c13)
+    base = dict(surface="semantic", top_k=2, routing_mode="topk_then_softmax")
+    ok = provider.supports(gpu(x), gpu(res), gpu(wr), c13, c2, **base)
+    assert ok, ok.reason
+    refused = moe_current.supports(gpu(x), gpu(res), gpu(wr), c13, c2, **base)
+    assert not refused and "fp8_block" in refused.reason
+    # A wrong scale shape is not the protocol: treated as a plain weight.
+    bad = ProtocolBlockWeight(torch.zeros(8, 256, 256, dtype=fp8), torch.ones(8, 1, 1))
+    assert block_parts(bad) is None

@@ -385,3 +385,30 @@ def test_layer_edge_shapes_match_fp8_oracle(device, tokens, experts, top_k):
         assert not bool(used[experts // 2:].any())
         assert bool((r["g13"][~used.to(device)] == 0).all())
         assert bool((r["g2"][~used.to(device)] == 0).all())
+
+
+def test_protocol_container_equals_block_fp8_weight(device):
+    """The same e4m3 blocks in a container class that only carries the
+    reference's component protocol (tests/foreign_container.py): every output
+    and gradient bitwise equal to BlockFP8Weight's, trained containers
+    included (their gradients arrive on the foreign leaves)."""
+    from tests.foreign_container import ProtocolBlockWeight
+
+    x, res, wr, w13, w2, dy = _inputs(device, tokens=192, hidden=256, experts=8, inter=256,
+                                      seed=41)
+
+    def run(make):
+        xl, wrl = x.clone().requires_grad_(True), wr.clone().requires_grad_(True)
+        c13 = make(*BlockFP8Weight.quantize(w13).components()).requires_grad_(True)
+        c2 = make(*BlockFP8Weight.quantize(w2).components()).requires_grad_(True)
+        out, aux, counts, psum = mlops_amd.moe(xl, res, wrl, c13, c2, top_k=2,
+                                               routing_mode="softmax_then_topk")
+        torch.autograd.backward([out, aux], [dy, torch.ones_like(aux) * 0.1])
+        return [out, aux, counts, psum, xl.grad, wrl.grad, c13.grad, c2.grad]
+
+    with capture_dispatch() as trace:
+        theirs = run(lambda d, s: ProtocolBlockWeight(d, s, dtype=torch.bfloat16))
+    assert trace == {"moe": {"mi355x.moe.block_fp8": 1}}
+    ours = run(lambda d, s: BlockFP8Weight(d, s, dtype=torch.bfloat16))
+    for a, b in zip(theirs, ours, strict=True):
+        assert a is not None and torch.equal(a, b)
