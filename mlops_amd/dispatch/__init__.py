@@ -1,47 +1,16 @@
-"""Dispatch: exact-ID implementation registry, selection and context controls."""
+"""Implementation dispatch for the MoE operation: the catalog of records
+(`registry`), the choice for one call (`resolution`), context-local settings
+(`context`) and cost figures (`costs`, `logical_costs`). The names exported
+here are the subset of the reference's ``mlops.dispatch`` API the MoE path
+uses."""
 
-from .context import (
-    capture_dispatch,
-    deterministic_kernels,
-    deterministic_required,
-    dispatch_manifest,
-    set_deterministic_kernels,
-    set_implementations,
-    set_weight_gradient_dtype,
-    use_implementation,
-    use_implementations,
-    weight_gradient_dtype,
-    weight_gradients_at,
-)
-from .costs import CostHints, estimate_implementation, flop_formula, has_flop_formula
-from .registry import (
-    Implementation,
-    SupportResult,
-    implementation_registry,
-    register_implementation,
-)
-from .resolution import explain_implementation, resolve_implementation
+from . import context, costs, registry, resolution
+from .context import *  # noqa: F401,F403
+from .costs import *  # noqa: F401,F403
+from .registry import *  # noqa: F401,F403
+from .resolution import *  # noqa: F401,F403
 
-__all__ = [
-    "CostHints",
-    "Implementation",
-    "SupportResult",
-    "capture_dispatch",
-    "deterministic_kernels",
-    "deterministic_required",
-    "dispatch_manifest",
-    "estimate_implementation",
-    "explain_implementation",
-    "flop_formula",
-    "has_flop_formula",
-    "implementation_registry",
-    "register_implementation",
-    "resolve_implementation",
-    "set_deterministic_kernels",
-    "set_implementations",
-    "set_weight_gradient_dtype",
-    "use_implementation",
-    "use_implementations",
-    "weight_gradient_dtype",
-    "weight_gradients_at",
-]
+_INTERNAL = {"ENVIRONMENT_OVERRIDES", "implementation_override", "record_dispatch",
+             "frozen_implementation", "implementations_for", "apply_environment_overrides"}
+__all__ = sorted({name for module in (context, costs, registry, resolution)
+                  for name in module.__all__} - _INTERNAL)

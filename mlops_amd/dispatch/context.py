@@ -1,177 +1,194 @@
-"""Context-local dispatch choices: forced implementations, the weight-gradient
-dtype, determinism requests and dispatch capture.
+"""Dispatch settings that belong to the calling context.
 
-Follows the reference's control surface (``src/mlops/dispatch/context.py:20-240``):
-``use_implementation(s)``/``set_implementations``, the ``MLOPS_IMPLEMENTATIONS``
-environment variable, ``weight_gradients_at``/``set_weight_gradient_dtype``,
-``deterministic_kernels`` and ``capture_dispatch``/``dispatch_manifest``.
+Four settings travel with the caller (thread / asyncio task), each readable
+anywhere below it and restorable on exit:
+
+* forced implementations, ``operation -> implementation ID`` (checked against
+  the catalog when set; also read from ``MLOPS_IMPLEMENTATIONS="op=id,..."``);
+* the dtype weight gradients are returned at (``None``: each weight's own);
+* whether bitwise-repeatable kernels were requested;
+* an optional trace that counts which implementation each resolution chose.
+
+The function names and their meaning are the reference's control surface
+(``src/mlops/dispatch/context.py``); here all four live in one immutable
+record in a single context variable, and every scoped helper swaps that
+record for the duration of its block.
 """
 
 from __future__ import annotations
 
 import os
+import re
 from contextlib import contextmanager
 from contextvars import ContextVar
+from dataclasses import dataclass, field, replace
 from types import MappingProxyType
 from typing import Mapping
 
 import torch
 
-_FORCED: ContextVar[Mapping[str, str]] = ContextVar(
-    "mlops_amd_forced_implementations", default=MappingProxyType({})
-)
-_TRACE: ContextVar[dict | None] = ContextVar("mlops_amd_dispatch_trace", default=None)
-_DETERMINISTIC: ContextVar[bool] = ContextVar("mlops_amd_deterministic", default=False)
-_GRAD_DTYPE: ContextVar[torch.dtype | None] = ContextVar(
-    "mlops_amd_weight_gradient_dtype", default=None
-)
-
 ENVIRONMENT_OVERRIDES = "MLOPS_IMPLEMENTATIONS"
+_PAIR = re.compile(r"^\s*([^\s=,]+)\s*=\s*([^\s=,]+)\s*$")
 
 
+@dataclass(frozen=True)
+class _Settings:
+    forced: Mapping[str, str] = field(default_factory=lambda: MappingProxyType({}))
+    gradient_dtype: torch.dtype | None = None
+    deterministic: bool = False
+    trace: dict | None = None
+
+
+_SETTINGS: ContextVar[_Settings] = ContextVar("mlops_amd_dispatch_settings",
+                                              default=_Settings())
+
+
+@contextmanager
+def _scoped(**changes):
+    token = _SETTINGS.set(replace(_SETTINGS.get(), **changes))
+    try:
+        yield
+    finally:
+        _SETTINGS.reset(token)
+
+
+def _update(**changes) -> None:
+    _SETTINGS.set(replace(_SETTINGS.get(), **changes))
+
+
+# ------------------------------------------------------------- forced choices
 def implementation_override(operation: str) -> str | None:
-    """The implementation forced for ``operation`` in this context, if any."""
-    return _FORCED.get().get(str(operation))
+    """The implementation ID forced for ``operation`` here, or None."""
+    return _SETTINGS.get().forced.get(str(operation))
 
 
-def _checked(overrides: Mapping[str, str]) -> dict[str, str]:
+def _validated(choices: Mapping[str, str]) -> dict[str, str]:
     from .registry import implementations_for
 
-    result = {}
-    for operation, implementation_id in overrides.items():
-        known = implementations_for(str(operation))
-        if str(implementation_id) not in known:
-            raise ValueError(
-                f"unknown implementation {implementation_id!r} for {operation!r}; "
-                f"choose one of {sorted(known)}"
-            )
-        result[str(operation)] = str(implementation_id)
-    return result
+    checked = {}
+    for operation, wanted in choices.items():
+        operation, wanted = str(operation), str(wanted)
+        available = implementations_for(operation)
+        if wanted not in available:
+            raise ValueError(f"unknown implementation {wanted!r} for operation {operation!r} "
+                             f"(registered: {', '.join(sorted(available))})")
+        checked[operation] = wanted
+    return checked
 
 
-def _with(extra: Mapping[str, str]) -> Mapping[str, str]:
-    merged = dict(_FORCED.get())
-    merged.update(extra)
-    return MappingProxyType(merged)
+def _forced_with(choices: Mapping[str, str]) -> Mapping[str, str]:
+    return MappingProxyType({**_SETTINGS.get().forced, **choices})
 
 
 @contextmanager
 def use_implementations(overrides: Mapping[str, str]):
-    """Force exact implementations inside the block (outer choices inherited)."""
-    chosen = _checked(overrides)
-    token = _FORCED.set(_with(chosen))
-    try:
+    """Force the given implementation IDs inside the block; choices made by
+    enclosing blocks for other operations still hold."""
+    chosen = _validated(overrides)
+    with _scoped(forced=_forced_with(chosen)):
         yield MappingProxyType(chosen)
-    finally:
-        _FORCED.reset(token)
 
 
 @contextmanager
 def use_implementation(operation: str, implementation_id: str):
-    """Force one implementation for one operation inside the block."""
+    """Force one operation's implementation inside the block."""
     with use_implementations({operation: implementation_id}) as chosen:
         yield chosen[str(operation)]
 
 
 def set_implementations(overrides: Mapping[str, str]) -> None:
-    """Force exact implementations from here on in the calling context."""
-    _FORCED.set(_with(_checked(overrides)))
+    """Force implementation IDs for the rest of the calling context."""
+    _update(forced=_forced_with(_validated(overrides)))
 
 
 def apply_environment_overrides() -> Mapping[str, str]:
-    """Apply ``MLOPS_IMPLEMENTATIONS="op=id,op=id"``; returns what was applied."""
-    text = os.environ.get(ENVIRONMENT_OVERRIDES, "").strip()
-    if not text:
+    """Force what ``MLOPS_IMPLEMENTATIONS`` lists (``op=id`` pairs separated by
+    commas) and return it; an empty or unset variable forces nothing."""
+    text = os.environ.get(ENVIRONMENT_OVERRIDES, "")
+    if not text.strip():
         return MappingProxyType({})
-    parsed: dict[str, str] = {}
+    pairs = {}
     for item in text.split(","):
-        operation, sep, implementation_id = item.partition("=")
-        if not sep or not operation.strip() or not implementation_id.strip():
-            raise ValueError(
-                f"{ENVIRONMENT_OVERRIDES} expects comma-separated "
-                f"operation=implementation_id pairs, got {item!r}"
-            )
-        parsed[operation.strip()] = implementation_id.strip()
-    set_implementations(parsed)
-    return MappingProxyType(parsed)
+        match = _PAIR.match(item)
+        if match is None:
+            raise ValueError(f"cannot read {item!r} in {ENVIRONMENT_OVERRIDES}: each entry "
+                             "must be operation=implementation_id")
+        pairs[match.group(1)] = match.group(2)
+    set_implementations(pairs)
+    return MappingProxyType(pairs)
 
 
+# -------------------------------------------------------------- determinism
 def deterministic_required() -> bool:
-    return _DETERMINISTIC.get()
+    return _SETTINGS.get().deterministic
 
 
 @contextmanager
 def deterministic_kernels(enabled: bool = True):
-    """Ask for bitwise-repeatable kernels. Every kernel of the MI355X MoE
-    provider is ordered (no float atomics), so it honours this unconditionally."""
-    token = _DETERMINISTIC.set(bool(enabled))
-    try:
+    """Request bitwise-repeatable kernels inside the block. The MI355X MoE
+    kernels fix every reduction order and use no float atomics, so they are
+    repeatable whether or not this is set."""
+    with _scoped(deterministic=bool(enabled)):
         yield bool(enabled)
-    finally:
-        _DETERMINISTIC.reset(token)
 
 
 def set_deterministic_kernels(enabled: bool = True) -> None:
-    _DETERMINISTIC.set(bool(enabled))
+    _update(deterministic=bool(enabled))
 
 
-def _floating(dtype):
-    if dtype is not None and (not isinstance(dtype, torch.dtype) or not dtype.is_floating_point):
-        raise ValueError(f"weight gradients need a floating dtype or None; got {dtype!r}")
-    return dtype
+# ----------------------------------------------------- weight-gradient dtype
+def _gradient_dtype(dtype):
+    if dtype is None or (isinstance(dtype, torch.dtype) and dtype.is_floating_point):
+        return dtype
+    raise ValueError(f"a weight-gradient dtype must be a floating torch dtype or None, "
+                     f"not {dtype!r}")
 
 
 def weight_gradient_dtype() -> torch.dtype | None:
-    """The dtype weight gradients are returned at; ``None`` = each weight's own."""
-    return _GRAD_DTYPE.get()
+    """The dtype weight gradients come back at; None means each weight's own."""
+    return _SETTINGS.get().gradient_dtype
 
 
 @contextmanager
 def weight_gradients_at(dtype: torch.dtype | None):
-    """Return weight gradients at ``dtype`` inside the block (sums stay fp32)."""
-    token = _GRAD_DTYPE.set(_floating(dtype))
-    try:
+    """Return weight gradients at ``dtype`` inside the block (the sums
+    themselves stay fp32)."""
+    with _scoped(gradient_dtype=_gradient_dtype(dtype)):
         yield dtype
-    finally:
-        _GRAD_DTYPE.reset(token)
 
 
 def set_weight_gradient_dtype(dtype: torch.dtype | None) -> None:
-    _GRAD_DTYPE.set(_floating(dtype))
+    _update(gradient_dtype=_gradient_dtype(dtype))
 
 
+# ------------------------------------------------------------------ tracing
 @contextmanager
 def capture_dispatch():
-    """Record which implementation each resolution picked inside the block."""
+    """Count, per operation, the implementations resolved inside the block."""
     trace: dict[str, dict[str, int]] = {}
-    token = _TRACE.set(trace)
-    try:
+    with _scoped(trace=trace):
         yield trace
-    finally:
-        _TRACE.reset(token)
 
 
 def record_dispatch(operation: str, implementation_id: str) -> None:
-    if torch.compiler.is_compiling():
+    trace = _SETTINGS.get().trace
+    if trace is None or torch.compiler.is_compiling():
         return
-    trace = _TRACE.get()
-    if trace is None:
-        return
-    counts = trace.setdefault(str(operation), {})
-    counts[str(implementation_id)] = counts.get(str(implementation_id), 0) + 1
+    per_operation = trace.setdefault(str(operation), {})
+    key = str(implementation_id)
+    per_operation[key] = per_operation.get(key, 0) + 1
 
 
 def dispatch_manifest(trace: Mapping[str, Mapping[str, int]]) -> Mapping[str, str]:
-    """Turn an unambiguous capture into ``{operation: implementation_id}``."""
+    """``{operation: implementation_id}`` from a capture in which every
+    operation resolved to exactly one implementation."""
     manifest = {}
     for operation, counts in trace.items():
-        used = [name for name, count in counts.items() if count]
-        if len(used) != 1:
-            raise ValueError(
-                f"operation {operation!r} exercised {sorted(used)}; "
-                "a frozen manifest requires exactly one implementation"
-            )
-        manifest[str(operation)] = used[0]
+        chosen = sorted(name for name, count in counts.items() if count)
+        if len(chosen) != 1:
+            raise ValueError(f"{operation!r} resolved to {chosen} in this capture; a manifest "
+                             "pins one implementation per operation")
+        manifest[str(operation)] = chosen[0]
     return MappingProxyType(manifest)
 
 

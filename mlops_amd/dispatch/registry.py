@@ -1,8 +1,13 @@
-"""Implementation records and the process-local catalog of the ``moe`` operation.
+"""The catalog of implementations, keyed by operation and exact ID.
 
-Mirrors the reference's registry contract (``src/mlops/dispatch/registry.py:12-69``):
-an implementation is an immutable record keyed by an exact ID, its forward and
-backward come as a pair or not at all, and registering an ID twice is an error.
+The records are the plugin contract of the reference registry
+(``src/mlops/dispatch/registry.py``): an `Implementation` names one
+operation, one unique ID, its provider, a priority and whether it is
+deterministic; it carries a metadata-only ``supports`` check, the autograd
+entry ``apply`` and, optionally, the explicit ``forward``/``backward`` pair
+and a cost ``estimate``. Here the catalog is a small class of nested dicts;
+reads go through read-only views, and providers are imported on first read
+so that every built-in implementation is present.
 """
 
 from __future__ import annotations
@@ -14,7 +19,7 @@ from types import MappingProxyType
 
 @dataclass(frozen=True)
 class SupportResult:
-    """Whether an implementation accepts one concrete invocation, and why not."""
+    """One implementation's answer for one concrete call: accepted, or why not."""
 
     supported: bool
     reason: str = ""
@@ -33,11 +38,7 @@ class SupportResult:
 
 @dataclass(frozen=True)
 class Implementation:
-    """One stateless implementation of one semantic operation.
-
-    ``supports`` inspects metadata only; ``apply`` is the autograd-visible
-    entry; ``forward``/``backward`` form the explicit (manual VJP) surface.
-    """
+    """A stateless implementation of one semantic operation (see module doc)."""
 
     operation: str
     implementation_id: str
@@ -51,56 +52,73 @@ class Implementation:
     estimate: Callable | None = None
 
     def __post_init__(self) -> None:
-        if not (self.operation and self.implementation_id and self.provider):
-            raise ValueError("operation, implementation_id and provider must be non-empty")
-        if (self.forward is None) is not (self.backward is None):
-            raise ValueError(
-                f"{self.implementation_id}: explicit forward and backward come together"
-            )
+        missing = [name for name in ("operation", "implementation_id", "provider")
+                   if not getattr(self, name)]
+        if missing:
+            raise ValueError(f"an implementation record needs a non-empty {', '.join(missing)}")
+        if (self.forward is None) != (self.backward is None):
+            raise ValueError(f"{self.implementation_id} gives only one of forward/backward; "
+                             "the explicit surface needs them together")
+
+    @property
+    def explicit(self) -> bool:
+        """Whether the record exposes the explicit forward/backward pair."""
+        return self.forward is not None
 
 
-_CATALOG: dict[str, dict[str, Implementation]] = {}
+class _Catalog:
+    def __init__(self) -> None:
+        self.tables: dict[str, dict[str, Implementation]] = {}
+        self._providers_loaded = False
+
+    def add(self, record: Implementation) -> Implementation:
+        table = self.tables.setdefault(str(record.operation), {})
+        key = str(record.implementation_id)
+        if key in table:
+            raise ValueError(f"implementation {key!r} of {record.operation!r} is already "
+                             "registered (duplicate IDs are not allowed)")
+        table[key] = record
+        return record
+
+    def load_providers(self) -> None:
+        if not self._providers_loaded:
+            self._providers_loaded = True
+            from ..providers import ensure_implementations_registered
+
+            ensure_implementations_registered()
+
+    def table(self, operation: str) -> dict[str, Implementation]:
+        self.load_providers()
+        found = self.tables.get(str(operation))
+        if found is None:
+            raise ValueError(f"no operation named {operation!r} is registered "
+                             f"(known: {', '.join(sorted(self.tables))})")
+        return found
+
+
+_catalog = _Catalog()
 
 
 def register_implementation(implementation: Implementation) -> Implementation:
-    """Add ``implementation`` to the catalog and return it; IDs are unique."""
-    table = _CATALOG.setdefault(str(implementation.operation), {})
-    key = str(implementation.implementation_id)
-    if key in table:
-        raise ValueError(
-            f"duplicate implementation ID {key!r} for {implementation.operation!r}"
-        )
-    table[key] = implementation
-    return implementation
-
-
-def _ensure_loaded() -> None:
-    from ..providers import ensure_implementations_registered
-
-    ensure_implementations_registered()
+    """Add a record to the catalog (its ID must be new) and return it."""
+    return _catalog.add(implementation)
 
 
 def implementation_registry() -> Mapping[str, Mapping[str, Implementation]]:
-    """A read-only snapshot of every registered implementation."""
-    _ensure_loaded()
-    return MappingProxyType(
-        {op: MappingProxyType(dict(table)) for op, table in sorted(_CATALOG.items())}
-    )
+    """Read-only view of every operation's implementations."""
+    _catalog.load_providers()
+    return MappingProxyType({operation: MappingProxyType(dict(table))
+                             for operation, table in sorted(_catalog.tables.items())})
 
 
 def implementations_for(operation: str) -> Mapping[str, Implementation]:
-    """The implementations of one exact operation name."""
-    _ensure_loaded()
-    try:
-        return MappingProxyType(_CATALOG[str(operation)])
-    except KeyError as error:
-        raise ValueError(f"unknown semantic operation {operation!r}") from error
+    """Read-only view of one operation's implementations, by ID."""
+    return MappingProxyType(_catalog.table(operation))
 
 
 def frozen_implementation(operation: str, implementation_id: str) -> Implementation:
-    """The record registered under ``implementation_id``."""
-    _ensure_loaded()
-    return _CATALOG[str(operation)][str(implementation_id)]
+    """The record registered under an exact ID."""
+    return _catalog.table(operation)[str(implementation_id)]
 
 
 __all__ = [

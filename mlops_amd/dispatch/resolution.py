@@ -1,9 +1,11 @@
-"""Support filtering and priority selection.
+"""Choosing an implementation for one call.
 
-Selection rule as in the reference (``src/mlops/dispatch/resolution.py:53-112``):
-every implementation's ``supports`` is asked; a forced choice wins if it is
-supported; otherwise the highest priority wins, ties broken by the smaller ID;
-the explicit surface only considers implementations with forward/backward.
+Every registered implementation of the operation is asked whether it
+supports the call (metadata only). The selection rule is the reference's
+(``src/mlops/dispatch/resolution.py``): a forced ID is taken if, and only if,
+it supports the call; otherwise the supporting implementation with the
+highest priority, ties going to the lexicographically smaller ID. The
+explicit surface only considers records with a forward/backward pair.
 """
 
 from __future__ import annotations
@@ -13,16 +15,15 @@ from dataclasses import dataclass
 from types import MappingProxyType
 
 from .context import implementation_override, record_dispatch
-from .registry import (
-    Implementation,
-    SupportResult,
-    frozen_implementation,
-    implementations_for,
-)
+from .registry import Implementation, SupportResult, frozen_implementation, implementations_for
+
+SURFACES = ("semantic", "explicit")
 
 
 @dataclass(frozen=True)
 class ImplementationExplanation:
+    """Every candidate's answer and the choice made from them."""
+
     operation: str
     surface: str
     selected: str | None
@@ -30,70 +31,60 @@ class ImplementationExplanation:
     candidates: Mapping[str, SupportResult]
 
 
-def _ask(implementation: Implementation, *args, surface: str, **kwargs) -> SupportResult:
-    if surface not in ("semantic", "explicit"):
-        return SupportResult.no(f"unknown surface {surface!r}")
-    if surface == "explicit" and implementation.forward is None:
-        return SupportResult.no("implementation does not expose explicit forward/backward")
-    try:
-        answer = implementation.supports(*args, surface=surface, **kwargs)
-    except Exception as error:  # a provider's refusal must not break resolution
-        return SupportResult.no(f"support check failed: {type(error).__name__}: {error}")
+def _as_result(implementation: Implementation, answer) -> SupportResult:
     if isinstance(answer, SupportResult):
         return answer
     if isinstance(answer, bool):
-        return SupportResult(answer, "supported" if answer else "rejected")
-    raise TypeError(
-        f"{implementation.implementation_id}.supports returned {type(answer).__name__}"
-    )
+        return SupportResult.yes() if answer else SupportResult.no("declined")
+    raise TypeError(f"supports() of {implementation.implementation_id} must return a "
+                    f"SupportResult or bool, not {type(answer).__name__}")
 
 
-def explain_implementation(
-    operation: str, *args, surface: str = "semantic", **kwargs
-) -> ImplementationExplanation:
+def _verdict(implementation: Implementation, surface: str, args, kwargs) -> SupportResult:
+    if surface not in SURFACES:
+        return SupportResult.no(f"surface {surface!r} is not one of {SURFACES}")
+    if surface == "explicit" and not implementation.explicit:
+        return SupportResult.no("no explicit forward/backward pair")
+    try:
+        answer = implementation.supports(*args, surface=surface, **kwargs)
+    except Exception as error:  # one provider's failure must not end resolution
+        return SupportResult.no(f"support check raised {type(error).__name__}: {error}")
+    return _as_result(implementation, answer)
+
+
+def _preference(implementation: Implementation):
+    """Sort key: higher priority first, then the smaller ID."""
+    return -implementation.priority, implementation.implementation_id
+
+
+def explain_implementation(operation: str, *args, surface: str = "semantic",
+                           **kwargs) -> ImplementationExplanation:
+    """The candidates' answers and the selection, without dispatching."""
     table = implementations_for(operation)
-    answers = {
-        name: _ask(impl, *args, surface=surface, **kwargs) for name, impl in table.items()
-    }
+    verdicts = {key: _verdict(record, surface, args, kwargs) for key, record in table.items()}
     forced = implementation_override(operation)
     if forced is not None:
-        selected = forced if answers[forced].supported else None
+        selected = forced if verdicts[forced].supported else None
     else:
-        ranked = sorted(
-            (impl for name, impl in table.items() if answers[name].supported),
-            key=lambda impl: (-impl.priority, impl.implementation_id),
-        )
-        selected = ranked[0].implementation_id if ranked else None
-    return ImplementationExplanation(
-        operation=str(operation),
-        surface=str(surface),
-        selected=selected,
-        forced=forced,
-        candidates=MappingProxyType(answers),
-    )
+        accepted = [table[key] for key, verdict in verdicts.items() if verdict.supported]
+        selected = min(accepted, key=_preference).implementation_id if accepted else None
+    return ImplementationExplanation(str(operation), str(surface), selected, forced,
+                                     MappingProxyType(verdicts))
 
 
-def resolve_implementation(
-    operation: str, *args, surface: str = "semantic", **kwargs
-) -> Implementation:
-    """The selected implementation, or ``RuntimeError`` listing every refusal."""
+def resolve_implementation(operation: str, *args, surface: str = "semantic",
+                           **kwargs) -> Implementation:
+    """The implementation to run; RuntimeError with every refusal otherwise."""
     explanation = explain_implementation(operation, *args, surface=surface, **kwargs)
     if explanation.selected is None:
-        reasons = "; ".join(
-            f"{name}: {result.reason}"
-            for name, result in sorted(explanation.candidates.items())
-        )
-        head = (
-            f"forced implementation {explanation.forced!r} is unsupported"
-            if explanation.forced is not None
-            else "no supported implementation"
-        )
-        raise RuntimeError(
-            f"{head} for {explanation.operation!r} on {surface!r} surface; {reasons}"
-        )
-    implementation = frozen_implementation(explanation.operation, explanation.selected)
-    record_dispatch(explanation.operation, implementation.implementation_id)
-    return implementation
+        refusals = "; ".join(f"{key}: {verdict.reason}"
+                             for key, verdict in sorted(explanation.candidates.items()))
+        what = ("no supported implementation" if explanation.forced is None
+                else f"the forced implementation {explanation.forced!r} does not support it")
+        raise RuntimeError(f"{what} for {explanation.operation!r} ({surface} surface): "
+                           f"{refusals}")
+    record_dispatch(explanation.operation, explanation.selected)
+    return frozen_implementation(explanation.operation, explanation.selected)
 
 
 __all__ = ["ImplementationExplanation", "explain_implementation", "resolve_implementation"]

@@ -72,7 +72,7 @@ def test_priority_selection_and_forcing():
     def yes(*a, **k):
         return SupportResult.yes()
 
-    registry._CATALOG["toy"] = {}
+    registry._catalog.tables["toy"] = {}
     try:
         for name, prio in (("b.low", 1), ("a.high", 5), ("c.high", 5)):
             registry.register_implementation(
@@ -87,7 +87,7 @@ def test_priority_selection_and_forcing():
         assert explanation.selected is None
         assert "explicit" in explanation.candidates["a.high"].reason
     finally:
-        del registry._CATALOG["toy"]
+        del registry._catalog.tables["toy"]
 
 
 def test_resolution_error_lists_reasons():
@@ -225,13 +225,13 @@ def test_facade_validation():
 
 def test_environment_override(monkeypatch):
     monkeypatch.setenv("MLOPS_IMPLEMENTATIONS", "moe=mi355x.moe.block_fp8")
-    token = context._FORCED.set(context._FORCED.get())
+    token = context._SETTINGS.set(context._SETTINGS.get())
     try:
         applied = context.apply_environment_overrides()
         assert dict(applied) == {"moe": "mi355x.moe.block_fp8"}
         assert context.implementation_override("moe") == "mi355x.moe.block_fp8"
     finally:
-        context._FORCED.reset(token)
+        context._SETTINGS.reset(token)
     monkeypatch.setenv("MLOPS_IMPLEMENTATIONS", "garbage")
     with pytest.raises(ValueError):
         context.apply_environment_overrides()
