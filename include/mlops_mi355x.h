@@ -341,6 +341,20 @@ size_t mi355x_quantize_weights_current_workspace_size(int experts, int out, int 
 int mi355x_rank_product(const void* a, int rows, int k, const void* bt, int rank,
                         const int32_t* offsets, int experts, void* out, void* stream);
 
+/* Expert LoRA factor gradients as grouped reductions over routed rows:
+ * out[e][m][n] = sum over expert e's rows j of big[j][m] * small[j][n], fp32
+ * sums, with big bf16 [rows, M] (M a multiple of 8), small bf16 [rows, R] (R a
+ * multiple of 16 up to 64), offsets int32 [E+1], out fp32 [E, M, R] (or
+ * [E, R, M] with transposed = 1). Rows are taken in chunks of `chunk` rows of
+ * one expert; workspace: mi355x_rank_grad_workspace_size(rows, E, M, R,
+ * chunk) bytes. No host synchronization. Replaces the per-expert loops of the
+ * factor gradients dB13 = s * sum dh z13^T and dA2 = sum u2 a'^T
+ * (src/mlops/lora/experts.py:53-167; providers/sonicmoe/lora.py:1062). */
+size_t mi355x_rank_grad_workspace_size(int rows, int experts, int m, int rank, int chunk);
+int mi355x_rank_grad(const void* big, int rows, int m, const void* small, int rank,
+                     const int32_t* offsets, int experts, int chunk, int transposed, float* out,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
 /* The up projection with SwiGLU fused: mi355x_gemm_fp8_block in gate/up mode
  * (w13 [E, 2I, K], interleave = 1) writing h [rows, 2I] bf16 interleaved, and
  * from the same bf16 values act = silu(min(g, L)) * clamp(u, +-L) (limit <=

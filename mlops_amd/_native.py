@@ -61,6 +61,8 @@ SIGNATURES = {
         [_P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _P],
     ),
     "mi355x_rank_product": (_I, [_P, _I, _I, _P, _I, _P, _I, _P, _P]),
+    "mi355x_rank_grad_workspace_size": (_S, [_I, _I, _I, _I, _I]),
+    "mi355x_rank_grad": (_I, [_P, _I, _I, _P, _I, _P, _I, _I, _I, _P, _P, _S, _P]),
     "mi355x_gemm_fp8_block_lora": (_I, [_P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _I,
                                         _P, _P]),
     "mi355x_gemm_fp8_block_swiglu": (

@@ -493,6 +493,34 @@ def rank_product(a, bt, offsets):
     return out
 
 
+def rank_grad(big, small, offsets, *, transposed=False, chunk=None):
+    """Per expert ``sum_j big[j]^T small[j]`` over its rows: fp32 ``[E, M, R]``
+    (``[E, R, M]`` when ``transposed``) from bf16 ``big [rows, M]`` and ``small
+    [rows, R]`` (``mi355x_rank_grad``; R a multiple of 16, at most 64)."""
+    rows, m = big.shape
+    rank = small.shape[1]
+    experts = offsets.numel() - 1
+    if big.dtype != torch.bfloat16 or small.dtype != torch.bfloat16:
+        raise ValueError("rank_grad takes bf16 operands")
+    _check(small, (rows, rank), torch.bfloat16, "rank operand")
+    _check(offsets, (experts + 1,), torch.int32, "offsets")
+    device = _on_gpu(big, small, offsets)
+    if chunk is None:
+        # Enough (chunk x 2048-column) blocks to fill the chip twice over.
+        blocks_per_chunk = -(-m // 2048) * (rank // 16)
+        chunk = 256
+        while chunk < 4096 and (rows // (2 * chunk)) * blocks_per_chunk >= 512:
+            chunk *= 2
+    out_shape = (experts, rank, m) if transposed else (experts, m, rank)
+    out = torch.empty(out_shape, dtype=torch.float32, device=device)
+    size = _native.query("mi355x_rank_grad_workspace_size", rows, experts, m, rank, chunk)
+    workspace = torch.empty(size, dtype=torch.uint8, device=device)
+    _timed("rank_grad", device, 2 * rows * m * rank, 2 * rows * (m + rank) + 4 * experts * m * rank,
+           "mi355x_rank_grad", _ptr(big), rows, m, _ptr(small), rank, _ptr(offsets), experts,
+           chunk, int(transposed), _ptr(out), _ptr(workspace), size, _stream(device))
+    return out
+
+
 def _gemm_lora(a, a_scale, w, w_scale, offsets, transposed_scale, interleave, z, b):
     rows, k = a.shape
     experts, n, wk = w.shape

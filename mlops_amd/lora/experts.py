@@ -66,40 +66,27 @@ def _rank16(r: int) -> int:
     return -(-r // 16) * 16
 
 
-def _segments(offsets: torch.Tensor):
-    """``[(expert, start, stop)]`` of the experts that have rows."""
-    bounds = offsets.tolist()
-    return [(e, bounds[e], bounds[e + 1]) for e in range(len(bounds) - 1)
-            if bounds[e + 1] > bounds[e]]
-
-
-def _per_expert(rows: torch.Tensor, factors: torch.Tensor, segments, out_cols: int,
-                *, transpose: bool) -> torch.Tensor:
-    """``rows[s:t] @ factors[e]^T`` (``transpose``) or ``rows[s:t] @ factors[e]``
-    for every expert segment, bf16 out (fp32 sums). The segments cover every
-    row."""
-    out = torch.empty((rows.shape[0], out_cols), dtype=torch.bfloat16, device=rows.device)
-    for e, start, stop in segments:
-        f = factors[e].t() if transpose else factors[e]
-        torch.mm(rows[start:stop], f, out=out[start:stop])
-    return out
-
-
-def _row_rank(rows: torch.Tensor, factors_t: torch.Tensor, offsets, segments) -> torch.Tensor:
-    """``rows[r] @ factors_t[e]^T`` for each expert's rows, bf16 ``[rows, R]``:
-    the thin product kernel for padded ranks up to 64, else per-expert GEMMs."""
-    if factors_t.shape[1] <= 64:
+def _row_rank(rows: torch.Tensor, factors_t: torch.Tensor, offsets) -> torch.Tensor:
+    """``rows[r] @ factors_t[e]^T`` for each expert's rows, bf16 ``[rows, R]``
+    (R a multiple of 16): the thin product kernel, 64 rank columns per call."""
+    rank = factors_t.shape[1]
+    if rank <= 64:
         return kernels.rank_product(rows, factors_t, offsets)
-    return _per_expert(rows, factors_t, segments, factors_t.shape[1], transpose=True)
+    return torch.cat([kernels.rank_product(rows, factors_t[:, c:c + 64].contiguous(), offsets)
+                      for c in range(0, rank, 64)], dim=1)
 
 
-def _factor_grad(left: torch.Tensor, right: torch.Tensor, segments, shape) -> torch.Tensor:
-    """``sum over each expert's rows of left_j right_j^T`` -> fp32 ``[E, *shape]``:
-    ``left[s:t]^T @ right[s:t]`` from bf16 operands with fp32 sums and output."""
-    out = torch.zeros(shape, dtype=torch.float32, device=left.device)
-    for e, start, stop in segments:
-        torch.mm(left[start:stop].t(), right[start:stop], out_dtype=torch.float32, out=out[e])
-    return out
+def _factor_grad(big: torch.Tensor, small: torch.Tensor, offsets, rank: int, *,
+                 transposed: bool) -> torch.Tensor:
+    """Per expert ``sum_j big[j]^T small[j]`` over its rows, fp32, cut to the
+    true ``rank``: ``[E, M, rank]``, or ``[E, rank, M]`` when ``transposed``.
+    bf16 operands with fp32 sums (``mi355x_rank_grad``, no host sync)."""
+    padded = _padded(small, _rank16(rank))
+    parts = [kernels.rank_grad(big, padded[:, c:c + 64].contiguous(), offsets,
+                               transposed=transposed)
+             for c in range(0, padded.shape[1], 64)]
+    out = parts[0] if len(parts) == 1 else torch.cat(parts, dim=1 if transposed else 2)
+    return (out[:, :rank] if transposed else out[..., :rank]).contiguous()
 
 
 def _token_projection(x_tok: torch.Tensor, factors_flat: torch.Tensor, experts: int,
@@ -152,7 +139,6 @@ class _ExpertLoRA(torch.autograd.Function):
             order_l = order.long()
             rows_token = order_l // top_k
             rows_expert = ids.reshape(-1).long()[order_l]
-            segments = _segments(offsets)
             # Factors at the activations' dtype, the scale folded into B.
             a13b = a13.detach().to(torch.bfloat16)
             b13s = (b13.detach().float() * scale).to(torch.bfloat16)
@@ -180,7 +166,7 @@ class _ExpertLoRA(torch.autograd.Function):
             # Down projection: z2 = a @ A2^T per routed row (the thin product
             # streams a once; rank padded to 16).
             z2p = _row_rank(act, _padded(a2b.transpose(1, 2), r2).transpose(1, 2).contiguous(),
-                            offsets, segments)
+                            offsets)
             del act
             z2 = z2p[:, :rank2]
             if current:
@@ -193,7 +179,6 @@ class _ExpertLoRA(torch.autograd.Function):
             aux, probability_sum, _, _ = kernels.router_stats(logits, ids, top_k, mode,
                                                               opts["lengths"])
         ctx.opts = opts
-        ctx.segments = segments
         ctx.w13, ctx.w2 = w13, w2
         ctx.factor_dtypes = (a13.dtype, b13.dtype, a2.dtype, b2.dtype)
         ctx.save_for_backward(hidden, router_weight, logits, weights, ids, order, offsets, slots,
@@ -205,7 +190,7 @@ class _ExpertLoRA(torch.autograd.Function):
     def backward(ctx, grad_output, grad_aux, _grad_counts, grad_probability_sum):
         (hidden, router_weight, logits, weights, ids, order, offsets, slots, h13, z13, z2,
          rows_token, rows_expert, a13b, b13b, a2b, b2b) = ctx.saved_tensors
-        opts, segments = ctx.opts, ctx.segments
+        opts = ctx.opts
         top_k, mode, scale, limit = opts["top_k"], opts["routing_mode"], opts["scale"], opts["limit"]
         need = ctx.needs_input_grad
         width = hidden.shape[-1]
@@ -247,8 +232,7 @@ class _ExpertLoRA(torch.autograd.Function):
             del r
             # Input gradient: dx_j = dh_j @ W13[e] + (dh_j @ (s B13[e])) @ A13[e].
             r13 = _rank16(rank13)
-            u13p = _row_rank(dh, _padded(b13b, r13).transpose(1, 2).contiguous(), offsets,
-                             segments)
+            u13p = _row_rank(dh, _padded(b13b, r13).transpose(1, 2).contiguous(), offsets)
             u13 = u13p[:, :rank13]
             lora_x = (u13p, _padded(a13b.transpose(1, 2), r13))
             if current:
@@ -274,9 +258,9 @@ class _ExpertLoRA(torch.autograd.Function):
                 g = router.split_k_product(zs.to(torch.bfloat16), dy).t()
                 grads[3] = g.reshape(width, experts, rank2).permute(1, 0, 2).contiguous()
             if need[7]:    # A2: sum_j u2_j a'_j^T, a' = score * a
-                grads[2] = _factor_grad(u2, a_prime, segments, (experts, rank2, inter))
+                grads[2] = _factor_grad(a_prime, u2, offsets, rank2, transposed=True)
             if need[6]:    # B13: s * sum_j dh_j z13_j^T (rows back to gate then up)
-                g = _factor_grad(dh, z13, segments, (experts, 2 * inter, rank13))
+                g = _factor_grad(dh, z13, offsets, rank13, transposed=False)
                 grads[1] = gate_up_rows(g.mul_(scale))
             if need[5]:    # A13: sum_j u13_j x_j^T, formed on the token side
                 zd = _scatter_tokens(u13, tokens, experts, rows_token, rows_expert)

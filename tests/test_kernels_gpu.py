@@ -533,3 +533,35 @@ def test_rank_product_matches_fp32(device, counts, k, rank):
     # fp32 sums of exact bf16 products, one bf16 rounding of the result
     assert max_rel(out.float(), want) < 1e-2
     assert frob_rel(out.float(), want) < 4e-3
+
+
+@pytest.mark.parametrize("counts,m,rank,transposed,chunk", [
+    ([0, 37, 5, 0, 150, 16], 512, 16, False, None),     # empty experts, short experts
+    ([700, 1, 1300], 1544, 32, True, 256),              # several chunks per expert, M % 2048
+    ([300, 0, 900], 3072, 48, False, 128),              # three rank passes, chunk tails
+    ([2048, 1024, 4096, 0, 512, 100, 90, 80], 14336, 16, True, None),  # C5-like widths
+])
+def test_rank_grad_matches_fp64(device, counts, m, rank, transposed, chunk):
+    """``sum_j big[j]^T small[j]`` per expert (the LoRA factor gradients)
+    against an fp64 product of the same bf16 operands."""
+    g = torch.Generator().manual_seed(sum(counts) + m + rank)
+    offsets = _ragged(counts)
+    rows = int(offsets[-1])
+    big = torch.randn(rows, m, generator=g).to(torch.bfloat16)
+    small = (torch.randn(rows, rank, generator=g) * 0.3).to(torch.bfloat16)
+    out = K.rank_grad(big.to(device), small.to(device), offsets.to(device),
+                      transposed=transposed, chunk=chunk).cpu()
+    for e in range(len(counts)):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        want = big[lo:hi].double().t() @ small[lo:hi].double()
+        if transposed:
+            want = want.t()
+        got = out[e].double()
+        if hi == lo:
+            assert torch.all(got == 0)
+            continue
+        # fp32 sums of exact bf16 products
+        assert (got - want).abs().max() <= 1e-5 * want.abs().max() + 1e-6, e
+    again = K.rank_grad(big.to(device), small.to(device), offsets.to(device),
+                        transposed=transposed, chunk=chunk).cpu()
+    assert torch.equal(out, again)  # fixed summation order

@@ -92,7 +92,7 @@ def _run_oracle(x, res, wr, w13, w2, a13, b13, a2, b2, dy, *, train_base, mode, 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("mode", ["topk_then_softmax", "softmax_then_topk", "sigmoid_noaux_tc"])
-@pytest.mark.parametrize("rank,train_base", [(16, False), (7, True), (1, False)])
+@pytest.mark.parametrize("rank,train_base", [(16, False), (7, True), (1, False), (80, False)])
 def test_expert_lora_matches_native_on_dequantized_weights(device, mode, rank, train_base):
     case = _inputs(device, rank, seed=rank)
     out, aux, counts, psum, grads = _run_gpu(*case, train_base=train_base, mode=mode)
@@ -276,3 +276,37 @@ def test_expert_lora_at_mixtral_widths(device):
         assert a.shape == b.shape, name
         err = frob_rel(a.float(), b.float())
         assert err < BOUND, f"{name}: relative error {err:.3e}"
+
+
+@pytest.mark.gpu
+@pytest.mark.filterwarnings("ignore:Synchronization debug mode")
+@pytest.mark.parametrize("precision", ["fp8_block", "fp8_current"])
+def test_no_host_synchronization(device, precision):
+    """The reference's provider contract (docs/PROVIDERS.md:64-69): no
+    device-to-host synchronization in forward or backward. torch's sync debug
+    mode turns any synchronizing call (``.item()``, ``.tolist()``, ``nonzero``,
+    a blocking copy) into an error; expert LoRA and ``mlops_amd.moe`` run
+    forward and backward under it."""
+    x, res, wr, w13, w2, a13, b13, a2, b2, dy = _inputs(device, 16, seed=8)
+    factors = [_leaf(t) for t in (a13, b13, a2, b2)]
+    if precision == "fp8_current":
+        w13c, w2c = RowFP8Weight.quantize(w13, interleaved=True), RowFP8Weight.quantize(w2)
+    else:
+        w13c, w2c = BlockFP8Weight.quantize(w13), BlockFP8Weight.quantize(w2)
+    torch.cuda.synchronize(device)
+    previous = torch.cuda.get_sync_debug_mode()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        with pytest.raises(RuntimeError):  # the mode is live: .item() is refused
+            torch.ones(1, device=device).sum().item()
+        xl, wrl = _leaf(x), _leaf(wr)
+        out, aux, _, _ = expert_lora(xl, res, wrl, w13c, w2c, *factors, top_k=TOP_K,
+                                     routing_mode="softmax_then_topk", scale=SCALE)
+        torch.autograd.backward([out, aux], [dy, torch.ones_like(aux)])
+        xm, wrm = _leaf(x), _leaf(wr)
+        out, aux, _, _ = mlops_amd.moe(xm, res, wrm, w13c, w2c, top_k=TOP_K,
+                                       routing_mode="softmax_then_topk")
+        torch.autograd.backward([out, aux], [dy, torch.ones_like(aux)])
+    finally:
+        torch.cuda.set_sync_debug_mode(previous)
+    assert all(f.grad is not None for f in factors) and xm.grad is not None
