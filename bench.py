@@ -35,7 +35,12 @@ HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 
 CONFIGS = {
     "qwen3_30b_a3b": dict(tokens=16384, hidden=2048, inter=768, experts=128, top_k=8),
-    "deepseek_v3_shard": dict(tokens=4096, hidden=7168, inter=2048, experts=32, top_k=8),
+    # One EP rank's share of DeepSeek-V3: 32 local experts and 32768 routed
+    # token-slots, each slot's expert drawn i.i.d. Zipf(s=1.2) (forced through
+    # the routing override, so group sizes are as ragged as the draw makes
+    # them), bf16 master weights N(0, 0.006).
+    "deepseek_v3_shard": dict(tokens=32768, hidden=7168, inter=2048, experts=32, top_k=1,
+                              zipf=1.2, weight_std=0.006),
     "mixtral_8x7b": dict(tokens=8192, hidden=4096, inter=14336, experts=8, top_k=2),
     # Expert LoRA on a frozen block-FP8 base: rank-16 bf16 factors, logits
     # N(0,1) + 2 on expert 0; gradients reach the factors, the router and the
@@ -168,8 +173,9 @@ def make_inputs(cfg, device, seed=0):
     x = torch.randn(t, h, generator=g, device=device).to(torch.bfloat16)
     res = torch.randn(t, h, generator=g, device=device).to(torch.bfloat16)
     wr = torch.randn(e, h, generator=g, device=device) / math.sqrt(h)
-    w13 = (torch.randn(e, 2 * i, h, generator=g, device=device) * 0.02).to(torch.bfloat16)
-    w2 = (torch.randn(e, h, i, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    std = cfg.get("weight_std", 0.02)
+    w13 = (torch.randn(e, 2 * i, h, generator=g, device=device) * std).to(torch.bfloat16)
+    w2 = (torch.randn(e, h, i, generator=g, device=device) * std).to(torch.bfloat16)
     dy = torch.randn(t, h, generator=g, device=device).to(torch.bfloat16)
     return x, res, wr, w13, w2, dy
 
@@ -209,19 +215,49 @@ def lora_step(args, cfg):
     torch.autograd.backward([out, aux], [dy, torch.full_like(aux, 0.01)])
 
 
-def gpu_step(moe, args, cfg):
+def zipf_ids(cfg, device, seed=0):
+    """``[tokens, top_k]`` expert ids with every slot's expert drawn i.i.d. from
+    Zipf(s) over the experts (p_e proportional to (e + 1)^-s); needs top_k = 1
+    (i.i.d. slots could repeat an expert within a token otherwise)."""
+    import numpy as np
+
+    if cfg["top_k"] != 1:
+        raise ValueError("i.i.d. Zipf slots are drawn with top_k = 1")
+    p = np.arange(1, cfg["experts"] + 1, dtype=np.float64) ** -cfg["zipf"]
+    rng = np.random.default_rng(seed)
+    ids = rng.choice(cfg["experts"], size=(cfg["tokens"], 1), p=p / p.sum())
+    return torch.from_numpy(ids.astype(np.int32)).to(device)
+
+
+def gpu_step(moe, args, cfg, forced=None):
     x, res, wr, w13, w2, dy = args
     # A training step starts from cleared gradients (optimizer.zero_grad(set_to_none=True));
     # without this, autograd would add each step's weight gradients into the last ones.
     for t in (wr, w13, w2):
         t.grad = None
-    out, aux, counts, psum = moe(x, res, wr, w13, w2, top_k=cfg["top_k"],
-                                 routing_mode="topk_then_softmax",
-                                 compute_precision=cfg.get("precision", "fp8_block"))
+    kwargs = dict(top_k=cfg["top_k"], routing_mode="topk_then_softmax",
+                  compute_precision=cfg.get("precision", "fp8_block"))
+    if forced is None:
+        out, aux, counts, psum = moe(x, res, wr, w13, w2, **kwargs)
+    else:
+        from mlops_amd.routing import routing_override
+
+        with routing_override([forced]):
+            out, aux, counts, psum = moe(x, res, wr, w13, w2, **kwargs)
     torch.autograd.backward([out, aux], [dy, torch.full_like(aux, 0.01)])
 
 
-def cpu_baseline(cfg_name, sample_tokens=128, budget_s=20.0, max_iters=10):
+def host_cores():
+    """The cores this process may run on (its affinity set; os.cpu_count() can
+    count cores of the machine that are not ours)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(cfg_name, sample_tokens=128, budget_s=20.0, max_iters=10, warmups=2,
+                 threads=None):
     """The reference's native path (``oracle.native_moe``, the restatement of
     moe_reference.py:20-109: every expert on every token, masked, torch
     autograd, fp32 as the reference computes off the GPU) on a bounded sample of the benchmark's own workload: the
@@ -230,7 +266,7 @@ def cpu_baseline(cfg_name, sample_tokens=128, budget_s=20.0, max_iters=10):
     reported as tokens/s of that sample."""
     from oracle import moe_oracle as O
 
-    threads = max(1, min(os.cpu_count() or 1, 16))
+    threads = max(1, min(host_cores(), 16)) if threads is None else int(threads)
     torch.set_num_threads(threads)
     cfg = dict(CONFIGS[cfg_name], tokens=int(sample_tokens))
     x, res, wr, w13, w2, dy = make_inputs(cfg, torch.device("cpu"))
@@ -257,7 +293,7 @@ def cpu_baseline(cfg_name, sample_tokens=128, budget_s=20.0, max_iters=10):
                                               compute_dtype=torch.float32, lora=lora)
         torch.autograd.backward([out, aux], [dy, torch.full_like(aux, 0.01)])
 
-    for _ in range(2):
+    for _ in range(warmups):
         step()
     times = []
     start = time.perf_counter()
@@ -275,7 +311,7 @@ def cpu_baseline(cfg_name, sample_tokens=128, budget_s=20.0, max_iters=10):
                    f"k={cfg['top_k']}{', LoRA r=' + str(cfg['lora_rank']) + ' on a frozen base' if lora else ''}) "
                    f"with {cfg['tokens']} tokens: reference native path (dense "
                    f"per-expert loop, masked, per-expert weight leaves) fwd+bwd in fp32 via torch autograd, median of "
-                   f"{len(times)} runs after 2 warmups"),
+                   f"{len(times)} runs after {warmups} warmups, {threads} threads"),
         "ms_per_step": median * 1e3,
     }
 
@@ -303,6 +339,9 @@ def main():
     parser.add_argument("--calibration-copy-mib", type=int, default=0,
                         help="after the timed steps, run one device copy of this many MiB "
                              "(the known-size kernel that calibrates rocprofv3 byte counters)")
+    parser.add_argument("--calibration-read-mib", type=int, default=0,
+                        help="after the timed steps, run one read-only reduction over this many "
+                             "MiB (calibrates rocprofv3 FETCH_SIZE)")
     parser.add_argument("--vendor-gemm", action="store_true",
                         help="instead of the benchmark line, time the layer's four GEMM shapes "
                              "as dense problems through hipBLASLt and this package's kernels")
@@ -334,7 +373,8 @@ def main():
         _, _, wr, w13, w2, _ = inputs
         for t in (wr, w13, w2):
             t.requires_grad_(True)
-        step = lambda: gpu_step(mlops_amd.moe, inputs, cfg)
+        forced = zipf_ids(cfg, device) if "zipf" in cfg else None
+        step = lambda: gpu_step(mlops_amd.moe, inputs, cfg, forced)
     if args.implementation is not None:
         from mlops_amd.dispatch import set_implementations
 
@@ -391,7 +431,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8_e4m3 (block-scaled) GEMMs, fp32 accumulate, bf16 activations",
-        "data": "synthetic (N(0,1) activations, N(0,0.02) bf16 master weights, random init)",
+        "data": (f"synthetic (N(0,1) activations, N(0,{cfg.get('weight_std', 0.02)}) bf16 master "
+                 "weights, random init"
+                 + (f", expert of each slot drawn Zipf({cfg['zipf']}))" if "zipf" in cfg else ")")),
         "config": {
             "workload": f"{args.config} MoE layer fwd+bwd, block-FP8",
             **cfg,
@@ -416,6 +458,16 @@ def main():
         },
         "kernels": per_kernel,
     }
+    if args.calibration_read_mib > 0:
+        # A read-only kernel of known size: torch's sum of n bytes (the output
+        # is 4 bytes), for the FETCH_SIZE calibration of rocprofv3 runs.
+        n = args.calibration_read_mib << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=device)
+        torch.cuda.synchronize()
+        total = src.sum()
+        torch.cuda.synchronize()
+        result["calibration_read_bytes"] = n
+        del src, total
     if args.calibration_copy_mib > 0:
         n = args.calibration_copy_mib << 20
         src = torch.empty(n, dtype=torch.uint8, device=device).fill_(1)
@@ -426,6 +478,11 @@ def main():
         result["calibration_copy_bytes"] = n
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_sample_tokens)
+        # BASELINE's own CPU case: config 1 (T=256, H=512, I=1024, E=8, k=2) on
+        # every core this process has, 3 warmups, median of 20.
+        result["cpu_baseline_config1"] = cpu_baseline(
+            "config1", CONFIGS["config1"]["tokens"], budget_s=120.0, max_iters=20, warmups=3,
+            threads=host_cores())
     print(json.dumps(result))
 
 

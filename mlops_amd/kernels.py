@@ -134,7 +134,10 @@ def router_topk(
     device = _on_gpu(logits, bias, forced_ids)
     weights = torch.empty((tokens, top_k), dtype=torch.float32, device=device)
     ids = torch.empty((tokens, top_k), dtype=torch.int32, device=device)
-    _native.call(
+    # logits read, weights and ids written (bias / forced ids are small)
+    nbytes = 4 * tokens * experts + 8 * tokens * int(top_k)
+    _timed(
+        "router_topk", device, 0, nbytes,
         "mi355x_router_topk", _ptr(logits), tokens, experts, int(top_k), ROUTING_MODES[mode],
         _ptr(bias), int(n_group), int(topk_group), float(routed_scaling), _ptr(forced_ids),
         _ptr(weights), _ptr(ids), _stream(device),
@@ -171,7 +174,10 @@ def router_stats(logits, ids, top_k: int, mode: str, lengths: Sequence[int]):
     seg_counts = torch.empty((segments, experts), dtype=torch.int32, device=device)
     size = _native.query("mi355x_router_stats_workspace_size", nchunks, experts)
     workspace = torch.empty(size, dtype=torch.uint8, device=device)
-    _native.call(
+    # logits and ids read once; per-expert outputs are negligible
+    nbytes = 4 * tokens * experts + 4 * ids.numel()
+    _timed(
+        "router_stats", device, 0, nbytes,
         "mi355x_router_stats", _ptr(logits), _ptr(ids), tokens, experts, int(top_k),
         ROUTING_MODES[mode], segments, _ptr(seg_offsets), _ptr(table), nchunks, _ptr(aux),
         _ptr(prob_sum), _ptr(seg_counts), _ptr(workspace), size, _stream(device),
@@ -194,7 +200,10 @@ def router_backward(
                      seg_offsets, seg_counts)
     segments = 1 if seg_counts is None else seg_counts.shape[0]
     grad = torch.empty((tokens, experts), dtype=torch.float32, device=device)
-    _native.call(
+    # logits read and their gradient written; weights, ids and dscore read
+    nbytes = 8 * tokens * experts + 12 * tokens * top_k
+    _timed(
+        "router_topk_bwd", device, 0, nbytes,
         "mi355x_router_topk_bwd", _ptr(logits), _ptr(weights), _ptr(ids), _ptr(dscore),
         _ptr(slots), tokens, experts, top_k, ROUTING_MODES[mode], _ptr(grad_aux),
         _ptr(grad_prob_sum), _ptr(offsets), segments, _ptr(seg_offsets), _ptr(seg_counts),
@@ -216,7 +225,9 @@ def permute_plan(ids: torch.Tensor, experts: int):
     slots = torch.empty(ids.shape, dtype=torch.int32, device=device)
     size = _native.query("mi355x_permute_plan_workspace_size", n, experts)
     workspace = torch.empty(size, dtype=torch.uint8, device=device)
-    _native.call(
+    # ids read, order and slots written (counts / offsets are per expert)
+    _timed(
+        "permute_plan", device, 0, 12 * n + 12 * experts,
         "mi355x_permute_plan", _ptr(ids), n, int(experts), _ptr(counts), _ptr(offsets),
         _ptr(order), _ptr(slots), _ptr(workspace), size, _stream(device),
     )
@@ -250,8 +261,9 @@ def quantize_rows(x: torch.Tensor, *, gate_up: bool = False):
     device = _on_gpu(x)
     q = torch.empty((rows, width), dtype=FP8, device=device)
     scales = torch.empty((width // 128, rows), dtype=torch.float32, device=device)
-    _native.call("mi355x_quantize_rows_fp8", _ptr(x), rows, width, width, int(gate_up), _ptr(q),
-                 _ptr(scales), _stream(device))
+    nbytes = 2 * rows * width + rows * width + 4 * rows * (width // 128)
+    _timed("quantize_rows_fp8", device, 0, nbytes, "mi355x_quantize_rows_fp8", _ptr(x), rows,
+           width, width, int(gate_up), _ptr(q), _ptr(scales), _stream(device))
     return q, scales
 
 
@@ -284,8 +296,11 @@ def quantize_weight_blocks(w: torch.Tensor, *, transposed: bool = False):
     scale = torch.empty((experts, -(-out // 128), -(-inner // 128)), dtype=torch.float32,
                         device=device)
     data_t = torch.empty((experts, inner, out), dtype=FP8, device=device) if transposed else None
-    _native.call("mi355x_quantize_weight_blocks", _ptr(w), int(w.dtype == torch.float32),
-                 experts, out, inner, _ptr(data), _ptr(scale), _ptr(data_t), _stream(device))
+    # the weight read once; e4m3 data (and its transpose) and the block scales written
+    nbytes = w.numel() * w.element_size() + w.numel() * (2 if transposed else 1) + scale.numel() * 4
+    _timed("quantize_weight_blocks", device, 0, nbytes, "mi355x_quantize_weight_blocks", _ptr(w),
+           int(w.dtype == torch.float32), experts, out, inner, _ptr(data), _ptr(scale),
+           _ptr(data_t), _stream(device))
     return (data, scale, data_t) if transposed else (data, scale)
 
 
@@ -296,8 +311,8 @@ def transpose_fp8(data: torch.Tensor) -> torch.Tensor:
     device = _on_gpu(data)
     experts, rows, cols = data.shape
     out = torch.empty((experts, cols, rows), dtype=FP8, device=device)
-    _native.call("mi355x_transpose_fp8", _ptr(data), experts, rows, cols, _ptr(out),
-                 _stream(device))
+    _timed("transpose_fp8", device, 0, 2 * data.numel(), "mi355x_transpose_fp8", _ptr(data),
+           experts, rows, cols, _ptr(out), _stream(device))
     return out
 
 
@@ -338,7 +353,11 @@ def quantize_transpose(
     qt = torch.empty((width, padded), dtype=FP8, device=device)
     scales = torch.empty((padded // 128, width), dtype=torch.float32, device=device)
     if assignments > 0:
-        _native.call(
+        # the routed bf16 rows read once (gathered or not), e4m3 [W, P] and the
+        # per-(feature, 128-row block) scales written
+        nbytes = 2 * assignments * width + width * padded + 4 * width * (padded // 128)
+        _timed(
+            "quantize_transpose_fp8", device, 0, nbytes,
             "mi355x_quantize_transpose_fp8", _ptr(x), x.stride(0), width, _ptr(gather),
             int(gather_div), int(gate_up), _ptr(row_blocks), int(padded), _ptr(qt), _ptr(scales),
             _stream(device),
@@ -366,8 +385,9 @@ def unpermute_sum(dx, slots):
     width = dx.shape[1]
     device = _on_gpu(dx, slots)
     out = torch.empty((tokens, width), dtype=dx.dtype, device=device)
-    _native.call("mi355x_unpermute_sum", _ptr(dx), _ptr(slots), tokens, top_k, width, _ptr(out),
-                 _stream(device))
+    nbytes = 2 * tokens * top_k * width + 4 * tokens * top_k + 2 * tokens * width
+    _timed("unpermute_sum", device, 0, nbytes, "mi355x_unpermute_sum", _ptr(dx), _ptr(slots),
+           tokens, top_k, width, _ptr(out), _stream(device))
     return out
 
 
@@ -384,8 +404,11 @@ def routed_swiglu_backward(r, h, weights, order, limit=None, *, dh_out=None):
     dh = torch.empty_like(h) if dh_out is None else dh_out
     a_prime = torch.empty_like(r)
     dscore = torch.empty(rows, dtype=torch.float32, device=device)
-    _native.call("mi355x_routed_swiglu_bwd", _ptr(r), _ptr(h), _ptr(weights), _ptr(order), rows,
-                 width, _limit(limit), _ptr(dh), _ptr(a_prime), _ptr(dscore), _stream(device))
+    # r and h read; dh, a' and dscore written
+    nbytes = 2 * rows * width + 4 * rows * width + 4 * rows * width + 2 * rows * width + 8 * rows
+    _timed("routed_swiglu_bwd", device, 0, nbytes, "mi355x_routed_swiglu_bwd", _ptr(r), _ptr(h),
+           _ptr(weights), _ptr(order), rows, width, _limit(limit), _ptr(dh), _ptr(a_prime),
+           _ptr(dscore), _stream(device))
     return dh, a_prime, dscore
 
 
