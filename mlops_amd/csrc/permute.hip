@@ -132,8 +132,8 @@ __global__ void __launch_bounds__(256) permute_quantize_kernel(
       const int col = base0 + c * 1024 + lane * 16;
       raw[c][0] = raw[c][1] = make_uint4(0, 0, 0, 0);
       if (col < width) {
-        raw[c][0] = *(const uint4*)(src + col);
-        raw[c][1] = *(const uint4*)(src + col + 8);
+        raw[c][0] = load_stream(src + col);
+        raw[c][1] = load_stream(src + col + 8);
       }
     }
 #pragma unroll
@@ -155,7 +155,7 @@ __global__ void __launch_bounds__(256) permute_quantize_kernel(
 #pragma unroll
         for (int j = 0; j < 32; ++j) {
           if (j < top_k) {
-            *(uint4*)(q + (size_t)dest[j] * width + col) = packed;
+            store_stream(q + (size_t)dest[j] * width + col, packed);
             if ((lane & 7) == 0) scales[(size_t)kb * rows + dest[j]] = s;
           }
         }
@@ -174,7 +174,7 @@ __global__ void __launch_bounds__(256) combine_kernel(
   for (int col = threadIdx.x * 8; col < width; col += blockDim.x * 8) {
     float acc[8];
     if (residual != nullptr) {
-      uint4 r = *(const uint4*)(residual + (size_t)t * width + col);
+      uint4 r = load_stream(residual + (size_t)t * width + col);
       uint32_t w4[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -189,7 +189,7 @@ __global__ void __launch_bounds__(256) combine_kernel(
       const size_t flat = (size_t)t * top_k + j;
       const int slot = slots[flat];
       const float w = weights != nullptr ? weights[flat] : 1.0f;
-      uint4 r = *(const uint4*)(y + (size_t)slot * width + col);
+      uint4 r = load_stream(y + (size_t)slot * width + col);
       uint32_t w4[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -207,7 +207,7 @@ __global__ void __launch_bounds__(256) combine_kernel(
     o.y = pack_bf16x2(acc[2], acc[3]);
     o.z = pack_bf16x2(acc[4], acc[5]);
     o.w = pack_bf16x2(acc[6], acc[7]);
-    *(uint4*)(out + (size_t)t * width + col) = o;
+    store_stream(out + (size_t)t * width + col, o);
   }
 }
 

@@ -205,43 +205,58 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __re
 // stores full 128-byte act lines.
 constexpr int kSwUnits = 4;
 
+// The kernel is ALU-bound (exp, reciprocal and a correctly rounded division
+// per element), so the unit -> (row, group) split is done once per group of
+// lanes in 32-bit arithmetic and then stepped, and the clamp is a template
+// flag rather than a per-element select.
+template <bool kClamp>
 __global__ void __launch_bounds__(256) swiglu_quantize_kernel(const uint16_t* __restrict__ h,
                                                               int rows, int width, float limit,
                                                               uint8_t* __restrict__ q,
                                                               float* __restrict__ scales,
                                                               uint16_t* __restrict__ act_out) {
-  const int groups = width / 128;
-  const long long units = (long long)rows * groups;
+  const uint32_t groups = (uint32_t)width / 128u;
+  const uint32_t units = (uint32_t)rows * groups;  // < 2^31, checked on the host
   const int lane16 = threadIdx.x & 15;
-  const long long g0 = ((long long)blockIdx.x * 16 + (threadIdx.x >> 4)) * kSwUnits;
+  const uint32_t g0 = (blockIdx.x * 16u + (threadIdx.x >> 4)) * (uint32_t)kSwUnits;
+  const uint32_t r0 = g0 / groups;
+  const uint32_t grp0 = g0 - r0 * groups;
+  uint32_t urow[kSwUnits], ugrp[kSwUnits];
+  {
+    uint32_t r = r0, grp = grp0;
+#pragma unroll
+    for (int u = 0; u < kSwUnits; ++u) {
+      urow[u] = r;
+      ugrp[u] = grp;
+      if (++grp == groups) { grp = 0; ++r; }
+    }
+  }
   uint4 ha[kSwUnits], hb[kSwUnits];
 #pragma unroll
   for (int u = 0; u < kSwUnits; ++u) {
-    const long long unit = g0 + u;
     ha[u] = hb[u] = make_uint4(0, 0, 0, 0);
-    if (unit < units) {
-      const long long r = unit / groups;
-      const int j = (int)(unit - r * groups) * 128 + lane16 * 8;
-      const uint16_t* src = h + r * 2 * width + 2 * j;
-      ha[u] = *(const uint4*)src;
-      hb[u] = *(const uint4*)(src + 8);
+    if (g0 + u < units) {
+      const uint16_t* src = h + (size_t)urow[u] * 2 * width + 2 * (ugrp[u] * 128 + lane16 * 8);
+      ha[u] = load_stream(src);
+      hb[u] = load_stream(src + 8);
     }
   }
 #pragma unroll
   for (int u = 0; u < kSwUnits; ++u) {
-    const long long unit = g0 + u;
-    if (unit >= units) break;  // uniform over the 16-lane group
-    const long long r = unit / groups;
-    const int grp = (int)(unit - r * groups);
-    const int j = grp * 128 + lane16 * 8;
+    if (g0 + u >= units) break;  // uniform over the 16-lane group
+    const size_t r = urow[u];
+    const uint32_t grp = ugrp[u];
+    const int j = (int)grp * 128 + lane16 * 8;
     float a[8], b[8], act[8];
     unpack_bf16x8(ha[u], a);
     unpack_bf16x8(hb[u], b);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float g0v = a[2 * i], u0 = a[2 * i + 1], g1 = b[2 * i], u1 = b[2 * i + 1];
-      clamp_gate_up(g0v, u0, limit);
-      clamp_gate_up(g1, u1, limit);
+      if (kClamp) {
+        clamp_gate_up(g0v, u0, limit);
+        clamp_gate_up(g1, u1, limit);
+      }
       act[i] = silu_f(g0v) * u0;
       act[4 + i] = silu_f(g1) * u1;
     }
@@ -250,7 +265,7 @@ __global__ void __launch_bounds__(256) swiglu_quantize_kernel(const uint16_t* __
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(act[i]));
     amax = group_max<16>(amax);
     const float sc = fmaxf(amax * kInv448, kMinScale);
-    *(uint2*)(q + r * width + j) = quant8(act, sc);
+    store_stream8(q + r * width + j, quant8(act, sc));
     if (lane16 == 0) scales[(size_t)grp * rows + r] = sc;
     if (act_out != nullptr) {
       uint4 o;
@@ -258,7 +273,7 @@ __global__ void __launch_bounds__(256) swiglu_quantize_kernel(const uint16_t* __
       o.y = pack_bf16x2(act[2], act[3]);
       o.z = pack_bf16x2(act[4], act[5]);
       o.w = pack_bf16x2(act[6], act[7]);
-      *(uint4*)(act_out + r * width + j) = o;
+      store_stream(act_out + r * width + j, o);
     }
   }
 }
@@ -322,13 +337,12 @@ __device__ __forceinline__ void transpose_tile_pow2(bool active, uint16_t* tile,
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float sc = pow2_ceil(fmaxf(m[j] * kInv448, kMinScale));
-      const float inv = 1.0f / sc;  // exact: sc is a power of two
-      auto q = [&](int i) { return fminf(fmaxf(v[i][j] * inv, -kE4M3Max), kE4M3Max); };
+      // v / sc is exact (sc a power of two) and within +-448 (v bf16).
       uint4 w;
-      w.x = f32x4_to_e4m3(q(0), q(1), q(2), q(3));
-      w.y = f32x4_to_e4m3(q(4), q(5), q(6), q(7));
-      w.z = f32x4_to_e4m3(q(8), q(9), q(10), q(11));
-      w.w = f32x4_to_e4m3(q(12), q(13), q(14), q(15));
+      w.x = f32x4_to_e4m3_pow2(v[0][j], v[1][j], v[2][j], v[3][j], sc);
+      w.y = f32x4_to_e4m3_pow2(v[4][j], v[5][j], v[6][j], v[7][j], sc);
+      w.z = f32x4_to_e4m3_pow2(v[8][j], v[9][j], v[10][j], v[11][j], sc);
+      w.w = f32x4_to_e4m3_pow2(v[12][j], v[13][j], v[14][j], v[15][j], sc);
       *(uint4*)&staged[(4 * fg + j) * kQtLine + rb * 16] = w;
       if (rb == 0)
         scales[(size_t)pb * width_f + tile_feature(4 * fg + j, feat0, c0, gate_half)] = sc;
@@ -391,6 +405,7 @@ __global__ void __launch_bounds__(256) quantize_transpose_kernel(
 // h and dh may be the same buffer (dh written in place over h): each lane
 // loads its h values before it stores their gradients, and no other lane
 // reads them, so they carry no __restrict__.
+template <bool kClamp>
 __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
     const uint16_t* __restrict__ rmat, const uint16_t* h,
     const float* __restrict__ weights, const int32_t* __restrict__ order, int rows, int width,
@@ -437,7 +452,7 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
           const float rg = i < 4 ? a[2 * i] : b[2 * (i - 4)];
           const float ru = i < 4 ? a[2 * i + 1] : b[2 * (i - 4) + 1];
           float gv = rg, uv = ru;
-          clamp_gate_up(gv, uv, limit);
+          if (kClamp) clamp_gate_up(gv, uv, limit);
           const float sig = sigmoid_f(gv);
           const float silu = gv * sig;
           const float act = silu * uv;
@@ -445,7 +460,7 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
           const float gg = r[i] * score;
           float dgate = gg * uv * (sig + silu * (1.0f - sig));
           float dup = gg * silu;
-          if (limit > 0.0f) {
+          if (kClamp) {
             dgate = rg <= limit ? dgate : 0.0f;
             dup = (ru >= -limit && ru <= limit) ? dup : 0.0f;
           }
@@ -488,6 +503,7 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
 //     power-of-two scales, as quantize_transpose_kernel does.
 constexpr int kSbThreads = 512;
 
+template <bool kClamp>
 __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
     const uint16_t* __restrict__ rmat, const uint16_t* __restrict__ h,
     const float* __restrict__ weights, const int32_t* __restrict__ order,
@@ -552,7 +568,7 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
         const float rg = i < 4 ? a[2 * i] : b[2 * (i - 4)];
         const float ru = i < 4 ? a[2 * i + 1] : b[2 * (i - 4) + 1];
         float gv = rg, uv = ru;
-        clamp_gate_up(gv, uv, limit);
+        if (kClamp) clamp_gate_up(gv, uv, limit);
         const float sig = sigmoid_f(gv);
         const float silu = gv * sig;
         const float act = silu * uv;
@@ -560,7 +576,7 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
         const float gg = rv[i] * score[pass];
         float dgate = gg * uv * (sig + silu * (1.0f - sig));
         float dup = gg * silu;
-        if (limit > 0.0f) {
+        if (kClamp) {
           dgate = rg <= limit ? dgate : 0.0f;
           dup = (ru >= -limit && ru <= limit) ? dup : 0.0f;
         }
@@ -718,10 +734,11 @@ extern "C" int mi355x_swiglu_quantize_fp8(const void* h, int rows, int width, fl
   MI355X_REQUIRE(width > 0 && width % 128 == 0, "swiglu_quantize: I must be a multiple of 128");
   if (rows == 0) return MI355X_OK;
   const long long units = (long long)rows * (width / 128);
+  MI355X_REQUIRE(units < (1LL << 31), "swiglu_quantize: rows x I/128 must stay below 2^31");
   const long long blocks = (units + 16 * kSwUnits - 1) / (16 * kSwUnits);
-  hipLaunchKernelGGL(swiglu_quantize_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     (hipStream_t)stream, (const uint16_t*)h, rows, width, limit, q, scales,
-                     (uint16_t*)act);
+  auto kernel = limit > 0.0f ? swiglu_quantize_kernel<true> : swiglu_quantize_kernel<false>;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)h, rows, width, limit, q, scales, (uint16_t*)act);
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
 }
@@ -764,7 +781,8 @@ extern "C" int mi355x_routed_swiglu_bwd(const void* r, const void* h, const floa
                                         void* dh, void* a_prime, float* dscore, void* stream) {
   MI355X_REQUIRE(width > 0 && width % 8 == 0, "routed_swiglu_bwd: width must be a multiple of 8");
   if (rows == 0) return MI355X_OK;
-  hipLaunchKernelGGL(routed_swiglu_bwd_kernel, dim3((rows + 3) / 4), dim3(256), 0,
+  auto kernel = limit > 0.0f ? routed_swiglu_bwd_kernel<true> : routed_swiglu_bwd_kernel<false>;
+  hipLaunchKernelGGL(kernel, dim3((rows + 3) / 4), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)r, (const uint16_t*)h, weights, order,
                      rows, width, limit, (uint16_t*)dh, (uint16_t*)a_prime, dscore);
   MI355X_LAUNCH_CHECK();
@@ -792,8 +810,8 @@ int swiglu_bwd_launch(const void* r, const void* h, const float* weights, const 
   if (rows == 0) return MI355X_OK;
   hipStream_t s = (hipStream_t)stream;
   float* dsp = (float*)workspace;
-  hipLaunchKernelGGL(swiglu_bwd_quantize_kernel, dim3(padded / 128, width / 128), dim3(kSbThreads),
-                     0, s, (const uint16_t*)r, (const uint16_t*)h, weights, order, row_blocks,
+  auto kernel = limit > 0.0f ? swiglu_bwd_quantize_kernel<true> : swiglu_bwd_quantize_kernel<false>;
+  hipLaunchKernelGGL(kernel, dim3(padded / 128, width / 128), dim3(kSbThreads), 0, s, (const uint16_t*)r, (const uint16_t*)h, weights, order, row_blocks,
                      rows, width, padded, limit, dhq, dh_scales, dh_t, dh_t_scales, ap_t,
                      ap_t_scales, dsp, (uint16_t*)dh);
   MI355X_LAUNCH_CHECK();
