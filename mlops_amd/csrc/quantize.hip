@@ -12,7 +12,7 @@ namespace {
 template <typename T>
 __device__ __forceinline__ void load8(const T* p, float* v);
 template <>
-__device__ __forceinline__ void load8<uint16_t>(const uint16_t* p, float* v) { load_bf16x8(p, v); }
+__device__ __forceinline__ void load8<uint16_t>(const uint16_t* p, float* v) { unpack_bf16x8(load_stream(p), v); }
 template <>
 __device__ __forceinline__ void load8<float>(const float* p, float* v) {
   float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
@@ -54,25 +54,22 @@ __global__ void __launch_bounds__(256) weight_blocks_kernel(
   for (int p = 0; p < 8; ++p) {
     const int row = bo * 128 + p * 16 + rsub;
     uint2 packed = quant8(v[p], s);
-    if (row < out && col < in) *(uint2*)(q + ebase + (size_t)row * in + col) = packed;
+    if (row < out && col < in) store_stream8(q + ebase + (size_t)row * in + col, packed);
     if (q_t != nullptr) *(uint2*)&tile[p * 16 + rsub][lane16 * 8] = packed;
   }
   if (q_t == nullptr) return;
   __syncthreads();
-  // Transposed copy: thread writes 8 consecutive source rows of one column.
+  // Transposed copy: thread writes 16 consecutive source rows of one column.
 #pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    const int idx = p * 256 + threadIdx.x;  // 2048 = 128 columns x 16 row groups
-    const int c = idx >> 4, rg = idx & 15;
-    uint32_t lo = 0, hi = 0;
+  for (int p = 0; p < 4; ++p) {
+    const int idx = p * 256 + threadIdx.x;  // 1024 = 128 columns x 8 row groups
+    const int c = idx >> 3, rg = idx & 7;
+    uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      lo |= (uint32_t)tile[rg * 8 + i][c] << (8 * i);
-      hi |= (uint32_t)tile[rg * 8 + 4 + i][c] << (8 * i);
-    }
-    const int tcol = bi * 128 + c, trow = bo * 128 + rg * 8;
+    for (int i = 0; i < 16; ++i) w[i >> 2] |= (uint32_t)tile[rg * 16 + i][c] << (8 * (i & 3));
+    const int tcol = bi * 128 + c, trow = bo * 128 + rg * 16;
     if (tcol < in && trow < out)
-      *(uint2*)(q_t + ebase + (size_t)tcol * out + trow) = make_uint2(lo, hi);
+      store_stream(q_t + ebase + (size_t)tcol * out + trow, make_uint4(w[0], w[1], w[2], w[3]));
   }
 }
 
