@@ -268,6 +268,7 @@ __global__ void __launch_bounds__(256) router_stats_final_kernel(
   float aux_part = 0.0f;
   for (int e = threadIdx.x; e < experts; e += blockDim.x) {
     float total_p = 0.0f;
+    int total_c = 0;
     int c = 0;
     for (int s = 0; s < segments; ++s) {
       float sp = 0.0f;
@@ -281,6 +282,7 @@ __global__ void __launch_bounds__(256) router_stats_final_kernel(
       }
       seg_counts[(size_t)s * experts + e] = sc;
       total_p += sp;
+      total_c += sc;
       if (mode == MI355X_ROUTE_SIGMOID_NOAUX_TC) {
         int len = seg_offsets == nullptr ? tokens : seg_offsets[s + 1] - seg_offsets[s];
         float freq = (float)sc * (float)experts / (float)(top_k * len);
@@ -289,7 +291,8 @@ __global__ void __launch_bounds__(256) router_stats_final_kernel(
     }
     prob_sum[e] = total_p;
     if (mode != MI355X_ROUTE_SIGMOID_NOAUX_TC) {
-      float freq = (float)seg_counts[e] / (float)(tokens * top_k);
+      // softmax modes: one aux over all rows, whatever the segments
+      float freq = (float)total_c / (float)(tokens * top_k);
       aux_part += freq * (total_p / (float)tokens);
     }
   }
@@ -368,9 +371,11 @@ __global__ void __launch_bounds__(kReduceThreads) router_stats_reduce_kernel(
   float aux_part = 0.0f;
   for (int e = tid; e < experts; e += kReduceThreads) {
     float total_p = 0.0f;
+    int total_c = 0;
     for (int s = 0; s < segments; ++s) {
       const float sp = sp_lds[s * experts + e];
       total_p += sp;
+      total_c += sc_lds[s * experts + e];
       if (mode == MI355X_ROUTE_SIGMOID_NOAUX_TC) {
         const int len = seg_offsets == nullptr ? tokens : seg_offsets[s + 1] - seg_offsets[s];
         const float freq = (float)sc_lds[s * experts + e] * (float)experts / (float)(top_k * len);
@@ -379,7 +384,8 @@ __global__ void __launch_bounds__(kReduceThreads) router_stats_reduce_kernel(
     }
     prob_sum[e] = total_p;
     if (mode != MI355X_ROUTE_SIGMOID_NOAUX_TC) {
-      const float freq = (float)sc_lds[e] / (float)(tokens * top_k);
+      // softmax modes: one aux over all rows, whatever the segments
+      const float freq = (float)total_c / (float)(tokens * top_k);
       aux_part += freq * (total_p / (float)tokens);
     }
   }

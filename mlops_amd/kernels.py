@@ -447,24 +447,30 @@ def swiglu_bwd_quantize(r, h, weights, order, offsets, *, padded=None, limit=Non
     return dhq, dhs, dht, dhts, apt, apts, dscore, padded
 
 
-def swiglu_bwd_bf16(r, h, weights, order, offsets, *, padded, row_blocks, limit=None):
+def swiglu_bwd_bf16(r, h, weights, order, offsets, *, padded, row_blocks, limit=None,
+                    transposed_dh=True, transposed_ap=True):
     """The fused routed SwiGLU backward with bf16 ``dh [A, 2I]`` (h's
-    interleaved order) and both transposed operands of the weight gradients
+    interleaved order) and the transposed operands of the weight gradients
     (``mi355x_swiglu_bwd_bf16``): ``(dh, dh_t [2I, P], dh_t_scales [P/128, 2I],
-    ap_t [I, P], ap_t_scales [P/128, I], dscore fp32 [A])``."""
+    ap_t [I, P], ap_t_scales [P/128, I], dscore fp32 [A])``; ``dh_t`` (for
+    dW13) and ``ap_t`` (for dW2) are skipped, and None, when not asked for."""
     rows, width = r.shape
     _check(h, (rows, 2 * width), torch.bfloat16, "h")
     device = _on_gpu(r, h, weights, order, offsets)
     _check(row_blocks, (padded // 128, 2), torch.int32, "row_blocks")
     dh = torch.empty((rows, 2 * width), dtype=torch.bfloat16, device=device)
-    dht = torch.empty((2 * width, padded), dtype=FP8, device=device)
-    dhts = torch.empty((padded // 128, 2 * width), dtype=torch.float32, device=device)
-    apt = torch.empty((width, padded), dtype=FP8, device=device)
-    apts = torch.empty((padded // 128, width), dtype=torch.float32, device=device)
+    dht = dhts = apt = apts = None
+    if transposed_dh:
+        dht = torch.empty((2 * width, padded), dtype=FP8, device=device)
+        dhts = torch.empty((padded // 128, 2 * width), dtype=torch.float32, device=device)
+    if transposed_ap:
+        apt = torch.empty((width, padded), dtype=FP8, device=device)
+        apts = torch.empty((padded // 128, width), dtype=torch.float32, device=device)
     dscore = torch.empty(rows, dtype=torch.float32, device=device)
     nbytes = _native.query("mi355x_swiglu_bwd_quantize_workspace_size", rows, width)
     work = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
-    traffic = 6 * rows * width + 4 * rows * width + (3 * width * padded if rows else 0)
+    written_t = (2 * transposed_dh + transposed_ap) * width * padded if rows else 0
+    traffic = 6 * rows * width + 4 * rows * width + written_t
     _timed("swiglu_bwd_bf16", device, 0, traffic, "mi355x_swiglu_bwd_bf16", _ptr(r), _ptr(h),
            _ptr(weights), _ptr(order), _ptr(row_blocks), rows, width, int(padded), _limit(limit),
            _ptr(dh), _ptr(dht), _ptr(dhts), _ptr(apt), _ptr(apts), _ptr(dscore), _ptr(work),

@@ -148,7 +148,8 @@ def backward_routed(grad_output, grad_aux, grad_probability_sum, h2, router_weig
             blocks = kernels.padded_row_blocks(offsets, padded)
             dh, dh_t, dh_ts, ap_t, ap_ts, dscore = kernels.swiglu_bwd_bf16(
                 r, h13, route_weights.reshape(-1), order, offsets, padded=padded,
-                row_blocks=blocks, limit=swiglu_limit)
+                row_blocks=blocks, limit=swiglu_limit, transposed_dh=need_w13,
+                transposed_ap=need_w2)
         else:
             dh, _, dscore = kernels.routed_swiglu_backward(
                 r, h13, route_weights.reshape(-1), order, swiglu_limit)

@@ -302,3 +302,30 @@ def test_explicit_surface_equals_autograd_and_repeats(device):
     assert torch.equal(out, r["out"])
     for got, name in zip(grads, ("gx", "gres", "gr", "g13", "g2")):
         assert torch.equal(got, r[name]), name
+
+
+@pytest.mark.parametrize("frozen", ["w13", "w2", "both"])
+def test_frozen_weights_skip_their_gradients(device, frozen):
+    """With one expert weight (or both) frozen, the fused SwiGLU backward
+    writes only the transposed operands the remaining weight gradients read,
+    and every gradient equals the all-trainable run's bitwise."""
+    x, res, wr, w13, w2, dy = _inputs(device, seed=49)
+    kw = dict(top_k=2, routing_mode="softmax_then_topk")
+    full = _run(x, res, wr, w13, w2, dy, **kw)
+    xl, wrl = x.clone().requires_grad_(True), wr.clone().requires_grad_(True)
+    w13c = RowFP8Weight.quantize(w13.detach(), interleaved=True)
+    w2c = RowFP8Weight.quantize(w2.detach())
+    if frozen not in ("w13", "both"):
+        w13c.requires_grad_(True)
+    if frozen not in ("w2", "both"):
+        w2c.requires_grad_(True)
+    out, aux, _, _ = mlops_amd.moe(xl, res, wrl, w13c, w2c, **kw)
+    torch.autograd.backward([out, aux], [dy, torch.ones_like(aux) * 0.3])
+    assert torch.equal(out, full["out"])
+    assert torch.equal(xl.grad, full["gx"]) and torch.equal(wrl.grad, full["gr"])
+    assert (w13c.grad is None) == (frozen in ("w13", "both"))
+    assert (w2c.grad is None) == (frozen in ("w2", "both"))
+    if w13c.grad is not None:
+        assert torch.equal(w13c.grad, full["g13"])
+    if w2c.grad is not None:
+        assert torch.equal(w2c.grad, full["g2"])

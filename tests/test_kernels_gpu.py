@@ -68,12 +68,19 @@ def test_router_forced_ids(device):
         assert max_rel(w.cpu(), ow) < 1e-5
 
 
-@pytest.mark.parametrize("mode,lengths", [("topk_then_softmax", None),
-                                          ("softmax_then_topk", None),
-                                          ("sigmoid_noaux_tc", (100, 37, 363))])
-def test_router_stats_and_backward(device, mode, lengths):
-    g = torch.Generator().manual_seed(13)
-    tokens, experts, top_k = 500, 32, 4
+@pytest.mark.parametrize("mode,lengths,experts,top_k", [
+    ("topk_then_softmax", None, 32, 4),
+    ("softmax_then_topk", None, 32, 4),
+    ("topk_then_softmax", (300, 200), 32, 4),         # softmax aux over all segments
+    ("sigmoid_noaux_tc", (100, 37, 363), 32, 4),
+    ("softmax_then_topk", (77, 250, 173), 512, 8),   # 8 logits per lane, odd segments
+    ("sigmoid_noaux_tc", (201, 299), 512, 6),
+    ("topk_then_softmax", None, 64, 32),               # top_k near the lane limit
+    ("sigmoid_noaux_tc", (13, 487), 64, 32),
+])
+def test_router_stats_and_backward(device, mode, lengths, experts, top_k):
+    g = torch.Generator().manual_seed(13 + experts + top_k)
+    tokens = 500
     lengths = (tokens,) if lengths is None else lengths
     logits = torch.randn(tokens, experts, generator=g)
     w, ids = O.route(logits, top_k, mode)
