@@ -39,11 +39,18 @@ __device__ __forceinline__ Tile describe(const int* prefix, const int32_t* __res
   t.row0 = __builtin_amdgcn_readfirstlane(offsets[t.e] + (mt - prefix[t.e]) * BM);
   t.nvalid = __builtin_amdgcn_readfirstlane(min(BM, offsets[t.e + 1] - t.row0));
   // Tiles that share an operand panel run at the same time on neighbouring
-  // CUs of one XCD; starting each at a different K step means one of them
-  // takes a panel step's L2 miss and the others find it in L2 later,
-  // instead of all of them waiting on the same miss together. The grouped
-  // order runs unrotated: there the CUs sharing a panel read it together.
-  t.rot = rotate ? __builtin_amdgcn_readfirstlane((tile * 7) % nk) : 0;
+  // CUs of one XCD; consecutive tiles start one K step apart, over a window
+  // of three steps, so that one of them takes a panel step's L2 miss and the
+  // others find the line in L2 a step later. The window is kept small: a
+  // rotation over all K steps (7t mod nk) took the same time but spread an
+  // expert's ~30 concurrent tiles over its whole 5 MB of panels, more than a
+  // 4 MB L2, and the up projection read its operands 3.6 times from HBM
+  // instead of 1.05 times (2% faster over C3's four launches). Short K
+  // (under 8 steps, e.g. the down projection) keeps the full rotation, which
+  // measured ~3% faster there, with panels small enough to stay in L2. The
+  // grouped order runs unrotated: there the CUs sharing a panel read it
+  // together.
+  t.rot = rotate ? __builtin_amdgcn_readfirstlane(nk >= 8 ? tile % 3 : (tile * 7) % nk) : 0;
   return t;
 }
 
