@@ -7,23 +7,21 @@
 // up to 64) and fp32 sums. Rows are expert-sorted (offsets[E+1]); nothing is
 // read on the host, so the call does not synchronize.
 //
-// The work streams `big` once from HBM (R/16 times for R > 16). Each block
-// takes a chunk of up to `chunk` rows of one expert and 2048 columns: a
-// thread owns 8 consecutive columns and 16 rank sums for each (128 fp32
-// accumulators), and walks the chunk's rows in order, reading its 16-byte
-// slice of each row; the chunk's rank values sit in LDS as fp32 and every
-// lane reads the same ones (broadcast). Partial sums of each chunk go to a
-// workspace; a second kernel adds an expert's chunks in chunk order. Both
-// orders are fixed, so the result is bitwise repeatable.
+// The work streams `big` once from HBM (R/16 times for R > 16), so it must
+// run at HBM speed: with 16 ranks it is 16 FMAs per element read, which the
+// VALU alone cannot keep up with, so the products run on the bf16 MFMA
+// (v_mfma_f32_16x16x32_bf16: 16 columns x 16 ranks over 32 rows). Each block
+// takes a chunk of up to `chunk` rows of one expert and 256 columns, 64 per
+// wave, and walks the chunk 64 rows at a time through LDS. Partial sums of
+// each chunk go to a workspace; a second kernel adds an expert's chunks in
+// chunk order. Both orders are fixed, so the result is bitwise repeatable.
 #include "common.h"
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kCols = 8;                      // columns per thread
-constexpr int kBlockCols = kThreads * kCols;  // 2048
+constexpr int kThreads = 256;                 // 4 waves
+constexpr int kBlockColsMfma = 256;          // big columns per block, 64 per wave
 constexpr int kRanks = 16;                    // rank sums per pass (blockIdx.z picks the 16)
-constexpr int kStageRows = 256;               // rank rows staged in LDS at a time
 constexpr int kMaxExperts = 1024;
 
 // prefix[e] = number of chunks before expert e (chunks of `chunk` rows).
@@ -49,11 +47,31 @@ __device__ __forceinline__ int expert_of_chunk(const int* prefix, int experts, i
   return lo;
 }
 
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
+
+// A stage: 64 rows x 256 columns of big (32 KB) and 64 rows x 16 ranks of
+// small, copied row-major into LDS with coalesced 16-byte loads. An MFMA
+// operand needs 8 consecutive rows of one column per lane (the reduction runs
+// over rows), so each fragment is gathered with eight 2-byte LDS reads; the
+// row pitches put the four 8-row groups of a fragment read in different banks.
+constexpr int kStRows = 64;
+constexpr int kBigPitch = 2 * kBlockColsMfma + 8;   // bytes per staged big row (520)
+constexpr int kSmallPitch = 2 * kRanks + 8;         // bytes per staged rank row (40)
+
+__device__ __forceinline__ bf16x8_t gather8(const uint8_t* base, int pitch) {
+  u16x8_t v;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = *(const uint16_t*)(base + i * pitch);
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
 __global__ void __launch_bounds__(kThreads) rank_grad_partial_kernel(
     const uint16_t* __restrict__ big, int M, const uint16_t* __restrict__ small, int R,
     const int32_t* __restrict__ offsets, int experts, int chunk, float* __restrict__ partial) {
   __shared__ int prefix[kMaxExperts + 1];
-  __shared__ float4 svals[kStageRows][kRanks / 4];
+  __shared__ __align__(16) uint8_t big_s[kStRows * kBigPitch];
+  __shared__ __align__(16) uint8_t small_s[kStRows * kSmallPitch];
   chunk_prefix(offsets, experts, chunk, prefix);
   const int c = blockIdx.y;
   if (c >= prefix[experts]) return;  // uniform over the block
@@ -61,86 +79,65 @@ __global__ void __launch_bounds__(kThreads) rank_grad_partial_kernel(
   const int row0 = offsets[e] + (c - prefix[e]) * chunk;
   const int row1 = min(row0 + chunk, offsets[e + 1]);
   const int n0 = blockIdx.z * kRanks;
-  const int col = blockIdx.x * kBlockCols + threadIdx.x * kCols;
-  const bool active = col < M;  // M is a multiple of 8
+  const int m0 = blockIdx.x * kBlockColsMfma;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lcol = (tid & 31) * 8;  // this thread's 8 columns of the copy
+  const bool col_ok = m0 + lcol < M;  // M is a multiple of 8
 
-  float acc[kCols][kRanks];
+  v4f acc[4];
 #pragma unroll
-  for (int i = 0; i < kCols; ++i)
-#pragma unroll
-    for (int n = 0; n < kRanks; ++n) acc[i][n] = 0.0f;
+  for (int i = 0; i < 4; ++i) acc[i] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
 
-  for (int s0 = row0; s0 < row1; s0 += kStageRows) {
-    const int s1 = min(s0 + kStageRows, row1);
-    __syncthreads();  // the previous stage's rank values are consumed
-    {
-      const int j = s0 + threadIdx.x;
-      float v[kRanks];
-      if (j < s1) {
-        const uint4* p = (const uint4*)(small + (size_t)j * R + n0);
-        unpack_bf16x8(p[0], v);
-        unpack_bf16x8(p[1], v + 8);
-      } else {
+  for (int s0 = row0; s0 < row1; s0 += kStRows) {
+    // Loads first (rows past the chunk read as zeros), then the LDS stores.
+    uint4 v[8];
 #pragma unroll
-        for (int n = 0; n < kRanks; ++n) v[n] = 0.0f;
-      }
+    for (int i = 0; i < 8; ++i) {
+      const int r = s0 + i * 8 + (tid >> 5);
+      v[i] = (r < row1 && col_ok) ? load_stream(big + (size_t)r * M + m0 + lcol)
+                                  : make_uint4(0, 0, 0, 0);
+    }
+    uint4 sv = make_uint4(0, 0, 0, 0);
+    if (tid < 2 * kStRows) {
+      const int r = s0 + (tid >> 1);
+      if (r < row1) sv = *(const uint4*)(small + (size_t)r * R + n0 + (tid & 1) * 8);
+    }
+    __syncthreads();  // the previous stage's fragments are read
 #pragma unroll
-      for (int q = 0; q < kRanks / 4; ++q)
-        svals[threadIdx.x][q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    for (int i = 0; i < 8; ++i) {
+      uint8_t* d = big_s + (i * 8 + (tid >> 5)) * kBigPitch + 2 * lcol;
+      *(uint2*)d = make_uint2(v[i].x, v[i].y);
+      *(uint2*)(d + 8) = make_uint2(v[i].z, v[i].w);
+    }
+    if (tid < 2 * kStRows) {
+      uint8_t* d = small_s + (tid >> 1) * kSmallPitch + (tid & 1) * 16;
+      *(uint2*)d = make_uint2(sv.x, sv.y);
+      *(uint2*)(d + 8) = make_uint2(sv.z, sv.w);
     }
     __syncthreads();
-    if (!active) continue;
-    const uint16_t* src = big + (size_t)s0 * M + col;
-    // Rows in groups of 4 with the group's loads issued first.
-    int j = s0;
-    for (; j + 4 <= s1; j += 4) {
-      uint4 raw[4];
+    // D[m][n] += sum over 32 rows of big[row][m] * small[row][n], twice.
+    const int g = lane >> 4, l16 = lane & 15;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) raw[u] = *(const uint4*)(src + (size_t)(j - s0 + u) * M);
+    for (int kk = 0; kk < kStRows; kk += 32) {
+      const int rr = kk + 8 * g;
+      const bf16x8_t b = gather8(small_s + rr * kSmallPitch + 2 * l16, kSmallPitch);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        float b[kCols];
-        unpack_bf16x8(raw[u], b);
-        const int lj = j - s0 + u;
-#pragma unroll
-        for (int q = 0; q < kRanks / 4; ++q) {
-          const float4 s = svals[lj][q];
-#pragma unroll
-          for (int i = 0; i < kCols; ++i) {
-            acc[i][4 * q] = fmaf(b[i], s.x, acc[i][4 * q]);
-            acc[i][4 * q + 1] = fmaf(b[i], s.y, acc[i][4 * q + 1]);
-            acc[i][4 * q + 2] = fmaf(b[i], s.z, acc[i][4 * q + 2]);
-            acc[i][4 * q + 3] = fmaf(b[i], s.w, acc[i][4 * q + 3]);
-          }
-        }
-      }
-    }
-    for (; j < s1; ++j) {
-      float b[kCols];
-      unpack_bf16x8(*(const uint4*)(src + (size_t)(j - s0) * M), b);
-      const int lj = j - s0;
-#pragma unroll
-      for (int q = 0; q < kRanks / 4; ++q) {
-        const float4 s = svals[lj][q];
-#pragma unroll
-        for (int i = 0; i < kCols; ++i) {
-          acc[i][4 * q] = fmaf(b[i], s.x, acc[i][4 * q]);
-          acc[i][4 * q + 1] = fmaf(b[i], s.y, acc[i][4 * q + 1]);
-          acc[i][4 * q + 2] = fmaf(b[i], s.z, acc[i][4 * q + 2]);
-          acc[i][4 * q + 3] = fmaf(b[i], s.w, acc[i][4 * q + 3]);
-        }
+      for (int mb = 0; mb < 4; ++mb) {
+        const int m = wave * 64 + mb * 16 + l16;
+        const bf16x8_t a = gather8(big_s + rr * kBigPitch + 2 * m, kBigPitch);
+        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[mb], 0, 0, 0);
       }
     }
   }
-  if (!active) return;
-  // partial[c][m][n] (n fastest, R wide): 16 rank sums of a column are 64 bytes.
-  float* dst = partial + ((size_t)c * M + col) * R + n0;
+  // acc[mb][i]: column m = m0 + wave * 64 + mb * 16 + 4 * (lane / 16) + i,
+  // rank n = n0 + lane % 16. partial[c][m][n], R wide.
 #pragma unroll
-  for (int i = 0; i < kCols; ++i)
+  for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-    for (int q = 0; q < kRanks / 4; ++q)
-      *(float4*)(dst + (size_t)i * R + 4 * q) =
-          make_float4(acc[i][4 * q], acc[i][4 * q + 1], acc[i][4 * q + 2], acc[i][4 * q + 3]);
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + wave * 64 + mb * 16 + 4 * (lane >> 4) + i;
+      if (m < M) partial[((size_t)c * M + m) * R + n0 + (lane & 15)] = acc[mb][i];
+    }
 }
 
 // out[e] = sum of expert e's chunks in chunk order (zeros for an expert with
@@ -202,7 +199,7 @@ extern "C" int mi355x_rank_grad(const void* big, int rows, int m, const void* sm
                  chunks);
   float* partial = (float*)workspace;
   if (rows > 0) {
-    const dim3 grid((m + kBlockCols - 1) / kBlockCols, (unsigned)chunks, rank / kRanks);
+    const dim3 grid((m + kBlockColsMfma - 1) / kBlockColsMfma, (unsigned)chunks, rank / kRanks);
     hipLaunchKernelGGL(rank_grad_partial_kernel, grid, dim3(kThreads), 0, s,
                        (const uint16_t*)big, m, (const uint16_t*)small, rank, offsets, experts,
                        chunk, partial);

@@ -535,8 +535,8 @@ def rank_grad(big, small, offsets, *, transposed=False, chunk=None):
     _check(offsets, (experts + 1,), torch.int32, "offsets")
     device = _on_gpu(big, small, offsets)
     if chunk is None:
-        # Enough (chunk x 2048-column) blocks to fill the chip twice over.
-        blocks_per_chunk = -(-m // 2048) * (rank // 16)
+        # Enough (chunk x 256-column) blocks to fill the chip twice over.
+        blocks_per_chunk = -(-m // 256) * (rank // 16)
         chunk = 256
         while chunk < 4096 and (rows // (2 * chunk)) * blocks_per_chunk >= 512:
             chunk *= 2
@@ -544,7 +544,8 @@ def rank_grad(big, small, offsets, *, transposed=False, chunk=None):
     out = torch.empty(out_shape, dtype=torch.float32, device=device)
     size = _native.query("mi355x_rank_grad_workspace_size", rows, experts, m, rank, chunk)
     workspace = torch.empty(size, dtype=torch.uint8, device=device)
-    _timed("rank_grad", device, 2 * rows * m * rank, 2 * rows * (m + rank) + 4 * experts * m * rank,
+    # HBM-bound: big is streamed once; the products are on the bf16 MFMA
+    _timed("rank_grad", device, 0, 2 * rows * (m + rank) + 4 * experts * m * rank,
            "mi355x_rank_grad", _ptr(big), rows, m, _ptr(small), rank, _ptr(offsets), experts,
            chunk, int(transposed), _ptr(out), _ptr(workspace), size, _stream(device))
     return out
