@@ -190,6 +190,18 @@ int mi355x_routed_swiglu_bwd(const void* r, const void* h, const float* weights,
                              const int32_t* order, int rows, int width, float limit, void* dh,
                              void* a_prime, float* dscore, void* stream);
 
+/* mi355x_routed_swiglu_bwd that also row-quantizes dh, gate-first, from its
+ * bf16 values: dhq e4m3 [A, 2I] and dh_scales [2I/128][A], equal to
+ * mi355x_quantize_rows_fp8 (gate_up = 1) on the dh it writes, without reading
+ * dh back (expert LoRA needs the bf16 dh too, for its rank products). I must
+ * be a multiple of 128. Replaces routed_swiglu_rows_backward followed by
+ * quantize_rows_fp8(gate_up=True) (kernels/quack_moe/swiglu_rows.py:278-318;
+ * quantize_rows.py:140). */
+int mi355x_routed_swiglu_bwd_rows_fp8(const void* r, const void* h, const float* weights,
+                                      const int32_t* order, int rows, int width, float limit,
+                                      void* dh, void* a_prime, float* dscore, uint8_t* dhq,
+                                      float* dh_scales, void* stream);
+
 /* Fused routed SwiGLU backward and the quantizers its outputs feed, from
  * r = dy @ W2 [rows, I] (bf16), h [rows, 2I] interleaved and the route score
  * of each sorted row (weights[order[row]]), with dh and a' rounded to bf16 as

@@ -47,6 +47,7 @@ SIGNATURES = {
     "mi355x_unpermute_combine": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
     "mi355x_unpermute_sum": (_I, [_P, _P, _I, _I, _I, _P, _P]),
     "mi355x_routed_swiglu_bwd": (_I, [_P, _P, _P, _P, _I, _I, _F, _P, _P, _P, _P]),
+    "mi355x_routed_swiglu_bwd_rows_fp8": (_I, [_P, _P, _P, _P, _I, _I, _F, _P, _P, _P, _P, _P, _P]),
     "mi355x_swiglu_bwd_quantize_workspace_size": (_S, [_I, _I]),
     "mi355x_swiglu_bwd_quantize": (
         _I,

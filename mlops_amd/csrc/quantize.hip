@@ -407,7 +407,7 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
     const uint16_t* __restrict__ rmat, const uint16_t* h,
     const float* __restrict__ weights, const int32_t* __restrict__ order, int rows, int width,
     float limit, uint16_t* dh, uint16_t* __restrict__ a_prime,
-    float* __restrict__ dscore) {
+    float* __restrict__ dscore, uint8_t* __restrict__ dhq, float* __restrict__ dhs) {
   const int wave = threadIdx.x >> 6, lane = lane_id();
   const int row = blockIdx.x * 4 + wave;
   if (row >= rows) return;
@@ -475,6 +475,32 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
         *(uint4*)(dh + (size_t)row * 2 * width + 2 * j) = o0;
         *(uint4*)(dh + (size_t)row * 2 * width + 2 * j + 8) = o1;
         *(uint4*)(a_prime + (size_t)row * width + j) = o2;
+        if (dhq != nullptr) {
+          // dh row-quantized gate-first from its bf16 values, as the row
+          // quantizer would read them back: the 16 lanes of this 128-column
+          // block hold gate block j / 128 and up block I / 128 + j / 128
+          // (width is a multiple of 128 here, so the group is all valid).
+          const uint32_t w8[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+          float gq[8], uq[8];
+          float ga = 0.0f, ua = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            gq[i] = bf16_to_f32(w8[i] & 0xffff);
+            uq[i] = bf16_to_f32(w8[i] >> 16);
+            ga = fmaxf(ga, fabsf(gq[i]));
+            ua = fmaxf(ua, fabsf(uq[i]));
+          }
+          ga = group_max<16>(ga);
+          ua = group_max<16>(ua);
+          const float sg = fmaxf(ga * kInv448, kMinScale), su = fmaxf(ua * kInv448, kMinScale);
+          uint8_t* qrow = dhq + (size_t)row * 2 * width;
+          *(uint2*)(qrow + j) = quant8(gq, sg);
+          *(uint2*)(qrow + width + j) = quant8(uq, su);
+          if ((lane & 15) == 0) {
+            dhs[(size_t)(j >> 7) * rows + row] = sg;
+            dhs[(size_t)(width / 128 + (j >> 7)) * rows + row] = su;
+          }
+        }
       }
       dot = group_sum<16>(dot);
       const int blocks = min(4, (width - base + 127) / 128);  // 128-column blocks here
@@ -773,17 +799,39 @@ extern "C" int mi355x_quantize_transpose_fp8(const void* x, int64_t pitch, int w
   return MI355X_OK;
 }
 
-extern "C" int mi355x_routed_swiglu_bwd(const void* r, const void* h, const float* weights,
-                                        const int32_t* order, int rows, int width, float limit,
-                                        void* dh, void* a_prime, float* dscore, void* stream) {
-  MI355X_REQUIRE(width > 0 && width % 8 == 0, "routed_swiglu_bwd: width must be a multiple of 8");
+namespace {
+int routed_swiglu_launch(const void* r, const void* h, const float* weights, const int32_t* order,
+                         int rows, int width, float limit, void* dh, void* a_prime, float* dscore,
+                         uint8_t* dhq, float* dhs, void* stream) {
   if (rows == 0) return MI355X_OK;
   auto kernel = limit > 0.0f ? routed_swiglu_bwd_kernel<true> : routed_swiglu_bwd_kernel<false>;
   hipLaunchKernelGGL(kernel, dim3((rows + 3) / 4), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)r, (const uint16_t*)h, weights, order,
-                     rows, width, limit, (uint16_t*)dh, (uint16_t*)a_prime, dscore);
+                     rows, width, limit, (uint16_t*)dh, (uint16_t*)a_prime, dscore, dhq, dhs);
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
+}
+}  // namespace
+
+extern "C" int mi355x_routed_swiglu_bwd(const void* r, const void* h, const float* weights,
+                                        const int32_t* order, int rows, int width, float limit,
+                                        void* dh, void* a_prime, float* dscore, void* stream) {
+  MI355X_REQUIRE(width > 0 && width % 8 == 0, "routed_swiglu_bwd: width must be a multiple of 8");
+  return routed_swiglu_launch(r, h, weights, order, rows, width, limit, dh, a_prime, dscore,
+                              nullptr, nullptr, stream);
+}
+
+extern "C" int mi355x_routed_swiglu_bwd_rows_fp8(const void* r, const void* h,
+                                                 const float* weights, const int32_t* order,
+                                                 int rows, int width, float limit, void* dh,
+                                                 void* a_prime, float* dscore, uint8_t* dhq,
+                                                 float* dh_scales, void* stream) {
+  MI355X_REQUIRE(width > 0 && width % 128 == 0,
+                 "routed_swiglu_bwd_rows_fp8: I must be a multiple of 128");
+  MI355X_REQUIRE(dhq != nullptr && dh_scales != nullptr,
+                 "routed_swiglu_bwd_rows_fp8: dhq and its scales are required");
+  return routed_swiglu_launch(r, h, weights, order, rows, width, limit, dh, a_prime, dscore, dhq,
+                              dh_scales, stream);
 }
 
 extern "C" size_t mi355x_swiglu_bwd_quantize_workspace_size(int rows, int width) {

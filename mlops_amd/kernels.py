@@ -412,6 +412,26 @@ def routed_swiglu_backward(r, h, weights, order, limit=None, *, dh_out=None):
     return dh, a_prime, dscore
 
 
+def routed_swiglu_backward_rows(r, h, weights, order, limit=None):
+    """``routed_swiglu_backward`` plus dh row-quantized gate-first from its
+    bf16 values: ``(dh, a', dscore, dhq e4m3 [A, 2I], dh_scales [2I/128, A])``,
+    the last two equal to ``quantize_rows(dh, gate_up=True)``."""
+    rows, width = r.shape
+    _check(h, (rows, 2 * width), torch.bfloat16, "h")
+    device = _on_gpu(r, h, weights, order)
+    dh = torch.empty_like(h)
+    a_prime = torch.empty_like(r)
+    dscore = torch.empty(rows, dtype=torch.float32, device=device)
+    dhq = torch.empty((rows, 2 * width), dtype=FP8, device=device)
+    dhs = torch.empty((2 * width // 128, rows), dtype=torch.float32, device=device)
+    # r and h read; dh, a', dscore, dhq and its scales written
+    nbytes = (6 + 6 + 2) * rows * width + 8 * rows + 4 * rows * (2 * width // 128)
+    _timed("routed_swiglu_bwd_rows", device, 0, nbytes, "mi355x_routed_swiglu_bwd_rows_fp8",
+           _ptr(r), _ptr(h), _ptr(weights), _ptr(order), rows, width, _limit(limit), _ptr(dh),
+           _ptr(a_prime), _ptr(dscore), _ptr(dhq), _ptr(dhs), _stream(device))
+    return dh, a_prime, dscore, dhq, dhs
+
+
 def swiglu_bwd_quantize(r, h, weights, order, offsets, *, padded=None, limit=None,
                         transposed_dh=True, transposed_ap=True, row_blocks=None):
     """Fused routed SwiGLU backward + quantizers (see the C header):

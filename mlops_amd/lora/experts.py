@@ -227,8 +227,13 @@ class _ExpertLoRA(torch.autograd.Function):
                 w2_t = provider.transposed_data(ctx.w2)
                 r = kernels.gemm(dyq, dys, w2_t, w2_scale, offsets, transposed_scale=True,
                                  lora=lora_r)
-            dh, a_prime, dscore = kernels.routed_swiglu_backward(
-                r, h13, weights.reshape(-1), order, limit)
+            if current:
+                dh, a_prime, dscore = kernels.routed_swiglu_backward(
+                    r, h13, weights.reshape(-1), order, limit)
+            else:
+                # dh row-quantized for the input-gradient GEMM in the same pass
+                dh, a_prime, dscore, dhq, dhs = kernels.routed_swiglu_backward_rows(
+                    r, h13, weights.reshape(-1), order, limit)
             del r
             # Input gradient: dx_j = dh_j @ W13[e] + (dh_j @ (s B13[e])) @ A13[e].
             r13 = _rank16(rank13)
@@ -240,7 +245,6 @@ class _ExpertLoRA(torch.autograd.Function):
                 dhq, dhs = kernels.quantize_rows_current(dh)
                 dx = kernels.gemm_rowwise(dhq, dhs, w13_t, w13_ts, offsets, lora=lora_x)
             else:
-                dhq, dhs = kernels.quantize_rows(dh, gate_up=True)
                 w13_t = provider.transposed_data(ctx.w13)
                 dx = kernels.gemm(dhq, dhs, w13_t, w13_scale, offsets, transposed_scale=True,
                                   lora=lora_x)

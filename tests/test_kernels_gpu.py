@@ -431,6 +431,26 @@ def test_routed_swiglu_backward(device, limit):
 
 
 @pytest.mark.parametrize("limit", [None, 0.7])
+@pytest.mark.parametrize("rows,width", [(256, 384), (37, 1152), (1, 128)])
+def test_routed_swiglu_backward_rows_matches_unfused(device, limit, rows, width):
+    """The routed backward with dh row-quantized in the same pass writes the
+    plain kernel's dh, a' and dscore, and the row quantizer's bytes and scales
+    on that dh (widths past one 1024-column chunk, ragged row counts)."""
+    g = torch.Generator().manual_seed(rows + width)
+    r = torch.randn(rows, width, generator=g).to(torch.bfloat16).to(device)
+    h = torch.randn(rows, 2 * width, generator=g).to(torch.bfloat16).to(device)
+    h[0] *= 40.0
+    weights = torch.rand(rows, generator=g).to(device)
+    order = torch.randperm(rows, generator=g).int().to(device)
+    dh, ap, ds, dhq, dhs = K.routed_swiglu_backward_rows(r, h, weights, order, limit)
+    dh_ref, ap_ref, ds_ref = K.routed_swiglu_backward(r, h, weights, order, limit)
+    q_ref, s_ref = K.quantize_rows(dh_ref, gate_up=True)
+    assert torch.equal(dh, dh_ref) and torch.equal(ap, ap_ref) and torch.equal(ds, ds_ref)
+    assert torch.equal(_bytes(dhq), _bytes(q_ref))
+    assert torch.equal(dhs, s_ref)
+
+
+@pytest.mark.parametrize("limit", [None, 0.7])
 def test_swiglu_bwd_quantize_matches_unfused(device, limit):
     """The fused kernel's outputs are, byte for byte, the unfused kernels'
     (routed SwiGLU backward -> bf16 dh / a' -> row and transposing quantizers),
