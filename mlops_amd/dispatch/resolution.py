@@ -87,4 +87,26 @@ def resolve_implementation(operation: str, *args, surface: str = "semantic",
     return frozen_implementation(explanation.operation, explanation.selected)
 
 
-__all__ = ["ImplementationExplanation", "explain_implementation", "resolve_implementation"]
+def implementation_pairs(operations) -> Mapping[str, Mapping[str, Mapping[str, str]]]:
+    """For each operation, the two forcing maps a verifier compares: the
+    implementation resolution prefers (``"default"``) and the preferred
+    ``native_torch`` provider record (``"native_torch"``), each as
+    ``{operation: implementation ID}`` ready for ``use_implementations``.
+    Support is not consulted (the pair is fixed by the catalog alone); an
+    operation with no native_torch record raises ValueError (reference
+    ``src/mlops/dispatch/resolution.py:113-140``)."""
+    pairs = {}
+    for operation in map(str, operations):
+        ranked = sorted(implementations_for(operation).values(), key=_preference)
+        natives = [record for record in ranked if record.provider == "native_torch"]
+        if not natives:
+            raise ValueError(f"{operation!r} has no native_torch implementation to pair with")
+        pairs[operation] = MappingProxyType({
+            "default": MappingProxyType({operation: ranked[0].implementation_id}),
+            "native_torch": MappingProxyType({operation: natives[0].implementation_id}),
+        })
+    return MappingProxyType(pairs)
+
+
+__all__ = ["ImplementationExplanation", "explain_implementation", "implementation_pairs",
+           "resolve_implementation"]

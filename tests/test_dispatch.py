@@ -393,3 +393,83 @@ def test_protocol_containers_are_recognised(monkeypatch):
     # A wrong scale shape is not the protocol: treated as a plain weight.
     bad = ProtocolBlockWeight(torch.zeros(8, 256, 256, dtype=fp8), torch.ones(8, 1, 1))
     assert block_parts(bad) is None
+
+
+class _WrongCube(torch.autograd.Function):
+    """x**3 with a backward that misses the factor 3."""
+
+    @staticmethod
+    def forward(ctx, x):
+        ctx.save_for_backward(x)
+        return x ** 3
+
+    @staticmethod
+    def backward(ctx, grad):
+        (x,) = ctx.saved_tensors
+        return grad * x * x
+
+
+def _toy_catalog():
+    def yes(*a, **k):
+        return SupportResult.yes()
+
+    def float32_only(x, **k):
+        return SupportResult.yes() if x.dtype == torch.float32 else SupportResult.no("float32 only")
+
+    registry._catalog.tables["toy.cube"] = {}
+    for name, provider_name, prio, supports, apply in (
+            ("toy.native", "native_torch", 0, yes, lambda x: x ** 3),
+            ("toy.wrong", "t", 7, yes, _WrongCube.apply),
+            ("toy.narrow", "t", 9, float32_only, lambda x: x ** 3)):
+        registry.register_implementation(
+            Implementation("toy.cube", name, provider_name, prio, True, supports, apply))
+
+
+def test_gradcheck_reports_each_implementation_exactly():
+    from mlops_amd.dispatch import GradcheckCase, gradcheck_implementation, gradcheck_implementations
+
+    _toy_catalog()
+    try:
+        x = torch.randn(5, dtype=torch.float64, requires_grad=True)
+        results = {r.implementation_id: r for r in gradcheck_implementations(
+            [GradcheckCase("toy.cube", (x,))])}
+        assert list(results) == ["toy.narrow", "toy.native", "toy.wrong"]  # sorted IDs
+        assert results["toy.native"].status == "passed"
+        assert results["toy.wrong"].status == "failed"
+        # the float32-only record declines float64 and is skipped, not replaced
+        assert results["toy.narrow"].status == "skipped"
+        assert "float32 only" in results["toy.narrow"].reason
+        with pytest.raises(Exception):
+            gradcheck_implementation("toy.cube", "toy.wrong", (x,), raise_exception=True)
+        with pytest.raises(ValueError, match="no implementation 'toy.none'"):
+            gradcheck_implementation("toy.cube", "toy.none", (x,))
+    finally:
+        del registry._catalog.tables["toy.cube"]
+
+
+def test_gradcheck_of_the_mi355x_moe_is_skipped_off_gpu():
+    from mlops_amd.dispatch import gradcheck_implementation
+
+    args = [a.double().requires_grad_() if a.is_floating_point() else a for a in _args()]
+    result = gradcheck_implementation(
+        "moe", provider.IMPLEMENTATION_ID, args,
+        kwargs=dict(top_k=2, routing_mode="topk_then_softmax", compute_precision="fp8_block"))
+    assert result.status == "skipped" and result.reason
+
+
+def test_implementation_pairs():
+    from mlops_amd.dispatch import implementation_pairs
+
+    _toy_catalog()
+    try:
+        pairs = implementation_pairs(["toy.cube"])
+        assert dict(pairs["toy.cube"]["default"]) == {"toy.cube": "toy.narrow"}
+        assert dict(pairs["toy.cube"]["native_torch"]) == {"toy.cube": "toy.native"}
+        with use_implementation("toy.cube", pairs["toy.cube"]["native_torch"]["toy.cube"]):
+            x = torch.tensor([2.0])
+            assert resolve_implementation("toy.cube", x).apply(x).item() == 8.0
+    finally:
+        del registry._catalog.tables["toy.cube"]
+    # The MoE catalog has no plain-torch record: the hot path has no fallback.
+    with pytest.raises(ValueError, match="no native_torch"):
+        implementation_pairs(["moe"])
