@@ -97,7 +97,7 @@ int mi355x_permute_plan(const int32_t* ids, int assignments, int experts, int64_
  * device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc). Its histogram scratch is a fixed 4 MiB file-scope
  * device array, one per GPU, held until the process ends, so it never calls
- * hipMalloc/hipFree. Sizes beyond that scratch (chunks of 4096 assignments x
+ * hipMalloc/hipFree. Sizes beyond that scratch (chunks of 1024 assignments x
  * experts above 2^20 - 64 int32) are refused with MI355X_EINVAL;
  * mi355x_permute_plan_noalloc_max_assignments(E) gives the largest A for E.
  * Calls that overlap on one GPU share the scratch and race. */

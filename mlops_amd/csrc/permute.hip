@@ -7,7 +7,7 @@
 
 namespace {
 
-constexpr int kPlanChunk = 4096;  // assignments per plan block
+constexpr int kPlanChunk = 1024;  // assignments per plan block
 constexpr int kPlanThreads = 256;
 constexpr int kMaxExperts = 1024;
 
@@ -32,12 +32,21 @@ __global__ void __launch_bounds__(kMaxExperts) plan_scan_kernel(
     int32_t* __restrict__ offsets) {
   __shared__ int scan[kMaxExperts];
   const int e = threadIdx.x;
+  // Sixteen chunks' counts are loaded before any of them is rewritten, so a
+  // pass costs chunks / 16 memory round trips rather than one per chunk.
+  constexpr int kBatch = 16;
   int total = 0;
   if (e < experts) {
-    for (int c = 0; c < chunks; ++c) {
-      int v = hist[(size_t)c * experts + e];
-      hist[(size_t)c * experts + e] = total;
-      total += v;
+    for (int c0 = 0; c0 < chunks; c0 += kBatch) {
+      int v[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        v[j] = c0 + j < chunks ? hist[(size_t)(c0 + j) * experts + e] : 0;
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        if (c0 + j < chunks) hist[(size_t)(c0 + j) * experts + e] = total;
+        total += v[j];
+      }
     }
   }
   scan[e] = total;
@@ -52,7 +61,15 @@ __global__ void __launch_bounds__(kMaxExperts) plan_scan_kernel(
   if (e < experts) {
     counts[e] = total;
     offsets[e] = base;
-    for (int c = 0; c < chunks; ++c) hist[(size_t)c * experts + e] += base;
+    for (int c0 = 0; c0 < chunks; c0 += kBatch) {
+      int v[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        v[j] = c0 + j < chunks ? hist[(size_t)(c0 + j) * experts + e] : 0;
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        if (c0 + j < chunks) hist[(size_t)(c0 + j) * experts + e] = v[j] + base;
+    }
   }
   if (e == 0) offsets[experts] = n;
 }

@@ -30,25 +30,56 @@ __device__ __forceinline__ int wave_argmax(float v, int idx) {
   return idx;
 }
 
+// Maximum over the wave, in every lane: within each row of 16 lanes by four
+// DPP steps (quad swaps, then the half-row and row mirrors), then over the
+// four rows' results read as scalars. No LDS round trips.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+  const int b = __float_as_int(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 // One selection round: the best remaining eligible candidate of the wave
-// (stable descending order). `taken` is the lane's bitmask of used slots.
+// (stable descending order: the largest value, ties to the lower expert id).
+// `taken` is the lane's bitmask of used slots. Each lane keeps its best slot
+// (the lower slot on ties); the wave maximum of those values comes from DPP
+// steps, and the lanes holding it are found with one ballot per slot, slot 0
+// first (ids lane + 64 * slot), lowest lane first. The winner is wave-uniform.
 __device__ __forceinline__ int select_next(const float* val, const bool* eligible, int per_lane,
                                            uint32_t& taken) {
   const int lane = lane_id();
-  float best = 0.0f;
-  int best_idx = -1;
+  float best = -INFINITY;
+  int slot = -1;
   SLOTS(i) {
     if (!eligible[i] || ((taken >> i) & 1u)) continue;
-    if (best_idx < 0 || val[i] > best) {  // ascending e: strict > keeps the lower id
+    if (slot < 0 || val[i] > best) {  // ascending slot: strict > keeps the lower id
       best = val[i];
-      best_idx = lane + 64 * i;
+      slot = i;
     }
   }
-  int winner = wave_argmax(best, best_idx);
+  const float top = wave_max_dpp(slot >= 0 ? best : -INFINITY);
+  int winner = -1;
+  for (int s = 0; s < per_lane && winner < 0; ++s) {
+    const uint64_t hit = __ballot(slot == s && best == top);
+    if (hit != 0) winner = 64 * s + __builtin_ctzll(hit);
+  }
+  // No lane matched (only NaN values left): the lowest remaining id.
+  for (int s = 0; s < per_lane && winner < 0; ++s) {
+    const uint64_t any = __ballot(slot == s);
+    if (any != 0) winner = 64 * s + __builtin_ctzll(any);
+  }
   if (winner >= 0 && (winner & 63) == lane) taken |= 1u << (winner >> 6);
   return winner;
 }
 
+template <int PL>
 __global__ void __launch_bounds__(256) router_topk_kernel(
     const float* __restrict__ logits, int tokens, int experts, int top_k, int mode,
     const float* __restrict__ bias, int n_group, int topk_group, float routed_scaling,
@@ -58,7 +89,7 @@ __global__ void __launch_bounds__(256) router_topk_kernel(
   const int lane = lane_id();
   const int token = blockIdx.x * kTokensPerBlock + wave;
   if (token >= tokens) return;
-  const int per_lane = (experts + 63) / 64;
+  constexpr int per_lane = PL;  // slots per lane (experts <= 64 * PL)
   const float* row = logits + (size_t)token * experts;
 
   float l[kMaxPerLane], val[kMaxPerLane];
@@ -142,7 +173,7 @@ __global__ void __launch_bounds__(256) router_topk_kernel(
   for (int j = 0; j < top_k; ++j) {
     int e = forced != nullptr ? forced[(size_t)token * top_k + j]
                               : select_next(val, ok, per_lane, taken);
-    int owner = e & 63, slot = e >> 6;
+    const int owner = __builtin_amdgcn_readfirstlane(e & 63), slot = e >> 6;
     float lv = 0.0f, pv = 0.0f;
     SLOTS(i) {
       if (i == slot) {
@@ -150,8 +181,8 @@ __global__ void __launch_bounds__(256) router_topk_kernel(
         pv = p[i];
       }
     }
-    lv = __shfl(lv, owner, 64);
-    pv = __shfl(pv, owner, 64);
+    lv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv), owner));
+    pv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), owner));
     if (lane == j) {
       mine = (mode == MI355X_ROUTE_TOPK_THEN_SOFTMAX) ? lv : pv;
       my_id = e;
@@ -179,6 +210,7 @@ __global__ void __launch_bounds__(256) router_topk_kernel(
 // Per-chunk partial column sums of the routing probabilities and per-chunk
 // expert counts. Wave w sums tokens start+w, start+w+4, ...; the four wave
 // partials are then added in wave order, so the result is deterministic.
+template <int PL>
 __global__ void __launch_bounds__(256) router_stats_partial_kernel(
     const float* __restrict__ logits, const int32_t* __restrict__ ids, int tokens, int experts,
     int top_k, int mode, const int32_t* __restrict__ seg_offsets,
@@ -199,7 +231,7 @@ __global__ void __launch_bounds__(256) router_stats_partial_kernel(
   for (int e = threadIdx.x; e < experts; e += blockDim.x) counts[e] = 0;
   __syncthreads();
   const int wave = threadIdx.x >> 6, lane = lane_id();
-  const int per_lane = (experts + 63) / 64;
+  constexpr int per_lane = PL;  // slots per lane (experts <= 64 * PL)
   float acc[kMaxPerLane];
   _Pragma("unroll") for (int i = 0; i < kMaxPerLane; ++i) acc[i] = 0.0f;
   // The wave's tokens t = start + wave + 4u, four at a time: the four rows'
@@ -399,6 +431,7 @@ __global__ void __launch_bounds__(kReduceThreads) router_stats_reduce_kernel(
   }
 }
 
+template <int PL>
 __global__ void __launch_bounds__(256) router_bwd_kernel(
     const float* __restrict__ logits, const float* __restrict__ weights,
     const int32_t* __restrict__ ids, const float* __restrict__ dscore,
@@ -409,7 +442,7 @@ __global__ void __launch_bounds__(256) router_bwd_kernel(
   const int wave = threadIdx.x >> 6, lane = lane_id();
   const int token = blockIdx.x * kTokensPerBlock + wave;
   if (token >= tokens) return;
-  const int per_lane = (experts + 63) / 64;
+  constexpr int per_lane = PL;  // slots per lane (experts <= 64 * PL)
   const float* row = logits + (size_t)token * experts;
   float l[kMaxPerLane], g[kMaxPerLane];
   _Pragma("unroll") for (int i = 0; i < kMaxPerLane; ++i) {
@@ -561,6 +594,13 @@ __global__ void __launch_bounds__(256) router_bwd_kernel(
   }
 }
 
+// Expert slots per lane the kernels are compiled for: the smallest of 1, 2,
+// 4 and 8 that covers ceil(experts / 64) (slots past `experts` are masked).
+int slots_per_lane(int experts) {
+  const int need = (experts + 63) / 64;
+  return need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+}
+
 }  // namespace
 
 extern "C" int mi355x_router_topk(const float* logits, int tokens, int experts, int top_k,
@@ -579,9 +619,17 @@ extern "C" int mi355x_router_topk(const float* logits, int tokens, int experts, 
   }
   if (tokens == 0) return MI355X_OK;
   dim3 grid((tokens + kTokensPerBlock - 1) / kTokensPerBlock);
-  hipLaunchKernelGGL(router_topk_kernel, grid, dim3(256), 0, (hipStream_t)stream, logits, tokens,
-                     experts, top_k, mode, bias, n_group, topk_group, routed_scaling, forced_ids,
-                     weights, ids);
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, (hipStream_t)stream, logits, tokens, experts,
+                       top_k, mode, bias, n_group, topk_group, routed_scaling, forced_ids,
+                       weights, ids);
+  };
+  switch (slots_per_lane(experts)) {
+    case 1: launch(router_topk_kernel<1>); break;
+    case 2: launch(router_topk_kernel<2>); break;
+    case 4: launch(router_topk_kernel<4>); break;
+    default: launch(router_topk_kernel<8>); break;
+  }
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
 }
@@ -612,8 +660,16 @@ extern "C" int mi355x_router_stats(const float* logits, const int32_t* ids, int 
   float* part_p = (float*)workspace;
   int32_t* part_c = (int32_t*)(part_p + (size_t)nchunks * experts);
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(router_stats_partial_kernel, dim3(nchunks), dim3(256), 0, s, logits, ids,
-                     tokens, experts, top_k, mode, seg_offsets, chunk_table, part_p, part_c);
+  auto partial = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(nchunks), dim3(256), 0, s, logits, ids, tokens, experts, top_k,
+                       mode, seg_offsets, chunk_table, part_p, part_c);
+  };
+  switch (slots_per_lane(experts)) {
+    case 1: partial(router_stats_partial_kernel<1>); break;
+    case 2: partial(router_stats_partial_kernel<2>); break;
+    case 4: partial(router_stats_partial_kernel<4>); break;
+    default: partial(router_stats_partial_kernel<8>); break;
+  }
   MI355X_LAUNCH_CHECK();
   if (segments <= kReduceMaxSegments && (size_t)segments * experts <= kReduceMaxPairs) {
     hipLaunchKernelGGL(router_stats_reduce_kernel, dim3(1), dim3(kReduceThreads), 0, s, part_p,
@@ -646,9 +702,17 @@ extern "C" int mi355x_router_topk_bwd(const float* logits, const float* weights,
     MI355X_REQUIRE(offsets != nullptr, "router_bwd: aux gradient needs expert offsets");
   if (tokens == 0) return MI355X_OK;
   dim3 grid((tokens + kTokensPerBlock - 1) / kTokensPerBlock);
-  hipLaunchKernelGGL(router_bwd_kernel, grid, dim3(256), 0, (hipStream_t)stream, logits, weights,
-                     ids, dscore, slots, tokens, experts, top_k, mode, grad_aux, grad_prob_sum,
-                     offsets, segments, seg_offsets, seg_counts, grad_logits);
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, (hipStream_t)stream, logits, weights, ids,
+                       dscore, slots, tokens, experts, top_k, mode, grad_aux, grad_prob_sum,
+                       offsets, segments, seg_offsets, seg_counts, grad_logits);
+  };
+  switch (slots_per_lane(experts)) {
+    case 1: launch(router_bwd_kernel<1>); break;
+    case 2: launch(router_bwd_kernel<2>); break;
+    case 4: launch(router_bwd_kernel<4>); break;
+    default: launch(router_bwd_kernel<8>); break;
+  }
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
 }
