@@ -366,6 +366,19 @@ size_t mi355x_rank_grad_workspace_size(int rows, int experts, int m, int rank, i
 int mi355x_rank_grad(const void* big, int rows, int m, const void* small, int rank,
                      const int32_t* offsets, int experts, int chunk, int transposed, float* out,
                      void* workspace, size_t workspace_bytes, void* stream);
+/* mi355x_rank_grad with token rows: row j of big is big[gather[j] / gather_div]
+ * (big bf16 [big_rows, M], the routed row's token when gather is the routed
+ * order and gather_div = k), and, when weight is given, row j of small is
+ * bf16(small[j] * (weight[gather[j]] * alpha)). The token-side factor
+ * gradients dB2 = s * sum (score dy) z2^T and dA13 = sum u13 x^T as
+ * reductions over each expert's routed rows (src/mlops/lora/experts.py:
+ * 53-167; providers/sonicmoe/lora.py:1062). Workspace as for
+ * mi355x_rank_grad with `rows` routed rows. */
+int mi355x_rank_grad_gather(const void* big, int big_rows, int m, const void* small, int rows,
+                            int rank, const int32_t* offsets, int experts, int chunk,
+                            const int32_t* gather, int gather_div, const float* weight,
+                            float alpha, int transposed, float* out, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 /* The up projection with SwiGLU fused: mi355x_gemm_fp8_block in gate/up mode
  * (w13 [E, 2I, K], interleave = 1) writing h [rows, 2I] bf16 interleaved, and

@@ -15,6 +15,12 @@
 // wave, and walks the chunk 64 rows at a time through LDS. Partial sums of
 // each chunk go to a workspace; a second kernel adds an expert's chunks in
 // chunk order. Both orders are fixed, so the result is bitwise repeatable.
+//
+// Gathered form: row j of `big` may be a token row, big[gather[j] / div]
+// (the routed row's token), and row j of `small` may be scaled by
+// weight[gather[j]] * alpha (rounded to bf16 once, as bf16(z * (w * alpha))):
+// the token-side factor gradients of expert LoRA as reductions over each
+// expert's routed rows, with no [tokens, E * R] scatter.
 #include "common.h"
 
 namespace {
@@ -68,7 +74,8 @@ __device__ __forceinline__ bf16x8_t gather8(const uint8_t* base, int pitch) {
 
 __global__ void __launch_bounds__(kThreads) rank_grad_partial_kernel(
     const uint16_t* __restrict__ big, int M, const uint16_t* __restrict__ small, int R,
-    const int32_t* __restrict__ offsets, int experts, int chunk, float* __restrict__ partial) {
+    const int32_t* __restrict__ offsets, int experts, int chunk, const int32_t* __restrict__ gather,
+    int gather_div, const float* __restrict__ weight, float alpha, float* __restrict__ partial) {
   __shared__ int prefix[kMaxExperts + 1];
   __shared__ __align__(16) uint8_t big_s[kStRows * kBigPitch];
   __shared__ __align__(16) uint8_t small_s[kStRows * kSmallPitch];
@@ -89,18 +96,34 @@ __global__ void __launch_bounds__(kThreads) rank_grad_partial_kernel(
   for (int i = 0; i < 4; ++i) acc[i] = (v4f){0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int s0 = row0; s0 < row1; s0 += kStRows) {
-    // Loads first (rows past the chunk read as zeros), then the LDS stores.
+    // Loads first (rows past the chunk read as zeros), then the LDS stores;
+    // the gather indices before the rows they select.
+    int brow[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = min(s0 + i * 8 + (tid >> 5), row1 - 1);
+      brow[i] = gather != nullptr ? gather[r] / gather_div : r;
+    }
     uint4 v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = s0 + i * 8 + (tid >> 5);
-      v[i] = (r < row1 && col_ok) ? load_stream(big + (size_t)r * M + m0 + lcol)
+      v[i] = (r < row1 && col_ok) ? load_stream(big + (size_t)brow[i] * M + m0 + lcol)
                                   : make_uint4(0, 0, 0, 0);
     }
     uint4 sv = make_uint4(0, 0, 0, 0);
     if (tid < 2 * kStRows) {
       const int r = s0 + (tid >> 1);
-      if (r < row1) sv = *(const uint4*)(small + (size_t)r * R + n0 + (tid & 1) * 8);
+      if (r < row1) {
+        sv = *(const uint4*)(small + (size_t)r * R + n0 + (tid & 1) * 8);
+        if (weight != nullptr) {
+          const float f = weight[gather != nullptr ? gather[r] : r] * alpha;
+          float z[8];
+          unpack_bf16x8(sv, z);
+          sv = make_uint4(pack_bf16x2(z[0] * f, z[1] * f), pack_bf16x2(z[2] * f, z[3] * f),
+                          pack_bf16x2(z[4] * f, z[5] * f), pack_bf16x2(z[6] * f, z[7] * f));
+        }
+      }
     }
     __syncthreads();  // the previous stage's fragments are read
 #pragma unroll
@@ -180,10 +203,11 @@ extern "C" size_t mi355x_rank_grad_workspace_size(int rows, int experts, int m, 
   return max_chunks(rows, experts, chunk) * (size_t)m * (size_t)rank * sizeof(float);
 }
 
-extern "C" int mi355x_rank_grad(const void* big, int rows, int m, const void* small, int rank,
-                                const int32_t* offsets, int experts, int chunk, int transposed,
-                                float* out, void* workspace, size_t workspace_bytes,
-                                void* stream) {
+namespace {
+int rank_grad_launch(const void* big, int rows, int m, const void* small, int rank,
+                     const int32_t* offsets, int experts, int chunk, const int32_t* gather,
+                     int gather_div, const float* weight, float alpha, int transposed, float* out,
+                     void* workspace, size_t workspace_bytes, void* stream) {
   MI355X_REQUIRE(m > 0 && m % 8 == 0, "rank_grad: the wide dimension must be a multiple of 8");
   MI355X_REQUIRE(rank > 0 && rank % 16 == 0 && rank <= 64,
                  "rank_grad: the rank must be a multiple of 16 up to 64 (pad with zeros)");
@@ -202,7 +226,7 @@ extern "C" int mi355x_rank_grad(const void* big, int rows, int m, const void* sm
     const dim3 grid((m + kBlockColsMfma - 1) / kBlockColsMfma, (unsigned)chunks, rank / kRanks);
     hipLaunchKernelGGL(rank_grad_partial_kernel, grid, dim3(kThreads), 0, s,
                        (const uint16_t*)big, m, (const uint16_t*)small, rank, offsets, experts,
-                       chunk, partial);
+                       chunk, gather, gather_div, weight, alpha, partial);
     MI355X_LAUNCH_CHECK();
   }
   const size_t per = (size_t)m * rank;
@@ -211,4 +235,26 @@ extern "C" int mi355x_rank_grad(const void* big, int rows, int m, const void* sm
                      offsets, experts, chunk, transposed, out);
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
+}
+}  // namespace
+
+extern "C" int mi355x_rank_grad(const void* big, int rows, int m, const void* small, int rank,
+                                const int32_t* offsets, int experts, int chunk, int transposed,
+                                float* out, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+  return rank_grad_launch(big, rows, m, small, rank, offsets, experts, chunk, nullptr, 1, nullptr,
+                          1.0f, transposed, out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mi355x_rank_grad_gather(const void* big, int big_rows, int m, const void* small,
+                                       int rows, int rank, const int32_t* offsets, int experts,
+                                       int chunk, const int32_t* gather, int gather_div,
+                                       const float* weight, float alpha, int transposed,
+                                       float* out, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
+  MI355X_REQUIRE(gather != nullptr && gather_div >= 1,
+                 "rank_grad_gather: a gather index and a divisor >= 1 are required");
+  MI355X_REQUIRE(big_rows >= 0, "rank_grad_gather: negative token count");
+  return rank_grad_launch(big, rows, m, small, rank, offsets, experts, chunk, gather, gather_div,
+                          weight, alpha, transposed, out, workspace, workspace_bytes, stream);
 }

@@ -542,18 +542,33 @@ def rank_product(a, bt, offsets):
     return out
 
 
-def rank_grad(big, small, offsets, *, transposed=False, chunk=None):
+def rank_grad(big, small, offsets, *, transposed=False, chunk=None, gather=None, gather_div=1,
+              weight=None, alpha=1.0):
     """Per expert ``sum_j big[j]^T small[j]`` over its rows: fp32 ``[E, M, R]``
     (``[E, R, M]`` when ``transposed``) from bf16 ``big [rows, M]`` and ``small
-    [rows, R]`` (``mi355x_rank_grad``; R a multiple of 16, at most 64)."""
-    rows, m = big.shape
-    rank = small.shape[1]
+    [rows, R]`` (``mi355x_rank_grad``; R a multiple of 16, at most 64).
+
+    With ``gather`` (int32 ``[rows]``), row j of ``big [tokens, M]`` is
+    ``big[gather[j] // gather_div]``, and with ``weight`` (fp32, indexed by
+    ``gather[j]``) row j of ``small`` is ``bf16(small[j] * (weight[gather[j]]
+    * alpha))`` (``mi355x_rank_grad_gather``)."""
+    big_rows, m = big.shape
+    rows, rank = small.shape
     experts = offsets.numel() - 1
     if big.dtype != torch.bfloat16 or small.dtype != torch.bfloat16:
         raise ValueError("rank_grad takes bf16 operands")
-    _check(small, (rows, rank), torch.bfloat16, "rank operand")
+    if gather is None:
+        if weight is not None:
+            raise ValueError("rank_grad: a row weight needs the gather index")
+        _check(small, (big_rows, rank), torch.bfloat16, "rank operand")
+    else:
+        _check(gather, (rows,), torch.int32, "gather index")
+        if weight is not None and (weight.dtype != torch.float32 or not weight.is_contiguous()):
+            raise ValueError("rank_grad: the row weight must be contiguous fp32")
+        if not big.is_contiguous() or not small.is_contiguous():
+            raise ValueError("rank_grad: operands must be contiguous")
     _check(offsets, (experts + 1,), torch.int32, "offsets")
-    device = _on_gpu(big, small, offsets)
+    device = _on_gpu(big, small, offsets, *(t for t in (gather, weight) if t is not None))
     if chunk is None:
         # Enough (chunk x 256-column) blocks to fill the chip twice over.
         blocks_per_chunk = -(-m // 256) * (rank // 16)
@@ -565,9 +580,16 @@ def rank_grad(big, small, offsets, *, transposed=False, chunk=None):
     size = _native.query("mi355x_rank_grad_workspace_size", rows, experts, m, rank, chunk)
     workspace = torch.empty(size, dtype=torch.uint8, device=device)
     # HBM-bound: big is streamed once; the products are on the bf16 MFMA
-    _timed("rank_grad", device, 0, 2 * rows * (m + rank) + 4 * experts * m * rank,
-           "mi355x_rank_grad", _ptr(big), rows, m, _ptr(small), rank, _ptr(offsets), experts,
-           chunk, int(transposed), _ptr(out), _ptr(workspace), size, _stream(device))
+    nbytes = 2 * rows * (m + rank) + 4 * experts * m * rank
+    if gather is None:
+        _timed("rank_grad", device, 0, nbytes, "mi355x_rank_grad", _ptr(big), rows, m,
+               _ptr(small), rank, _ptr(offsets), experts, chunk, int(transposed), _ptr(out),
+               _ptr(workspace), size, _stream(device))
+    else:
+        _timed("rank_grad", device, 0, nbytes + 4 * rows, "mi355x_rank_grad_gather", _ptr(big),
+               big_rows, m, _ptr(small), rows, rank, _ptr(offsets), experts, chunk,
+               _ptr(gather), int(gather_div), _ptr(weight), float(alpha), int(transposed),
+               _ptr(out), _ptr(workspace), size, _stream(device))
     return out
 
 

@@ -22,11 +22,13 @@ folded into the small ``B`` factors; ranks are padded with zero columns to a
 multiple of 16.
 
 Rank projections of token rows (``x @ A13^T`` forward, ``dy @ B2`` backward)
-are formed once per token for all experts, as one dense ``[T, E*r]`` GEMM,
-and gathered to the routed rows; the rest are per-expert GEMMs over each
-expert's rows. These rank-r products and the factor gradients are plain
-library GEMMs (hipBLASLt through torch), bf16 operands with fp32 sums; the
-factor gradients come back at the factors' dtype (fp32 sums throughout).
+are formed once per token for all experts, as one dense ``[T, E*r]`` GEMM
+(hipBLASLt through torch), and gathered to the routed rows; those of routed
+rows (``a @ A2^T``, ``dh @ B13``) run on ``mi355x_rank_product``. The four
+factor gradients are reductions over each expert's routed rows on
+``mi355x_rank_grad`` (token rows gathered for ``dB2`` and ``dA13``), bf16
+operands with fp32 sums, with no host synchronization; they come back at the
+factors' dtype.
 """
 
 from __future__ import annotations
@@ -62,6 +64,20 @@ def _padded(t: torch.Tensor, rank: int) -> torch.Tensor:
     return torch.nn.functional.pad(t, (0, extra)).contiguous() if extra else t.contiguous()
 
 
+def _padded_rank_rows(t: torch.Tensor, rank: int) -> torch.Tensor:
+    """``t [E, r, n]`` with zero rows up to ``rank``, contiguous."""
+    extra = rank - t.shape[1]
+    return torch.nn.functional.pad(t, (0, 0, 0, extra)).contiguous() if extra else t.contiguous()
+
+
+def _scaled_bf16(t: torch.Tensor, scale: float) -> torch.Tensor:
+    """``bf16(t * scale)`` with one rounding of the fp32 product (a bf16 ``t``
+    is multiplied in fp32 by torch and rounded once, in one kernel)."""
+    if t.dtype == torch.bfloat16:
+        return torch.mul(t, scale)
+    return (t.float() * scale).to(torch.bfloat16)
+
+
 def _rank16(r: int) -> int:
     return -(-r // 16) * 16
 
@@ -77,13 +93,15 @@ def _row_rank(rows: torch.Tensor, factors_t: torch.Tensor, offsets) -> torch.Ten
 
 
 def _factor_grad(big: torch.Tensor, small: torch.Tensor, offsets, rank: int, *,
-                 transposed: bool) -> torch.Tensor:
+                 transposed: bool, **gather) -> torch.Tensor:
     """Per expert ``sum_j big[j]^T small[j]`` over its rows, fp32, cut to the
     true ``rank``: ``[E, M, rank]``, or ``[E, rank, M]`` when ``transposed``.
-    bf16 operands with fp32 sums (``mi355x_rank_grad``, no host sync)."""
+    bf16 operands with fp32 sums (``mi355x_rank_grad``, no host sync).
+    ``gather`` options (token rows of ``big``, a per-row weight on ``small``)
+    pass through to :func:`kernels.rank_grad`."""
     padded = _padded(small, _rank16(rank))
     parts = [kernels.rank_grad(big, padded[:, c:c + 64].contiguous(), offsets,
-                               transposed=transposed)
+                               transposed=transposed, **gather)
              for c in range(0, padded.shape[1], 64)]
     out = parts[0] if len(parts) == 1 else torch.cat(parts, dim=1 if transposed else 2)
     return (out[:, :rank] if transposed else out[..., :rank]).contiguous()
@@ -97,15 +115,6 @@ def _token_projection(x_tok: torch.Tensor, factors_flat: torch.Tensor, experts: 
     projected = x_tok @ factors_flat
     rank = factors_flat.shape[1] // experts
     return projected.view(x_tok.shape[0], experts, rank)[tokens_of_row, experts_of_row]
-
-
-def _scatter_tokens(rows: torch.Tensor, tokens: int, experts: int,
-                    tokens_of_row: torch.Tensor, experts_of_row: torch.Tensor) -> torch.Tensor:
-    """``Z[t, e*r:(e+1)*r] = rows[j]`` for the row j of pair (t, e) (fp32,
-    zeros elsewhere): the token-side form of a per-row factor gradient."""
-    out = torch.zeros((tokens, experts, rows.shape[1]), dtype=torch.float32, device=rows.device)
-    out[tokens_of_row, experts_of_row] = rows.float()
-    return out.view(tokens, experts * rows.shape[1])
 
 
 class _ExpertLoRA(torch.autograd.Function):
@@ -141,10 +150,10 @@ class _ExpertLoRA(torch.autograd.Function):
             rows_expert = ids.reshape(-1).long()[order_l]
             # Factors at the activations' dtype, the scale folded into B.
             a13b = a13.detach().to(torch.bfloat16)
-            b13s = (b13.detach().float() * scale).to(torch.bfloat16)
+            b13s = _scaled_bf16(b13.detach(), scale)
             b13b = interleaved_rows(b13s)
             a2b = a2.detach().to(torch.bfloat16)
-            b2b = (b2.detach().float() * scale).to(torch.bfloat16)
+            b2b = _scaled_bf16(b2.detach(), scale)
             rank13, rank2 = a13b.shape[1], a2b.shape[1]
             r13, r2 = _rank16(rank13), _rank16(rank2)
             # Up projection: z13 = x @ A13^T per routed row; z13 (s B13)^T
@@ -165,10 +174,8 @@ class _ExpertLoRA(torch.autograd.Function):
                 aq, as_, act = kernels.swiglu_quantize(h13, limit, activation=True)
             # Down projection: z2 = a @ A2^T per routed row (the thin product
             # streams a once; rank padded to 16).
-            z2p = _row_rank(act, _padded(a2b.transpose(1, 2), r2).transpose(1, 2).contiguous(),
-                            offsets)
+            z2p = _row_rank(act, _padded_rank_rows(a2b, r2), offsets)
             del act
-            z2 = z2p[:, :rank2]
             if current:
                 y = kernels.gemm_rowwise(aq, as_, w2_data, w2_scale, offsets,
                                          lora=(z2p, _padded(b2b, r2)))
@@ -182,13 +189,13 @@ class _ExpertLoRA(torch.autograd.Function):
         ctx.w13, ctx.w2 = w13, w2
         ctx.factor_dtypes = (a13.dtype, b13.dtype, a2.dtype, b2.dtype)
         ctx.save_for_backward(hidden, router_weight, logits, weights, ids, order, offsets, slots,
-                              h13, z13, z2, rows_token, rows_expert, a13b, b13b, a2b, b2b)
+                              h13, z13, z2p, rows_token, rows_expert, a13b, b13b, a2b, b2b)
         ctx.mark_non_differentiable(counts)
         return output.reshape(hidden.shape), aux, counts, probability_sum
 
     @staticmethod
     def backward(ctx, grad_output, grad_aux, _grad_counts, grad_probability_sum):
-        (hidden, router_weight, logits, weights, ids, order, offsets, slots, h13, z13, z2,
+        (hidden, router_weight, logits, weights, ids, order, offsets, slots, h13, z13, z2p,
          rows_token, rows_expert, a13b, b13b, a2b, b2b) = ctx.saved_tensors
         opts = ctx.opts
         top_k, mode, scale, limit = opts["top_k"], opts["routing_mode"], opts["scale"], opts["limit"]
@@ -238,7 +245,6 @@ class _ExpertLoRA(torch.autograd.Function):
             # Input gradient: dx_j = dh_j @ W13[e] + (dh_j @ (s B13[e])) @ A13[e].
             r13 = _rank16(rank13)
             u13p = _row_rank(dh, _padded(b13b, r13).transpose(1, 2).contiguous(), offsets)
-            u13 = u13p[:, :rank13]
             lora_x = (u13p, _padded(a13b.transpose(1, 2), r13))
             if current:
                 # dh's interleaved columns are the K order of w13's transpose.
@@ -253,23 +259,18 @@ class _ExpertLoRA(torch.autograd.Function):
             del dx
             # Factor gradients (fp32 sums), scale applied once.
             grads = [None, None, None, None]
-            if need[8]:    # B2: s * sum_j (score_j dy_j) z2_j^T, on the token side
-                score = weights.reshape(-1)[order.long()]
-                zs = _scatter_tokens(z2.float() * (score[:, None] * scale), tokens, experts,
-                                     rows_token, rows_expert)
-                # dy^T zs as (zs^T dy)^T: the token-reduction product of the
-                # router weight gradient, bf16 operands with fp32 sums.
-                g = router.split_k_product(zs.to(torch.bfloat16), dy).t()
-                grads[3] = g.reshape(width, experts, rank2).permute(1, 0, 2).contiguous()
+            # Token rows of the routed rows: big[order[j] // k] in the reductions.
+            token_rows = dict(gather=order, gather_div=top_k)
+            if need[8]:    # B2: s * sum_j dy_{t(j)} (score_j z2_j)^T
+                grads[3] = _factor_grad(dy, z2p, offsets, rank2, transposed=False,
+                                        weight=weights.reshape(-1), alpha=scale, **token_rows)
             if need[7]:    # A2: sum_j u2_j a'_j^T, a' = score * a
                 grads[2] = _factor_grad(a_prime, u2, offsets, rank2, transposed=True)
             if need[6]:    # B13: s * sum_j dh_j z13_j^T (rows back to gate then up)
                 g = _factor_grad(dh, z13, offsets, rank13, transposed=False)
                 grads[1] = gate_up_rows(g.mul_(scale))
-            if need[5]:    # A13: sum_j u13_j x_j^T, formed on the token side
-                zd = _scatter_tokens(u13, tokens, experts, rows_token, rows_expert)
-                grads[0] = router.split_k_product(zd.to(torch.bfloat16), x
-                                                  ).view(experts, rank13, width)
+            if need[5]:    # A13: sum_j u13_j x_{t(j)}^T
+                grads[0] = _factor_grad(x, u13p, offsets, rank13, transposed=True, **token_rows)
             grads = [None if g is None else g.to(dtype)
                      for g, dtype in zip(grads, ctx.factor_dtypes)]
             # Base weight gradients, when the base is trained.

@@ -592,3 +592,39 @@ def test_rank_grad_matches_fp64(device, counts, m, rank, transposed, chunk):
     again = K.rank_grad(big.to(device), small.to(device), offsets.to(device),
                         transposed=transposed, chunk=chunk).cpu()
     assert torch.equal(out, again)  # fixed summation order
+
+
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_rank_grad_gathered_token_rows(device, weighted, transposed):
+    """The token-side form: row j of big is the token row big[order[j] // k],
+    and small's row j is scaled by weight[order[j]] * alpha (rounded to bf16
+    once), against an fp64 product of the same operands. An empty expert and
+    ragged counts come from the routing."""
+    g = torch.Generator().manual_seed(7 + 2 * weighted + transposed)
+    tokens, top_k, experts, m, rank = 300, 2, 6, 264, 16
+    ids = torch.stack([torch.randperm(experts, generator=g)[:top_k] for _ in range(tokens)]).int()
+    ids[ids == 2] = 3  # expert 2 gets no rows
+    order, offsets, _ = O.sort_assignments(ids, experts)
+    rows = tokens * top_k
+    big = torch.randn(tokens, m, generator=g).to(torch.bfloat16)
+    small = (torch.randn(rows, rank, generator=g) * 0.3).to(torch.bfloat16)
+    weight = torch.rand(rows, generator=g) if weighted else None
+    alpha = 1.5 if weighted else 1.0
+    out = K.rank_grad(big.to(device), small.to(device), offsets.to(device),
+                      transposed=transposed, gather=order.to(device), gather_div=top_k,
+                      weight=None if weight is None else weight.to(device), alpha=alpha).cpu()
+    tok = order.long() // top_k
+    scaled = small
+    if weighted:
+        scaled = (small.float() * (weight[order.long()] * alpha)[:, None]).to(torch.bfloat16)
+    for e in range(experts):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        want = big[tok[lo:hi]].double().t() @ scaled[lo:hi].double()
+        if transposed:
+            want = want.t()
+        got = out[e].double()
+        if hi == lo:
+            assert torch.all(got == 0)
+            continue
+        assert (got - want).abs().max() <= 1e-5 * want.abs().max() + 1e-6, e
