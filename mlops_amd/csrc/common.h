@@ -227,17 +227,44 @@ __device__ inline void padded_block_prefix(const int32_t* __restrict__ offsets, 
   __syncthreads();
 }
 
-// Max over aligned groups of `width` lanes (width a power of two <= 64).
+// Reductions over aligned groups of W lanes (W a power of two <= 64), the
+// result in every lane of the group. Within a DPP row (16 lanes) they are
+// DPP moves: quad swaps [1,0,3,2] and [2,3,0,1], then the half-row mirror
+// (lane i <-> 7 - i) and the row mirror (i <-> 15 - i), each pairing two
+// partial results that cover disjoint lanes; every lane adds the same two
+// values, so all lanes of the group hold the same sum. Wider groups finish
+// with lane shuffles. A source lane that is not active returns the `old`
+// operand: the lane's own value for max, 0 for sums.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_max_step(float v) {
+  const int b = __float_as_int(v);
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(b, b, kCtrl, 0xF, 0xF, false)));
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp_sum_step(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF,
+                                                        false));
+}
 template <int W>
 __device__ __forceinline__ float group_max(float v) {
+  static_assert(W >= 2 && W <= 64 && (W & (W - 1)) == 0, "group width");
+  v = dpp_max_step<0xB1>(v);
+  if constexpr (W >= 4) v = dpp_max_step<0x4E>(v);
+  if constexpr (W >= 8) v = dpp_max_step<0x141>(v);
+  if constexpr (W >= 16) v = dpp_max_step<0x140>(v);
 #pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  for (int o = 16; o < W; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
+  static_assert(W >= 2 && W <= 64 && (W & (W - 1)) == 0, "group width");
+  v = dpp_sum_step<0xB1>(v);
+  if constexpr (W >= 4) v = dpp_sum_step<0x4E>(v);
+  if constexpr (W >= 8) v = dpp_sum_step<0x141>(v);
+  if constexpr (W >= 16) v = dpp_sum_step<0x140>(v);
 #pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  for (int o = 16; o < W; o <<= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
 
