@@ -26,52 +26,75 @@ __global__ void __launch_bounds__(kPlanThreads) plan_hist_kernel(
 }
 
 // Pass 2 (one block): expert totals, their exclusive scan (offsets), and each
-// chunk's starting position per expert (written over the histogram).
+// chunk's starting position per expert (written over the histogram). Each
+// expert's chunks are split over G threads (G * experts <= the block), thread
+// (part, e) taking a contiguous range of chunks; its counts are loaded in
+// batches of sixteen before any is used, the parts' totals meet in LDS, and a
+// second pass rewrites the range with the running positions.
 __global__ void __launch_bounds__(kMaxExperts) plan_scan_kernel(
     int32_t* __restrict__ hist, int chunks, int experts, int n, int64_t* __restrict__ counts,
     int32_t* __restrict__ offsets) {
   __shared__ int scan[kMaxExperts];
-  const int e = threadIdx.x;
-  // Sixteen chunks' counts are loaded before any of them is rewritten, so a
-  // pass costs chunks / 16 memory round trips rather than one per chunk.
+  __shared__ int part_total[kMaxExperts];  // [part][expert]
   constexpr int kBatch = 16;
-  int total = 0;
-  if (e < experts) {
-    for (int c0 = 0; c0 < chunks; c0 += kBatch) {
+  const int tid = threadIdx.x;
+  int parts = 1;
+  while (parts * 2 * experts <= kMaxExperts) parts *= 2;
+  const int e = tid % experts, part = tid / experts;
+  const bool active = part < parts;
+  const int per = (chunks + parts - 1) / parts;
+  const int c_begin = min(chunks, part * per), c_end = min(chunks, c_begin + per);
+  int local = 0;
+  if (active) {
+    for (int c0 = c_begin; c0 < c_end; c0 += kBatch) {
       int v[kBatch];
 #pragma unroll
       for (int j = 0; j < kBatch; ++j)
-        v[j] = c0 + j < chunks ? hist[(size_t)(c0 + j) * experts + e] : 0;
+        v[j] = c0 + j < c_end ? hist[(size_t)(c0 + j) * experts + e] : 0;
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) local += v[j];
+    }
+    part_total[part * experts + e] = local;
+  }
+  __syncthreads();
+  // Expert totals and the parts' exclusive prefixes.
+  int total = 0, before = 0;
+  if (active) {
+    for (int p = 0; p < parts; ++p) {
+      const int t = part_total[p * experts + e];
+      if (p < part) before += t;
+      total += t;
+    }
+  }
+  scan[tid] = (active && part == 0) ? total : 0;
+  __syncthreads();
+  for (int o = 1; o < kMaxExperts; o <<= 1) {
+    int v = tid >= o ? scan[tid - o] : 0;
+    __syncthreads();
+    scan[tid] += v;
+    __syncthreads();
+  }
+  // scan[e] is now the inclusive prefix of expert totals over experts 0..e
+  if (active) {
+    const int base = scan[e] - total;  // exclusive prefix
+    if (part == 0) {
+      counts[e] = total;
+      offsets[e] = base;
+    }
+    int run = base + before;
+    for (int c0 = c_begin; c0 < c_end; c0 += kBatch) {
+      int v[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        v[j] = c0 + j < c_end ? hist[(size_t)(c0 + j) * experts + e] : 0;
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
-        if (c0 + j < chunks) hist[(size_t)(c0 + j) * experts + e] = total;
-        total += v[j];
+        if (c0 + j < c_end) hist[(size_t)(c0 + j) * experts + e] = run;
+        run += v[j];
       }
     }
   }
-  scan[e] = total;
-  __syncthreads();
-  for (int o = 1; o < kMaxExperts; o <<= 1) {
-    int v = e >= o ? scan[e - o] : 0;
-    __syncthreads();
-    scan[e] += v;
-    __syncthreads();
-  }
-  const int base = scan[e] - total;  // exclusive prefix
-  if (e < experts) {
-    counts[e] = total;
-    offsets[e] = base;
-    for (int c0 = 0; c0 < chunks; c0 += kBatch) {
-      int v[kBatch];
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j)
-        v[j] = c0 + j < chunks ? hist[(size_t)(c0 + j) * experts + e] : 0;
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j)
-        if (c0 + j < chunks) hist[(size_t)(c0 + j) * experts + e] = v[j] + base;
-    }
-  }
-  if (e == 0) offsets[experts] = n;
+  if (tid == 0) offsets[experts] = n;
 }
 
 // Pass 3: stable scatter. A chunk is walked in 256-element tiles in index

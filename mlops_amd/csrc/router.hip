@@ -382,11 +382,23 @@ __global__ void __launch_bounds__(kReduceThreads) router_stats_reduce_kernel(
     int sc = 0;
     if (pair < pairs) {
       const int seg = pair / experts, e = pair % experts;
-      // Unrolled so the loads run ahead of the in-order sums.
-#pragma unroll 8
-      for (int c = seg_start[seg] + part; c < seg_start[seg + 1]; c += G) {
-        sp += part_p[(size_t)c * experts + e];
-        sc += part_c[(size_t)c * experts + e];
+      // Sixteen chunks' partials are loaded before they are summed (in order).
+      constexpr int kBatch = 16;
+      const int c_end = seg_start[seg + 1];
+      for (int c0 = seg_start[seg] + part; c0 < c_end; c0 += kBatch * G) {
+        float pv[kBatch];
+        int cv[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int c = c0 + j * G;
+          pv[j] = c < c_end ? part_p[(size_t)c * experts + e] : 0.0f;
+          cv[j] = c < c_end ? part_c[(size_t)c * experts + e] : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          sp += pv[j];
+          sc += cv[j];
+        }
       }
     }
     for (int o = G >> 1; o >= 1; o >>= 1) {
