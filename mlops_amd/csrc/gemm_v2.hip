@@ -379,7 +379,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
                 pmax = fmaxf(pmax, fabsf(act[ii][r][m]));
               }
               pmax = group_max<16>(pmax);  // the 16 lanes of this row: 64 columns
-              if ((lane & 15) == 0) act_amax[wn][wm * 64 + lrow] = pmax;
+              if ((elane & 15) == 0) act_amax[wn][wm * 64 + lrow] = pmax;
             }
           }
         }
@@ -391,7 +391,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
         for (int ii = 0; ii < 2; ++ii) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int trow = wm * 64 + (half * 2 + ii) * 16 + 4 * (lane >> 4) + r;
+            const int trow = wm * 64 + (half * 2 + ii) * 16 + 4 * (elane >> 4) + r;
             if (trow < ct.nvalid) {
               const float amax = fmaxf(act_amax[0][trow], act_amax[1][trow]);
               const float sc = fmaxf(amax * kInv448, kMinScale);
@@ -399,8 +399,8 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
                   f32x4_to_e4m3(quant_div(act[ii][r][0], sc), quant_div(act[ii][r][1], sc),
                                 quant_div(act[ii][r][2], sc), quant_div(act[ii][r][3], sc));
               const size_t row = (size_t)(ct.row0 + trow);
-              *(uint32_t*)(act_q + row * half_w + ct.nt * 128 + wn * 64 + (lane & 15) * 4) = qv;
-              if (wn == 0 && (lane & 15) == 0) act_scales[(size_t)ct.nt * rows + row] = sc;
+              *(uint32_t*)(act_q + row * half_w + ct.nt * 128 + wn * 64 + (elane & 15) * 4) = qv;
+              if (wn == 0 && (elane & 15) == 0) act_scales[(size_t)ct.nt * rows + row] = sc;
             }
           }
         }
