@@ -33,7 +33,7 @@ def _zipf_ids(tokens, top_k, experts, s, seed):
 
 # ------------------------------------------------------------------ router
 @pytest.mark.parametrize("mode", ["topk_then_softmax", "softmax_then_topk", "sigmoid_noaux_tc"])
-@pytest.mark.parametrize("experts,top_k", [(128, 8), (8, 2), (300, 6)])
+@pytest.mark.parametrize("experts,top_k", [(128, 8), (8, 2), (300, 6), (256, 8), (512, 32), (64, 1)])
 def test_router_topk_matches_oracle(device, mode, experts, top_k):
     g = torch.Generator().manual_seed(experts + top_k)
     logits = torch.randn(1000, experts, generator=g)
@@ -77,6 +77,9 @@ def test_router_forced_ids(device):
     ("sigmoid_noaux_tc", (201, 299), 512, 6),
     ("topk_then_softmax", None, 64, 32),               # top_k near the lane limit
     ("sigmoid_noaux_tc", (13, 487), 64, 32),
+    ("topk_then_softmax", None, 128, 8),               # two expert slots per lane
+    ("softmax_then_topk", (250, 250), 200, 8),         # four slots per lane, masked tail
+    ("sigmoid_noaux_tc", None, 256, 8),
 ])
 def test_router_stats_and_backward(device, mode, lengths, experts, top_k):
     g = torch.Generator().manual_seed(13 + experts + top_k)
