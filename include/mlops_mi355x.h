@@ -352,6 +352,16 @@ size_t mi355x_quantize_weights_current_workspace_size(int experts, int out, int 
  * :49; sonicmoe/lora.py _low :87, _through :98). */
 int mi355x_rank_product(const void* a, int rows, int k, const void* bt, int rank,
                         const int32_t* offsets, int experts, void* out, void* stream);
+/* mi355x_rank_product with its K range split over `splits` blocks per 32-row
+ * block (K a multiple of 128, splits <= K / 128), for few rows: each split
+ * writes fp32 partial sums to the workspace
+ * (mi355x_rank_product_workspace_size(rows, R, splits) bytes) and a second
+ * pass adds them in split order and rounds once to bf16. splits = 1 is
+ * mi355x_rank_product. */
+size_t mi355x_rank_product_workspace_size(int rows, int rank, int splits);
+int mi355x_rank_product_split(const void* a, int rows, int k, const void* bt, int rank,
+                              const int32_t* offsets, int experts, int splits, void* out,
+                              void* workspace, size_t workspace_bytes, void* stream);
 
 /* Expert LoRA factor gradients as grouped reductions over routed rows:
  * out[e][m][n] = sum over expert e's rows j of big[j][m] * small[j][n], fp32

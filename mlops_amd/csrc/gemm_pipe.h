@@ -63,9 +63,9 @@ __device__ __forceinline__ void dma4(const void* base, uint32_t off, const uint8
 // Wait until at most N direct loads of this wave are in flight, then barrier.
 template <int N>
 __device__ __forceinline__ void wait_and_sync() {
-  static_assert(N >= 0 && N < 16, "vmcnt range");
-  // gfx9 s_waitcnt: vmcnt[3:0], expcnt[6:4]=7, lgkmcnt[11:8]=15, vmcnt[5:4]=0
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // gfx9 s_waitcnt: vmcnt[3:0], expcnt[6:4]=7, lgkmcnt[11:8]=15, vmcnt[5:4] in [15:14]
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");

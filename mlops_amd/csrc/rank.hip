@@ -16,7 +16,10 @@
 // multiple of 128 the staged form below is used instead: rows and factor
 // are copied to LDS with direct loads (16 lanes per 256-byte row slice, so
 // whole lines), three stages deep, and each wave reads its MFMA fragments
-// from there.
+// from there. With few row blocks (rows / 32 below ~4 per CU) the K chunks
+// are also split over `splits` blocks per row block, each writing fp32
+// partial sums that a second kernel adds in split order, so that enough
+// blocks stream at once.
 #include "gemm_pipe.h"
 
 namespace {
@@ -119,24 +122,28 @@ __global__ void __launch_bounds__(64 * kRankWaves) rank_product_kernel(
   }
 }
 
-// Staged form: a block of 2 waves takes 32 rows, a wave 16 rows over all of
+// Staged form: a block of 4 waves takes 64 rows, a wave 16 rows over all of
 // K, in chunks of 128 K (256 bytes per row). A chunk's row slices and the
 // factor's R slices go to LDS with direct loads; chunk c of a row r sits at
 // 16-byte position c ^ (r % 16), so the 16 rows of a fragment read fall in
 // distinct banks. R is a template parameter so that each wave's loads per
-// stage, 4 + R / 8, is a compile-time count for the wait.
-constexpr int kStRows = 32;
+// stage, 4 + R / 16, is a compile-time count for the wait.
+constexpr int kStWaves = 4;
+constexpr int kStRows = 16 * kStWaves;
 constexpr int kStSlice = 256;  // bytes of one row per K chunk
 constexpr int kStStages = 3;
 
 template <int R>
-__global__ void __launch_bounds__(128) rank_product_staged_kernel(
+__global__ void __launch_bounds__(64 * kStWaves) rank_product_staged_kernel(
     const uint16_t* __restrict__ a, int rows, int K, const uint16_t* __restrict__ bt,
-    const int32_t* __restrict__ offsets, int experts, uint16_t* __restrict__ out) {
+    const int32_t* __restrict__ offsets, int experts, uint16_t* __restrict__ out,
+    float* __restrict__ partial) {
   constexpr int A_BYTES = kStRows * kStSlice;              // 8 KB
   constexpr int B_BYTES = R * kStSlice;                    // 4-16 KB
   constexpr int STAGE = A_BYTES + B_BYTES;
-  constexpr int A_PER_WAVE = A_BYTES / 1024 / 2, B_PER_WAVE = B_BYTES / 1024 / 2;
+  constexpr int A_PER_WAVE = A_BYTES / 1024 / kStWaves, B_PER_WAVE = B_BYTES / 1024 / kStWaves;
+  static_assert(A_PER_WAVE * kStWaves * 1024 == A_BYTES && B_PER_WAVE * kStWaves * 1024 == B_BYTES,
+                "whole 1 KB copies per wave");
   constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;           // direct loads per wave per stage
   __shared__ __align__(1024) uint8_t smem[kStStages * STAGE];
   const int row0 = blockIdx.x * kStRows;
@@ -144,7 +151,10 @@ __global__ void __launch_bounds__(128) rank_product_staged_kernel(
   const int last = min(row0 + kStRows - 1, rows - 1);
   const int e_lo = __builtin_amdgcn_readfirstlane(expert_of(offsets, experts, row0));
   const int e_hi = __builtin_amdgcn_readfirstlane(expert_of(offsets, experts, last));
-  const int nch = K / 128;
+  // This block's K chunks: split blockIdx.y of gridDim.y.
+  const int nall = K / 128, splits = gridDim.y, sp = blockIdx.y;
+  const int ch0 = (int)((long long)nall * sp / splits);
+  const int nch = (int)((long long)nall * (sp + 1) / splits) - ch0;
   const uint32_t pitch = (uint32_t)K * 2u;
   // Slice position of this lane's 16 bytes and the 16-byte chunk it holds.
   const int pos = lane & 15;
@@ -153,8 +163,8 @@ __global__ void __launch_bounds__(128) rank_product_staged_kernel(
     const uint8_t* fbase = (const uint8_t*)(bt + (size_t)e * R * K);
     auto issue = [&](int ch, int st) {
       uint8_t* base = smem + st * STAGE;
-      const uint8_t* ab = (const uint8_t*)a + (size_t)ch * kStSlice;
-      const uint8_t* bb = fbase + (size_t)ch * kStSlice;
+      const uint8_t* ab = (const uint8_t*)a + (size_t)(ch0 + ch) * kStSlice;
+      const uint8_t* bb = fbase + (size_t)(ch0 + ch) * kStSlice;
 #pragma unroll
       for (int i = 0; i < A_PER_WAVE; ++i) {  // 4 rows per copy
         const int j = wave * A_PER_WAVE + i, r = j * 4 + (lane >> 4);
@@ -201,13 +211,33 @@ __global__ void __launch_bounds__(128) rank_product_staged_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = row0 + wave * 16 + 4 * (lane >> 4) + i;
-        if (r >= lo && r < hi) out[(size_t)r * R + cb * 16 + (lane & 15)] = f32_to_bf16(acc[cb][i]);
+        if (r >= lo && r < hi) {
+          const size_t o = (size_t)r * R + cb * 16 + (lane & 15);
+          if (partial == nullptr) out[o] = f32_to_bf16(acc[cb][i]);
+          else partial[(size_t)sp * rows * R + o] = acc[cb][i];
+        }
       }
     __syncthreads();  // the stages are refilled for the next expert
   }
 }
 
+// out = bf16(sum over splits of the partial sums, in split order).
+__global__ void __launch_bounds__(256) rank_product_reduce_kernel(const float* __restrict__ partial,
+                                                                  size_t n, int splits,
+                                                                  uint16_t* __restrict__ out) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float s = partial[i];
+  for (int p = 1; p < splits; ++p) s += partial[(size_t)p * n + i];
+  out[i] = f32_to_bf16(s);
+}
+
 }  // namespace
+
+extern "C" size_t mi355x_rank_product_workspace_size(int rows, int rank, int splits) {
+  if (rows <= 0 || rank <= 0 || splits <= 1) return 0;
+  return (size_t)splits * rows * rank * sizeof(float);
+}
 
 extern "C" int mi355x_rank_product(const void* a, int rows, int k, const void* bt, int rank,
                                    const int32_t* offsets, int experts, void* out, void* stream) {
@@ -222,8 +252,9 @@ extern "C" int mi355x_rank_product(const void* a, int rows, int k, const void* b
       (uint64_t)rank * (uint64_t)k * 2u < (1ull << 32)) {
     const dim3 grid((rows + kStRows - 1) / kStRows);
     auto launch = [&](auto kernel) {
-      hipLaunchKernelGGL(kernel, grid, dim3(128), 0, (hipStream_t)stream, (const uint16_t*)a, rows,
-                         k, (const uint16_t*)bt, offsets, experts, (uint16_t*)out);
+      hipLaunchKernelGGL(kernel, grid, dim3(64 * kStWaves), 0, (hipStream_t)stream, (const uint16_t*)a, rows,
+                         k, (const uint16_t*)bt, offsets, experts, (uint16_t*)out,
+                         (float*)nullptr);
     };
     switch (rank) {
       case 16: launch(rank_product_staged_kernel<16>); break;
@@ -237,6 +268,45 @@ extern "C" int mi355x_rank_product(const void* a, int rows, int k, const void* b
   hipLaunchKernelGGL(rank_product_kernel, dim3((rows + 15) / 16), dim3(64 * kRankWaves), 0,
                      (hipStream_t)stream, (const uint16_t*)a, rows, k, (const uint16_t*)bt, rank,
                      offsets, experts, (uint16_t*)out);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_rank_product_split(const void* a, int rows, int k, const void* bt, int rank,
+                                         const int32_t* offsets, int experts, int splits,
+                                         void* out, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
+  MI355X_REQUIRE(splits >= 1 && splits <= 64, "rank_product_split: splits must be in [1, 64]");
+  if (splits == 1) return mi355x_rank_product(a, rows, k, bt, rank, offsets, experts, out, stream);
+  MI355X_REQUIRE(rows >= 0 && k > 0 && k % 128 == 0,
+                 "rank_product_split: K must be a multiple of 128");
+  MI355X_REQUIRE(rank > 0 && rank % 16 == 0 && rank <= kMaxRank,
+                 "rank_product_split: rank must be a multiple of 16 up to %d, got %d", kMaxRank,
+                 rank);
+  MI355X_REQUIRE(splits <= k / 128, "rank_product_split: more splits than 128-wide K chunks");
+  MI355X_REQUIRE(experts > 0, "rank_product_split: experts must be positive");
+  MI355X_REQUIRE((uint64_t)rows * (uint64_t)k * 2u < (1ull << 32) &&
+                     (uint64_t)rank * (uint64_t)k * 2u < (1ull << 32),
+                 "rank_product_split: operands beyond 32-bit byte offsets");
+  MI355X_REQUIRE(workspace_bytes >= mi355x_rank_product_workspace_size(rows, rank, splits),
+                 "rank_product_split: workspace too small");
+  if (rows == 0) return MI355X_OK;
+  float* partial = (float*)workspace;
+  const dim3 grid((rows + kStRows - 1) / kStRows, splits);
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * kStWaves), 0, (hipStream_t)stream, (const uint16_t*)a, rows, k,
+                       (const uint16_t*)bt, offsets, experts, (uint16_t*)nullptr, partial);
+  };
+  switch (rank) {
+    case 16: launch(rank_product_staged_kernel<16>); break;
+    case 32: launch(rank_product_staged_kernel<32>); break;
+    case 48: launch(rank_product_staged_kernel<48>); break;
+    default: launch(rank_product_staged_kernel<64>); break;
+  }
+  MI355X_LAUNCH_CHECK();
+  const size_t n = (size_t)rows * rank;
+  hipLaunchKernelGGL(rank_product_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, partial, n, splits, (uint16_t*)out);
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
 }

@@ -73,6 +73,17 @@ def _timed(name, device, flops, nbytes, fn, *args):
     _TIMER.stop(name, device, start, flops, nbytes)
 
 
+_CU_COUNTS: dict[int, int] = {}
+
+
+def _cu_count(device: torch.device) -> int:
+    """Compute units of the device (cached; a host-side property query)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if index not in _CU_COUNTS:
+        _CU_COUNTS[index] = torch.cuda.get_device_properties(index).multi_processor_count
+    return _CU_COUNTS[index]
+
+
 def _ptr(t: torch.Tensor | None):
     return None if t is None else t.data_ptr()
 
@@ -527,9 +538,12 @@ def gemm(a, a_scale, w, w_scale, offsets, *, transposed_scale=False, interleave=
     return out
 
 
-def rank_product(a, bt, offsets):
+def rank_product(a, bt, offsets, *, splits=None):
     """``out[r] = a[r] @ bt[e]^T`` for the rows of each expert: bf16 ``[rows, R]``
-    from bf16 ``a [rows, K]`` and ``bt [E, R, K]`` (``mi355x_rank_product``)."""
+    from bf16 ``a [rows, K]`` and ``bt [E, R, K]`` (``mi355x_rank_product``).
+    ``splits`` divides K over several blocks per 32-row block (fp32 partials
+    added in order; ``mi355x_rank_product_split``); by default enough splits
+    for ~4 blocks per CU."""
     rows, k = a.shape
     experts, rank, bk = bt.shape
     if a.dtype != torch.bfloat16 or bt.dtype != torch.bfloat16 or bk != k:
@@ -537,8 +551,21 @@ def rank_product(a, bt, offsets):
     _check(offsets, (experts + 1,), torch.int32, "offsets")
     device = _on_gpu(a, bt, offsets)
     out = torch.empty((rows, rank), dtype=torch.bfloat16, device=device)
-    _timed("rank_product", device, 0, 2 * rows * k + 2 * rows * rank, "mi355x_rank_product",
-           _ptr(a), rows, k, _ptr(bt), rank, _ptr(offsets), experts, _ptr(out), _stream(device))
+    nbytes = 2 * rows * k + 2 * rows * rank
+    if splits is None:
+        blocks = -(-rows // 64)  # 64-row blocks of the staged kernel
+        splits = 1
+        if k % 128 == 0 and blocks:
+            splits = max(1, min(k // 128, 8, -(-4 * _cu_count(device) // blocks)))
+    if splits == 1:
+        _timed("rank_product", device, 0, nbytes, "mi355x_rank_product", _ptr(a), rows, k,
+               _ptr(bt), rank, _ptr(offsets), experts, _ptr(out), _stream(device))
+        return out
+    size = _native.query("mi355x_rank_product_workspace_size", rows, rank, splits)
+    workspace = torch.empty(size, dtype=torch.uint8, device=device)
+    _timed("rank_product", device, 0, nbytes, "mi355x_rank_product_split", _ptr(a), rows, k,
+           _ptr(bt), rank, _ptr(offsets), experts, int(splits), _ptr(out), _ptr(workspace), size,
+           _stream(device))
     return out
 
 

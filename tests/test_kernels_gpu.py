@@ -565,6 +565,26 @@ def test_rank_product_matches_fp32(device, counts, k, rank):
     assert frob_rel(out.float(), want) < 4e-3
 
 
+@pytest.mark.parametrize("splits", [1, 3, 7])
+def test_rank_product_k_splits(device, splits):
+    """K split over several blocks (fp32 partials added in split order, uneven
+    chunk ranges) against fp32, and each split count repeatable bit for bit."""
+    g = torch.Generator().manual_seed(90 + splits)
+    offsets = _ragged([300, 0, 77, 650])
+    rows, experts, k, rank = int(offsets[-1]), 4, 1152, 32
+    a = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+    bt = (torch.randn(experts, rank, k, generator=g) * 0.05).to(torch.bfloat16)
+    args = (a.to(device), bt.to(device), offsets.to(device))
+    out = K.rank_product(*args, splits=splits).cpu()
+    want = torch.zeros(rows, rank)
+    for e in range(experts):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        want[lo:hi] = a[lo:hi].float() @ bt[e].float().t()
+    assert max_rel(out.float(), want) < 1e-2
+    assert frob_rel(out.float(), want) < 4e-3
+    assert torch.equal(out, K.rank_product(*args, splits=splits).cpu())
+
+
 @pytest.mark.parametrize("counts,m,rank,transposed,chunk", [
     ([0, 37, 5, 0, 150, 16], 512, 16, False, None),     # empty experts, short experts
     ([700, 1, 1300], 1544, 32, True, 256),              # several chunks per expert, M % 2048
