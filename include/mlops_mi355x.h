@@ -183,8 +183,9 @@ int mi355x_unpermute_sum(const void* dx, const int32_t* slots, int tokens, int t
 /* Routed SwiGLU backward over sorted rows: from r = dy @ W2 [A,I] (bf16),
  * h [A,2I] interleaved and the route score of each sorted row
  * (weights[order[row]]): dscore = <r, act> (fp32), dh = dSwiGLU(score * r)
- * interleaved (bf16), a' = score * act (bf16). dh may be h itself (written
- * in place). Replaces routed_swiglu_rows_backward
+ * interleaved (bf16), a' = score * act (bf16; not written when a_prime is
+ * null). dh may be h itself (written in place). Replaces
+ * routed_swiglu_rows_backward
  * (kernels/quack_moe/swiglu_rows.py:101-146, :278-318). */
 int mi355x_routed_swiglu_bwd(const void* r, const void* h, const float* weights,
                              const int32_t* order, int rows, int width, float limit, void* dh,
@@ -376,19 +377,21 @@ size_t mi355x_rank_grad_workspace_size(int rows, int experts, int m, int rank, i
 int mi355x_rank_grad(const void* big, int rows, int m, const void* small, int rank,
                      const int32_t* offsets, int experts, int chunk, int transposed, float* out,
                      void* workspace, size_t workspace_bytes, void* stream);
-/* mi355x_rank_grad with token rows: row j of big is big[gather[j] / gather_div]
- * (big bf16 [big_rows, M], the routed row's token when gather is the routed
- * order and gather_div = k), and, when weight is given, row j of small is
- * bf16(small[j] * (weight[gather[j]] * alpha)). The token-side factor
- * gradients dB2 = s * sum (score dy) z2^T and dA13 = sum u13 x^T as
- * reductions over each expert's routed rows (src/mlops/lora/experts.py:
- * 53-167; providers/sonicmoe/lora.py:1062). Workspace as for
- * mi355x_rank_grad with `rows` routed rows. */
+/* mi355x_rank_grad with token rows and a row weight: row j of big is
+ * big[gather[j] / gather_div] (big bf16 [big_rows, M]; the routed row's token
+ * when gather is the routed order and gather_div = k; gather null: row j,
+ * big_rows = rows), and, when weight is given, row j of small is
+ * bf16(small[j] * (weight[weight_index[j]] * alpha)) (weight_index null:
+ * weight[j]). The factor gradients dB2 = s * sum (score dy) z2^T,
+ * dA13 = sum u13 x^T and dA2 = sum (score u2) a^T as reductions over each
+ * expert's routed rows (src/mlops/lora/experts.py:53-167;
+ * providers/sonicmoe/lora.py:1062). Workspace as for mi355x_rank_grad with
+ * `rows` routed rows. */
 int mi355x_rank_grad_gather(const void* big, int big_rows, int m, const void* small, int rows,
                             int rank, const int32_t* offsets, int experts, int chunk,
                             const int32_t* gather, int gather_div, const float* weight,
-                            float alpha, int transposed, float* out, void* workspace,
-                            size_t workspace_bytes, void* stream);
+                            const int32_t* weight_index, float alpha, int transposed, float* out,
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 /* The up projection with SwiGLU fused: mi355x_gemm_fp8_block in gate/up mode
  * (w13 [E, 2I, K], interleave = 1) writing h [rows, 2I] bf16 interleaved, and

@@ -66,8 +66,8 @@ SIGNATURES = {
     "mi355x_rank_product_split": (_I, [_P, _I, _I, _P, _I, _P, _I, _I, _P, _P, _S, _P]),
     "mi355x_rank_grad_workspace_size": (_S, [_I, _I, _I, _I, _I]),
     "mi355x_rank_grad": (_I, [_P, _I, _I, _P, _I, _P, _I, _I, _I, _P, _P, _S, _P]),
-    "mi355x_rank_grad_gather": (_I, [_P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _I, _P, _F, _I, _P,
-                                     _P, _S, _P]),
+    "mi355x_rank_grad_gather": (_I, [_P, _I, _I, _P, _I, _I, _P, _I, _I, _P, _I, _P, _P, _F, _I,
+                                     _P, _P, _S, _P]),
     "mi355x_gemm_fp8_block_lora": (_I, [_P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _I,
                                         _P, _P]),
     "mi355x_gemm_fp8_block_swiglu": (

@@ -474,7 +474,7 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
         o2.z = pack_bf16x2(ap[4], ap[5]); o2.w = pack_bf16x2(ap[6], ap[7]);
         *(uint4*)(dh + (size_t)row * 2 * width + 2 * j) = o0;
         *(uint4*)(dh + (size_t)row * 2 * width + 2 * j + 8) = o1;
-        *(uint4*)(a_prime + (size_t)row * width + j) = o2;
+        if (a_prime != nullptr) *(uint4*)(a_prime + (size_t)row * width + j) = o2;
         if (dhq != nullptr) {
           // dh row-quantized gate-first from its bf16 values, as the row
           // quantizer would read them back: the 16 lanes of this 128-column

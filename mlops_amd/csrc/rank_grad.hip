@@ -18,9 +18,11 @@
 //
 // Gathered form: row j of `big` may be a token row, big[gather[j] / div]
 // (the routed row's token), and row j of `small` may be scaled by
-// weight[gather[j]] * alpha (rounded to bf16 once, as bf16(z * (w * alpha))):
-// the token-side factor gradients of expert LoRA as reductions over each
-// expert's routed rows, with no [tokens, E * R] scatter.
+// weight[index[j]] * alpha (index null: weight[j]), rounded to bf16 once as
+// bf16(z * (w * alpha)): the token-side factor gradients of expert LoRA as
+// reductions over each expert's routed rows, with no [tokens, E * R]
+// scatter, and the route weight applied to a thin operand instead of a wide
+// one.
 #include "common.h"
 
 namespace {
@@ -75,7 +77,8 @@ __device__ __forceinline__ bf16x8_t gather8(const uint8_t* base, int pitch) {
 __global__ void __launch_bounds__(kThreads) rank_grad_partial_kernel(
     const uint16_t* __restrict__ big, int M, const uint16_t* __restrict__ small, int R,
     const int32_t* __restrict__ offsets, int experts, int chunk, const int32_t* __restrict__ gather,
-    int gather_div, const float* __restrict__ weight, float alpha, float* __restrict__ partial) {
+    int gather_div, const float* __restrict__ weight, const int32_t* __restrict__ windex,
+    float alpha, float* __restrict__ partial) {
   __shared__ int prefix[kMaxExperts + 1];
   __shared__ __align__(16) uint8_t big_s[kStRows * kBigPitch];
   __shared__ __align__(16) uint8_t small_s[kStRows * kSmallPitch];
@@ -117,7 +120,7 @@ __global__ void __launch_bounds__(kThreads) rank_grad_partial_kernel(
       if (r < row1) {
         sv = *(const uint4*)(small + (size_t)r * R + n0 + (tid & 1) * 8);
         if (weight != nullptr) {
-          const float f = weight[gather != nullptr ? gather[r] : r] * alpha;
+          const float f = weight[windex != nullptr ? windex[r] : r] * alpha;
           float z[8];
           unpack_bf16x8(sv, z);
           sv = make_uint4(pack_bf16x2(z[0] * f, z[1] * f), pack_bf16x2(z[2] * f, z[3] * f),
@@ -206,8 +209,9 @@ extern "C" size_t mi355x_rank_grad_workspace_size(int rows, int experts, int m, 
 namespace {
 int rank_grad_launch(const void* big, int rows, int m, const void* small, int rank,
                      const int32_t* offsets, int experts, int chunk, const int32_t* gather,
-                     int gather_div, const float* weight, float alpha, int transposed, float* out,
-                     void* workspace, size_t workspace_bytes, void* stream) {
+                     int gather_div, const float* weight, const int32_t* windex, float alpha,
+                     int transposed, float* out, void* workspace, size_t workspace_bytes,
+                     void* stream) {
   MI355X_REQUIRE(m > 0 && m % 8 == 0, "rank_grad: the wide dimension must be a multiple of 8");
   MI355X_REQUIRE(rank > 0 && rank % 16 == 0 && rank <= 64,
                  "rank_grad: the rank must be a multiple of 16 up to 64 (pad with zeros)");
@@ -226,7 +230,7 @@ int rank_grad_launch(const void* big, int rows, int m, const void* small, int ra
     const dim3 grid((m + kBlockColsMfma - 1) / kBlockColsMfma, (unsigned)chunks, rank / kRanks);
     hipLaunchKernelGGL(rank_grad_partial_kernel, grid, dim3(kThreads), 0, s,
                        (const uint16_t*)big, m, (const uint16_t*)small, rank, offsets, experts,
-                       chunk, gather, gather_div, weight, alpha, partial);
+                       chunk, gather, gather_div, weight, windex, alpha, partial);
     MI355X_LAUNCH_CHECK();
   }
   const size_t per = (size_t)m * rank;
@@ -243,18 +247,20 @@ extern "C" int mi355x_rank_grad(const void* big, int rows, int m, const void* sm
                                 float* out, void* workspace, size_t workspace_bytes,
                                 void* stream) {
   return rank_grad_launch(big, rows, m, small, rank, offsets, experts, chunk, nullptr, 1, nullptr,
-                          1.0f, transposed, out, workspace, workspace_bytes, stream);
+                          nullptr, 1.0f, transposed, out, workspace, workspace_bytes, stream);
 }
 
 extern "C" int mi355x_rank_grad_gather(const void* big, int big_rows, int m, const void* small,
                                        int rows, int rank, const int32_t* offsets, int experts,
                                        int chunk, const int32_t* gather, int gather_div,
-                                       const float* weight, float alpha, int transposed,
-                                       float* out, void* workspace, size_t workspace_bytes,
-                                       void* stream) {
-  MI355X_REQUIRE(gather != nullptr && gather_div >= 1,
-                 "rank_grad_gather: a gather index and a divisor >= 1 are required");
+                                       const float* weight, const int32_t* weight_index,
+                                       float alpha, int transposed, float* out, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  MI355X_REQUIRE(gather_div >= 1, "rank_grad_gather: the gather divisor must be >= 1");
+  MI355X_REQUIRE(gather != nullptr || big_rows == rows,
+                 "rank_grad_gather: without a gather index big has the routed rows");
   MI355X_REQUIRE(big_rows >= 0, "rank_grad_gather: negative token count");
   return rank_grad_launch(big, rows, m, small, rank, offsets, experts, chunk, gather, gather_div,
-                          weight, alpha, transposed, out, workspace, workspace_bytes, stream);
+                          weight, weight_index, alpha, transposed, out, workspace,
+                          workspace_bytes, stream);
 }

@@ -402,9 +402,10 @@ def unpermute_sum(dx, slots):
     return out
 
 
-def routed_swiglu_backward(r, h, weights, order, limit=None, *, dh_out=None):
+def routed_swiglu_backward(r, h, weights, order, limit=None, *, dh_out=None, a_prime=True):
     """``(dh [A,2I] interleaved, a' [A,I], dscore fp32 [A])``. ``dh`` is written
-    into ``dh_out`` when given, which may be ``h`` itself (in place)."""
+    into ``dh_out`` when given, which may be ``h`` itself (in place); with
+    ``a_prime=False`` a' is not written and ``None`` is returned for it."""
     rows, width = r.shape
     _check(h, (rows, 2 * width), torch.bfloat16, "h")
     device = _on_gpu(r, h, weights, order, dh_out)
@@ -413,30 +414,32 @@ def routed_swiglu_backward(r, h, weights, order, limit=None, *, dh_out=None):
         if not dh_out.is_contiguous():
             raise ValueError("dh_out must be contiguous")
     dh = torch.empty_like(h) if dh_out is None else dh_out
-    a_prime = torch.empty_like(r)
+    a_prime = torch.empty_like(r) if a_prime else None
     dscore = torch.empty(rows, dtype=torch.float32, device=device)
-    # r and h read; dh, a' and dscore written
-    nbytes = 2 * rows * width + 4 * rows * width + 4 * rows * width + 2 * rows * width + 8 * rows
+    # r and h read; dh, a' (when asked) and dscore written
+    nbytes = (6 + 4 + (2 if a_prime is not None else 0)) * rows * width + 8 * rows
     _timed("routed_swiglu_bwd", device, 0, nbytes, "mi355x_routed_swiglu_bwd", _ptr(r), _ptr(h),
            _ptr(weights), _ptr(order), rows, width, _limit(limit), _ptr(dh), _ptr(a_prime),
            _ptr(dscore), _stream(device))
     return dh, a_prime, dscore
 
 
-def routed_swiglu_backward_rows(r, h, weights, order, limit=None):
+def routed_swiglu_backward_rows(r, h, weights, order, limit=None, *, a_prime=True):
     """``routed_swiglu_backward`` plus dh row-quantized gate-first from its
     bf16 values: ``(dh, a', dscore, dhq e4m3 [A, 2I], dh_scales [2I/128, A])``,
-    the last two equal to ``quantize_rows(dh, gate_up=True)``."""
+    the last two equal to ``quantize_rows(dh, gate_up=True)``; a' is ``None``
+    (not written) with ``a_prime=False``."""
     rows, width = r.shape
     _check(h, (rows, 2 * width), torch.bfloat16, "h")
     device = _on_gpu(r, h, weights, order)
     dh = torch.empty_like(h)
-    a_prime = torch.empty_like(r)
+    a_prime = torch.empty_like(r) if a_prime else None
     dscore = torch.empty(rows, dtype=torch.float32, device=device)
     dhq = torch.empty((rows, 2 * width), dtype=FP8, device=device)
     dhs = torch.empty((2 * width // 128, rows), dtype=torch.float32, device=device)
     # r and h read; dh, a', dscore, dhq and its scales written
-    nbytes = (6 + 6 + 2) * rows * width + 8 * rows + 4 * rows * (2 * width // 128)
+    nbytes = ((12 + (2 if a_prime is not None else 0)) * rows * width + 8 * rows
+              + 4 * rows * (2 * width // 128))
     _timed("routed_swiglu_bwd_rows", device, 0, nbytes, "mi355x_routed_swiglu_bwd_rows_fp8",
            _ptr(r), _ptr(h), _ptr(weights), _ptr(order), rows, width, _limit(limit), _ptr(dh),
            _ptr(a_prime), _ptr(dscore), _ptr(dhq), _ptr(dhs), _stream(device))
@@ -570,32 +573,34 @@ def rank_product(a, bt, offsets, *, splits=None):
 
 
 def rank_grad(big, small, offsets, *, transposed=False, chunk=None, gather=None, gather_div=1,
-              weight=None, alpha=1.0):
+              weight=None, weight_index=None, alpha=1.0):
     """Per expert ``sum_j big[j]^T small[j]`` over its rows: fp32 ``[E, M, R]``
     (``[E, R, M]`` when ``transposed``) from bf16 ``big [rows, M]`` and ``small
     [rows, R]`` (``mi355x_rank_grad``; R a multiple of 16, at most 64).
 
     With ``gather`` (int32 ``[rows]``), row j of ``big [tokens, M]`` is
-    ``big[gather[j] // gather_div]``, and with ``weight`` (fp32, indexed by
-    ``gather[j]``) row j of ``small`` is ``bf16(small[j] * (weight[gather[j]]
-    * alpha))`` (``mi355x_rank_grad_gather``)."""
+    ``big[gather[j] // gather_div]``; with ``weight`` (fp32), row j of
+    ``small`` is ``bf16(small[j] * (weight[i] * alpha))``, i = ``weight_index[j]``
+    (or j) (``mi355x_rank_grad_gather``)."""
     big_rows, m = big.shape
     rows, rank = small.shape
     experts = offsets.numel() - 1
     if big.dtype != torch.bfloat16 or small.dtype != torch.bfloat16:
         raise ValueError("rank_grad takes bf16 operands")
+    plain = gather is None and weight is None
     if gather is None:
-        if weight is not None:
-            raise ValueError("rank_grad: a row weight needs the gather index")
         _check(small, (big_rows, rank), torch.bfloat16, "rank operand")
     else:
         _check(gather, (rows,), torch.int32, "gather index")
-        if weight is not None and (weight.dtype != torch.float32 or not weight.is_contiguous()):
-            raise ValueError("rank_grad: the row weight must be contiguous fp32")
-        if not big.is_contiguous() or not small.is_contiguous():
-            raise ValueError("rank_grad: operands must be contiguous")
+    if weight is not None and (weight.dtype != torch.float32 or not weight.is_contiguous()):
+        raise ValueError("rank_grad: the row weight must be contiguous fp32")
+    if weight_index is not None:
+        _check(weight_index, (rows,), torch.int32, "weight index")
+    if not plain and (not big.is_contiguous() or not small.is_contiguous()):
+        raise ValueError("rank_grad: operands must be contiguous")
     _check(offsets, (experts + 1,), torch.int32, "offsets")
-    device = _on_gpu(big, small, offsets, *(t for t in (gather, weight) if t is not None))
+    device = _on_gpu(big, small, offsets,
+                     *(t for t in (gather, weight, weight_index) if t is not None))
     if chunk is None:
         # Enough (chunk x 256-column) blocks to fill the chip twice over.
         blocks_per_chunk = -(-m // 256) * (rank // 16)
@@ -608,15 +613,15 @@ def rank_grad(big, small, offsets, *, transposed=False, chunk=None, gather=None,
     workspace = torch.empty(size, dtype=torch.uint8, device=device)
     # HBM-bound: big is streamed once; the products are on the bf16 MFMA
     nbytes = 2 * rows * (m + rank) + 4 * experts * m * rank
-    if gather is None:
+    if plain:
         _timed("rank_grad", device, 0, nbytes, "mi355x_rank_grad", _ptr(big), rows, m,
                _ptr(small), rank, _ptr(offsets), experts, chunk, int(transposed), _ptr(out),
                _ptr(workspace), size, _stream(device))
     else:
         _timed("rank_grad", device, 0, nbytes + 4 * rows, "mi355x_rank_grad_gather", _ptr(big),
                big_rows, m, _ptr(small), rows, rank, _ptr(offsets), experts, chunk,
-               _ptr(gather), int(gather_div), _ptr(weight), float(alpha), int(transposed),
-               _ptr(out), _ptr(workspace), size, _stream(device))
+               _ptr(gather), int(gather_div), _ptr(weight), _ptr(weight_index), float(alpha),
+               int(transposed), _ptr(out), _ptr(workspace), size, _stream(device))
     return out
 
 

@@ -175,7 +175,6 @@ class _ExpertLoRA(torch.autograd.Function):
             # Down projection: z2 = a @ A2^T per routed row (the thin product
             # streams a once; rank padded to 16).
             z2p = _row_rank(act, _padded_rank_rows(a2b, r2), offsets)
-            del act
             if current:
                 y = kernels.gemm_rowwise(aq, as_, w2_data, w2_scale, offsets,
                                          lora=(z2p, _padded(b2b, r2)))
@@ -189,13 +188,13 @@ class _ExpertLoRA(torch.autograd.Function):
         ctx.w13, ctx.w2 = w13, w2
         ctx.factor_dtypes = (a13.dtype, b13.dtype, a2.dtype, b2.dtype)
         ctx.save_for_backward(hidden, router_weight, logits, weights, ids, order, offsets, slots,
-                              h13, z13, z2p, rows_token, rows_expert, a13b, b13b, a2b, b2b)
+                              h13, act, z13, z2p, rows_token, rows_expert, a13b, b13b, a2b, b2b)
         ctx.mark_non_differentiable(counts)
         return output.reshape(hidden.shape), aux, counts, probability_sum
 
     @staticmethod
     def backward(ctx, grad_output, grad_aux, _grad_counts, grad_probability_sum):
-        (hidden, router_weight, logits, weights, ids, order, offsets, slots, h13, z13, z2p,
+        (hidden, router_weight, logits, weights, ids, order, offsets, slots, h13, act, z13, z2p,
          rows_token, rows_expert, a13b, b13b, a2b, b2b) = ctx.saved_tensors
         opts = ctx.opts
         top_k, mode, scale, limit = opts["top_k"], opts["routing_mode"], opts["scale"], opts["limit"]
@@ -234,13 +233,17 @@ class _ExpertLoRA(torch.autograd.Function):
                 w2_t = provider.transposed_data(ctx.w2)
                 r = kernels.gemm(dyq, dys, w2_t, w2_scale, offsets, transposed_scale=True,
                                  lora=lora_r)
+            # a' = score * a is only an operand of the base W2's gradient; the
+            # factor gradient dA2 takes the forward's bf16 a with the score on
+            # the thin u2 instead.
+            want_ap = bool(need[4])
             if current:
                 dh, a_prime, dscore = kernels.routed_swiglu_backward(
-                    r, h13, weights.reshape(-1), order, limit)
+                    r, h13, weights.reshape(-1), order, limit, a_prime=want_ap)
             else:
                 # dh row-quantized for the input-gradient GEMM in the same pass
                 dh, a_prime, dscore, dhq, dhs = kernels.routed_swiglu_backward_rows(
-                    r, h13, weights.reshape(-1), order, limit)
+                    r, h13, weights.reshape(-1), order, limit, a_prime=want_ap)
             del r
             # Input gradient: dx_j = dh_j @ W13[e] + (dh_j @ (s B13[e])) @ A13[e].
             r13 = _rank16(rank13)
@@ -263,9 +266,11 @@ class _ExpertLoRA(torch.autograd.Function):
             token_rows = dict(gather=order, gather_div=top_k)
             if need[8]:    # B2: s * sum_j dy_{t(j)} (score_j z2_j)^T
                 grads[3] = _factor_grad(dy, z2p, offsets, rank2, transposed=False,
-                                        weight=weights.reshape(-1), alpha=scale, **token_rows)
-            if need[7]:    # A2: sum_j u2_j a'_j^T, a' = score * a
-                grads[2] = _factor_grad(a_prime, u2, offsets, rank2, transposed=True)
+                                        weight=weights.reshape(-1), weight_index=order,
+                                        alpha=scale, **token_rows)
+            if need[7]:    # A2: sum_j (score_j u2_j) a_j^T  (= sum_j u2_j a'_j^T)
+                grads[2] = _factor_grad(act, u2, offsets, rank2, transposed=True,
+                                        weight=weights.reshape(-1), weight_index=order)
             if need[6]:    # B13: s * sum_j dh_j z13_j^T (rows back to gate then up)
                 g = _factor_grad(dh, z13, offsets, rank13, transposed=False)
                 grads[1] = gate_up_rows(g.mul_(scale))

@@ -565,6 +565,26 @@ def test_rank_product_matches_fp32(device, counts, k, rank):
     assert frob_rel(out.float(), want) < 4e-3
 
 
+def test_rank_grad_row_weight_without_gather(device):
+    """Routed rows of big (no gather) with small scaled by weight[order[j]]:
+    dA2 = sum_j (score_j u2_j) a_j^T, against fp64 on the same operands."""
+    g = torch.Generator().manual_seed(5)
+    tokens, top_k, experts, m, rank = 250, 2, 5, 392, 16
+    ids = torch.stack([torch.randperm(experts, generator=g)[:top_k] for _ in range(tokens)]).int()
+    order, offsets, _ = O.sort_assignments(ids, experts)
+    rows = tokens * top_k
+    big = torch.randn(rows, m, generator=g).to(torch.bfloat16)
+    small = (torch.randn(rows, rank, generator=g) * 0.3).to(torch.bfloat16)
+    weight = torch.rand(rows, generator=g)
+    out = K.rank_grad(big.to(device), small.to(device), offsets.to(device), transposed=True,
+                      weight=weight.to(device), weight_index=order.to(device)).cpu()
+    scaled = (small.float() * weight[order.long()][:, None]).to(torch.bfloat16)
+    for e in range(experts):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        want = (big[lo:hi].double().t() @ scaled[lo:hi].double()).t()
+        assert (out[e].double() - want).abs().max() <= 1e-5 * want.abs().max() + 1e-6, e
+
+
 @pytest.mark.parametrize("splits", [1, 3, 7])
 def test_rank_product_k_splits(device, splits):
     """K split over several blocks (fp32 partials added in split order, uneven
@@ -636,7 +656,8 @@ def test_rank_grad_gathered_token_rows(device, weighted, transposed):
     alpha = 1.5 if weighted else 1.0
     out = K.rank_grad(big.to(device), small.to(device), offsets.to(device),
                       transposed=transposed, gather=order.to(device), gather_div=top_k,
-                      weight=None if weight is None else weight.to(device), alpha=alpha).cpu()
+                      weight=None if weight is None else weight.to(device),
+                      weight_index=order.to(device), alpha=alpha).cpu()
     tok = order.long() // top_k
     scaled = small
     if weighted:
