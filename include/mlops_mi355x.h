@@ -80,6 +80,19 @@ int mi355x_router_topk_bwd(const float* logits, const float* weights, const int3
                            const float* grad_prob_sum, const int32_t* offsets, int segments,
                            const int32_t* seg_offsets, const int32_t* seg_counts,
                            float* grad_logits, void* stream);
+/* mi355x_router_topk_bwd that also writes the two bf16 pieces of the logit
+ * gradient g the router GEMMs consume, pieces bf16 [T, 2E]: row t holds
+ * hi = bf16(g[t, :]) then mid = bf16(g[t, :] - hi) (round to nearest even).
+ * hi is the input gradient's operand (grad_hidden += hi @ W) and [hi | mid]
+ * the weight gradient's (dW = hi^T x + mid^T x); grad_logits may be NULL.
+ * Replaces the casts of kernels/router.py:92-113 (and moe_common.py:142). */
+int mi355x_router_topk_bwd_split(const float* logits, const float* weights, const int32_t* ids,
+                                 const float* dscore, const int32_t* slots, int tokens,
+                                 int experts, int top_k, int mode, const float* grad_aux,
+                                 const float* grad_prob_sum, const int32_t* offsets,
+                                 int segments, const int32_t* seg_offsets,
+                                 const int32_t* seg_counts, float* grad_logits, void* pieces,
+                                 void* stream);
 
 /* ----------------------------------------------------------- permute ---- */
 

@@ -32,6 +32,10 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _P, _P, _P, _P],
     ),
+    "mi355x_router_topk_bwd_split": (
+        _I,
+        [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P],
+    ),
     "mi355x_permute_plan_workspace_size": (_S, [_I, _I]),
     "mi355x_permute_plan": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _S, _P]),
     "mi355x_permute_plan_noalloc_max_assignments": (_S, [_I]),

@@ -450,7 +450,7 @@ __global__ void __launch_bounds__(256) router_bwd_kernel(
     const int32_t* __restrict__ slots, int tokens, int experts, int top_k, int mode,
     const float* __restrict__ grad_aux, const float* __restrict__ grad_ps,
     const int32_t* __restrict__ offsets, int segments, const int32_t* __restrict__ seg_offsets,
-    const int32_t* __restrict__ seg_counts, float* __restrict__ grad_logits) {
+    const int32_t* __restrict__ seg_counts, float* __restrict__ grad_logits, uint16_t* __restrict__ pieces) {
   const int wave = threadIdx.x >> 6, lane = lane_id();
   const int token = blockIdx.x * kTokensPerBlock + wave;
   if (token >= tokens) return;
@@ -599,10 +599,26 @@ __global__ void __launch_bounds__(256) router_bwd_kernel(
       }
     }
   }
-  float* out = grad_logits + (size_t)token * experts;
-  SLOTS(i) {
-    int e = lane + 64 * i;
-    if (e < experts) out[e] = g[i];
+  if (grad_logits != nullptr) {
+    float* out = grad_logits + (size_t)token * experts;
+    SLOTS(i) {
+      int e = lane + 64 * i;
+      if (e < experts) out[e] = g[i];
+    }
+  }
+  if (pieces != nullptr) {
+    // The two bf16 pieces of the router weight gradient's operand, side by
+    // side in a row of 2E: hi = bf16(g), mid = bf16(g - hi) (both rounded to
+    // nearest even, as torch's casts).
+    uint16_t* row_out = pieces + (size_t)token * 2 * experts;
+    SLOTS(i) {
+      int e = lane + 64 * i;
+      if (e < experts) {
+        const uint16_t hi = f32_to_bf16(g[i]);
+        row_out[e] = hi;
+        row_out[experts + e] = f32_to_bf16(g[i] - bf16_to_f32(hi));
+      }
+    }
   }
 }
 
@@ -696,13 +712,13 @@ extern "C" int mi355x_router_stats(const float* logits, const int32_t* ids, int 
   return MI355X_OK;
 }
 
-extern "C" int mi355x_router_topk_bwd(const float* logits, const float* weights,
-                                      const int32_t* ids, const float* dscore,
-                                      const int32_t* slots, int tokens, int experts, int top_k,
-                                      int mode, const float* grad_aux, const float* grad_prob_sum,
-                                      const int32_t* offsets, int segments,
-                                      const int32_t* seg_offsets, const int32_t* seg_counts,
-                                      float* grad_logits, void* stream) {
+namespace {
+int router_bwd_launch(const float* logits, const float* weights, const int32_t* ids,
+                      const float* dscore, const int32_t* slots, int tokens, int experts,
+                      int top_k, int mode, const float* grad_aux, const float* grad_prob_sum,
+                      const int32_t* offsets, int segments, const int32_t* seg_offsets,
+                      const int32_t* seg_counts, float* grad_logits, uint16_t* pieces,
+                      void* stream) {
   MI355X_REQUIRE(experts > 0 && experts <= 64 * kMaxPerLane, "router_bwd: bad experts %d",
                  experts);
   MI355X_REQUIRE(top_k > 0 && top_k <= experts && top_k <= kMaxTopK, "router_bwd: bad top_k");
@@ -717,7 +733,7 @@ extern "C" int mi355x_router_topk_bwd(const float* logits, const float* weights,
   auto launch = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, grid, dim3(256), 0, (hipStream_t)stream, logits, weights, ids,
                        dscore, slots, tokens, experts, top_k, mode, grad_aux, grad_prob_sum,
-                       offsets, segments, seg_offsets, seg_counts, grad_logits);
+                       offsets, segments, seg_offsets, seg_counts, grad_logits, pieces);
   };
   switch (slots_per_lane(experts)) {
     case 1: launch(router_bwd_kernel<1>); break;
@@ -727,4 +743,32 @@ extern "C" int mi355x_router_topk_bwd(const float* logits, const float* weights,
   }
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
+}
+}  // namespace
+
+extern "C" int mi355x_router_topk_bwd(const float* logits, const float* weights,
+                                      const int32_t* ids, const float* dscore,
+                                      const int32_t* slots, int tokens, int experts, int top_k,
+                                      int mode, const float* grad_aux, const float* grad_prob_sum,
+                                      const int32_t* offsets, int segments,
+                                      const int32_t* seg_offsets, const int32_t* seg_counts,
+                                      float* grad_logits, void* stream) {
+  MI355X_REQUIRE(grad_logits != nullptr, "router_bwd: grad_logits is required");
+  return router_bwd_launch(logits, weights, ids, dscore, slots, tokens, experts, top_k, mode,
+                           grad_aux, grad_prob_sum, offsets, segments, seg_offsets, seg_counts,
+                           grad_logits, nullptr, stream);
+}
+
+extern "C" int mi355x_router_topk_bwd_split(const float* logits, const float* weights,
+                                            const int32_t* ids, const float* dscore,
+                                            const int32_t* slots, int tokens, int experts,
+                                            int top_k, int mode, const float* grad_aux,
+                                            const float* grad_prob_sum, const int32_t* offsets,
+                                            int segments, const int32_t* seg_offsets,
+                                            const int32_t* seg_counts, float* grad_logits,
+                                            void* pieces, void* stream) {
+  MI355X_REQUIRE(pieces != nullptr, "router_bwd_split: the bf16 pieces output is required");
+  return router_bwd_launch(logits, weights, ids, dscore, slots, tokens, experts, top_k, mode,
+                           grad_aux, grad_prob_sum, offsets, segments, seg_offsets, seg_counts,
+                           grad_logits, (uint16_t*)pieces, stream);
 }

@@ -198,9 +198,11 @@ def router_stats(logits, ids, top_k: int, mode: str, lengths: Sequence[int]):
 
 def router_backward(
     logits, weights, ids, dscore, slots, mode: str, *, grad_aux=None, grad_prob_sum=None,
-    offsets=None, seg_offsets=None, seg_counts=None,
+    offsets=None, seg_offsets=None, seg_counts=None, pieces=False,
 ):
-    """fp32 ``grad_logits [T,E]`` (route weights' cotangent = ``dscore[slots]``)."""
+    """fp32 ``grad_logits [T,E]`` (route weights' cotangent = ``dscore[slots]``).
+    With ``pieces=True``, instead the bf16 ``[T, 2E]`` buffer ``[hi | mid]``,
+    ``hi = bf16(g)``, ``mid = bf16(g - hi)`` (``mi355x_router_topk_bwd_split``)."""
     tokens, experts = logits.shape
     top_k = ids.shape[1]
     if grad_aux is not None:
@@ -210,6 +212,17 @@ def router_backward(
     device = _on_gpu(logits, weights, ids, dscore, slots, grad_aux, grad_prob_sum, offsets,
                      seg_offsets, seg_counts)
     segments = 1 if seg_counts is None else seg_counts.shape[0]
+    if pieces:
+        out = torch.empty((tokens, 2 * experts), dtype=torch.bfloat16, device=device)
+        # logits read, both bf16 pieces written; weights, ids and dscore read
+        _timed(
+            "router_topk_bwd", device, 0, 8 * tokens * experts + 12 * tokens * top_k,
+            "mi355x_router_topk_bwd_split", _ptr(logits), _ptr(weights), _ptr(ids), _ptr(dscore),
+            _ptr(slots), tokens, experts, top_k, ROUTING_MODES[mode], _ptr(grad_aux),
+            _ptr(grad_prob_sum), _ptr(offsets), segments, _ptr(seg_offsets), _ptr(seg_counts),
+            None, _ptr(out), _stream(device),
+        )
+        return out
     grad = torch.empty((tokens, experts), dtype=torch.float32, device=device)
     # logits read and their gradient written; weights, ids and dscore read
     nbytes = 8 * tokens * experts + 12 * tokens * top_k

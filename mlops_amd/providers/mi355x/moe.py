@@ -272,11 +272,27 @@ def routing_backward(grad_h2, x, router_weight, logits, route_weights, route_ids
         _, _, seg_counts, seg_offsets = kernels.router_stats(
             logits, route_ids, int(top_k), routing_mode, lengths
         )
+    # bf16 activations: the kernel writes the cotangent's bf16 pieces, the
+    # operands of both router GEMMs, in place of fp32 logit gradients.
+    split = (router.operand_dtype(x) == torch.bfloat16 and grad_h2.dtype == torch.bfloat16
+             and x.dtype == torch.bfloat16)
     grad_logits = kernels.router_backward(
         logits, route_weights, route_ids, dscore, slots, routing_mode,
         grad_aux=grad_aux, grad_prob_sum=grad_probability_sum, offsets=offsets,
-        seg_offsets=seg_offsets, seg_counts=seg_counts,
+        seg_offsets=seg_offsets, seg_counts=seg_counts, pieces=split,
     )
+    if split:
+        if need_router:
+            grad_router = router.router_weight_gradient_from_pieces(grad_logits, x, router_dtype)
+            if grad_router.stride() != router_weight.stride():
+                aligned = torch.empty_strided(grad_router.shape, router_weight.stride(),
+                                              dtype=grad_router.dtype, device=grad_router.device)
+                aligned.copy_(grad_router)
+                grad_router = aligned
+        else:
+            grad_router = skipped_gradient(router_weight, router_dtype)
+        router.add_router_input_gradient_from_pieces_(grad_h2, grad_logits, router_weight)
+        return grad_router
     if need_router:
         grad_router = router.router_weight_gradient(grad_logits, x, router_dtype)
         if grad_router.stride() != router_weight.stride():

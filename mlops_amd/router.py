@@ -65,6 +65,23 @@ def split_k_product(left: torch.Tensor, right: torch.Tensor) -> torch.Tensor:
     return _product_fp32(left.t(), right)
 
 
+def router_weight_gradient_from_pieces(pieces, hidden, dtype) -> torch.Tensor:
+    """:func:`router_weight_gradient` from the cotangent already split into
+    its bf16 ``[hi | mid]`` pieces ``[T, 2E]`` (the router backward kernel
+    writes them): ``hi^T x + mid^T x`` with fp32 sums."""
+    experts = pieces.shape[1] // 2
+    both = split_k_product(pieces, hidden)
+    return both[:experts].add_(both[experts:]).to(dtype)
+
+
+def add_router_input_gradient_from_pieces_(grad_hidden, pieces, weight):
+    """``grad_hidden += hi @ weight`` in place, ``hi = bf16(g)`` the first half
+    of the pieces (the same operand as ``grad_logits.to(bf16)``)."""
+    experts = pieces.shape[1] // 2
+    grad_hidden.addmm_(pieces[:, :experts], weight.to(grad_hidden.dtype))
+    return grad_hidden
+
+
 def router_weight_gradient(grad_logits, hidden, dtype) -> torch.Tensor:
     """``grad_logits.T @ hidden`` with fp32 sums, the cotangent in two bf16 pieces."""
     operands = operand_dtype(hidden)
@@ -90,6 +107,8 @@ def router_weight_gradient(grad_logits, hidden, dtype) -> torch.Tensor:
 
 __all__ = [
     "add_router_input_gradient_",
+    "add_router_input_gradient_from_pieces_",
+    "router_weight_gradient_from_pieces",
     "split_k_product",
     "operand_dtype",
     "router_logits",

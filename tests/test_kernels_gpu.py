@@ -105,6 +105,15 @@ def test_router_stats_and_backward(device, mode, lengths, experts, top_k):
                              seg_offsets=seg_offsets, seg_counts=seg_counts)
     want = O.routing_gradient(ga, gps, gw, w, ids, logits, mode, lengths)
     assert max_rel(grad.cpu(), want) < 1e-5
+    # the split form: [hi | mid] bf16 pieces of the same fp32 gradient, as
+    # torch's casts make them
+    pieces = K.router_backward(logits.to(device), w.to(device), ids.to(device),
+                               dscore.to(device), slots.to(device), mode, grad_aux=ga.to(device),
+                               grad_prob_sum=gps.to(device), offsets=offsets.to(device),
+                               seg_offsets=seg_offsets, seg_counts=seg_counts, pieces=True).cpu()
+    hi = grad.cpu().to(torch.bfloat16)
+    assert torch.equal(pieces[:, :experts], hi)
+    assert torch.equal(pieces[:, experts:], (grad.cpu() - hi.float()).to(torch.bfloat16))
 
 
 # ------------------------------------------------------------------ permute
