@@ -270,6 +270,18 @@ int mi355x_gemm_fp8_block(const uint8_t* a, const float* a_scale, int rows, cons
                           const float* w_scale, int w_scale_t, int experts, int n, int k,
                           const int32_t* offsets, int interleave, const void* addend, void* out,
                           void* stream);
+/* The input-gradient GEMM on the weight as stored, without a transposed
+ * copy: w is e4m3 [E,K,N] with its own block scales w_scale [E,K/128,N/128]
+ * (for dx = dh @ W13: W13 [E,2I,H]; for r = dy @ W2: W2 [E,H,I]), out bf16
+ * [rows,N]; N a multiple of 256, K of 128. Bitwise equal to
+ * mi355x_gemm_fp8_block with w_scale_t = 1 on the transposed copy. The
+ * weight tile is copied K-major and its MFMA operand gathered with gfx950's
+ * transposing LDS read (ds_read_b64_tr_b8). Replaces
+ * block_fp8_transposed_gemm (kernels/quack_moe/block_fp8_gemm.py:1424, which
+ * reads the weight MN-major as well). */
+int mi355x_gemm_fp8_block_kmajor(const uint8_t* a, const float* a_scale, int rows,
+                                 const uint8_t* w, const float* w_scale, int experts, int n, int k,
+                                 const int32_t* offsets, void* out, void* stream);
 
 /* mi355x_gemm_fp8_block with a rank-r term in place of the addend:
  *   out[r, n] = (block-FP8 product as above) + sum_j lora_z[r, j] * lora_b[e][n', j]

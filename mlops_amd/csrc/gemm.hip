@@ -403,6 +403,9 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
                           const int32_t* offsets, int interleave, const void* addend, void* out,
                           uint8_t* act_q, float* act_scales, float limit, const void* lora_z,
                           const void* lora_b, int lora_rank, void* stream);
+int mi355x_gemm_v2_kmajor_launch(const uint8_t* a, const float* a_scale, int rows,
+                                 const uint8_t* w, const float* w_scale, int experts, int n, int k,
+                                 const int32_t* offsets, void* out, void* stream);
 
 int mi355x_gemm_v2_rowwise_launch(const uint8_t* a, const float* a_scale, int rows,
                                   const uint8_t* w, const float* w_scale, int experts, int n,
@@ -436,6 +439,25 @@ extern "C" int mi355x_gemm_fp8_block(const uint8_t* a, const float* a_scale, int
                      (hipStream_t)stream, a, a_scale, rows, w, w_scale, w_scale_t, experts, n, k,
                      offsets, interleave, (const uint16_t*)addend, (uint16_t*)out);
   MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_gemm_fp8_block_kmajor(const uint8_t* a, const float* a_scale, int rows,
+                                            const uint8_t* w, const float* w_scale, int experts,
+                                            int n, int k, const int32_t* offsets, void* out,
+                                            void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= kMaxExperts,
+                 "gemm_kmajor: experts must be in [1, %d]", kMaxExperts);
+  MI355X_REQUIRE(n > 0 && n % 256 == 0, "gemm_kmajor: N must be a multiple of 256, got %d", n);
+  MI355X_REQUIRE(k > 0 && k % BK == 0, "gemm_kmajor: K must be a multiple of %d, got %d", BK, k);
+  MI355X_REQUIRE(rows >= 0, "gemm_kmajor: negative rows");
+  MI355X_REQUIRE((uint64_t)(k - 1) * (uint64_t)n + 256 < (1ull << 32),
+                 "gemm_kmajor: a weight slice beyond 32-bit offsets");
+  if (rows == 0) return MI355X_OK;
+  const int v2 = mi355x_gemm_v2_kmajor_launch(a, a_scale, rows, w, w_scale, experts, n, k, offsets,
+                                              out, stream);
+  if (v2 < 0) return v2;
+  MI355X_REQUIRE(v2 == 0, "gemm_kmajor: shape outside the pipelined kernel");
   return MI355X_OK;
 }
 

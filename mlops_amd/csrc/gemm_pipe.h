@@ -101,6 +101,37 @@ __device__ __forceinline__ v8i frag(const uint8_t* tile, int row, int lane) {
   return r;
 }
 
+// Position of 16-byte unit u in row r of a K-major stage tile: u ^ kmsw(r).
+// A fragment read takes rows r .. r+7 (r % 8 == 0) in each 16-lane group and
+// rows 16 apart across the four groups of a wave: the low bits spread a
+// group's rows over 8 positions, and bit 3 (row / 16 odd) moves the odd
+// groups to the other 8, so a 64-lane read meets each bank twice.
+__device__ __forceinline__ int kmsw(int r) { return (r & 15) ^ (((r >> 4) & 1) << 3); }
+
+// The same fragment (32 fp8 K-values of one B column) from a K-major stage
+// tile: 128 K rows of 256 bytes (one byte per column), 16-byte unit u of row
+// r stored at u ^ kmsw(r). ds_read_b64_tr_b8 gives lane j of each 16-lane
+// group byte (j % 8) of the 8 bytes addressed by lane 2b + j / 8, as its
+// byte b; so with lane i addressing K row kbase + i / 2 at column
+// col0 + 8 (i % 2), lane j receives column col0 + j at K rows kbase .. +7.
+// Four such reads give the K rows of frag(): 16g .. 16g+15 and
+// 64+16g .. 64+16g+15 (g = lane / 16).
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ v8i frag_kmajor(const uint8_t* tile, int col0, int lane) {
+  const int g = lane >> 4, j = lane & 15;
+  const int unit = col0 >> 4;
+  v8i r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int row = (p >> 1) * 64 + 16 * g + (p & 1) * 8 + (j >> 1);
+    const uint8_t* at = tile + row * 256 + 16 * (unit ^ kmsw(row)) + 8 * (j & 1);
+    const v2i_t v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i_t*)(lds_ptr_t)at);
+    r[2 * p] = v[0];
+    r[2 * p + 1] = v[1];
+  }
+  return r;
+}
+
 __device__ __forceinline__ v4f mfma(v8i a, v8i b) {
   const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, zero, 0, 0, 0, 0, 0, 0);

@@ -74,7 +74,12 @@ typedef short v4s __attribute__((ext_vector_type(4)));
 // kRow: row-scaled operands (one descale per activation row, a_scale[rows],
 // and one per weight output row, w_scale[E, N]): the K loop accumulates in
 // the MFMA itself and the epilogue applies (acc * a_scale) * w_scale once.
-template <bool kAct, bool kAdd, bool kLora, bool kRow = false>
+// kKM: the weight is read as stored, [E, K, N] (K-major: the input-gradient
+// GEMMs on the forward weights, no transposed copy). Its tiles are copied as
+// 128 K rows of 256 bytes and the B fragments read with ds_read_b64_tr_b8;
+// the MFMA columns are then the tile's columns in order, so the epilogue
+// regroups each row's values through LDS into 8-column stores.
+template <bool kAct, bool kAdd, bool kLora, bool kRow = false, bool kKM = false>
 __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ a_scale, int rows,
     const uint8_t* __restrict__ w, const float* __restrict__ w_scale, int w_scale_t, int experts,
@@ -95,6 +100,14 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
   const int tid = threadIdx.x, lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 wave grid
+  // B fragment of MFMA block jb of this wave's 128 columns. The K-major
+  // form takes the lane id through an empty asm at each step, so its 32
+  // per-lane fragment addresses are formed where used instead of being
+  // hoisted out of the K loop (live across it, they would spill).
+  auto bfrag = [&](const uint8_t* tb, int jb, uint32_t step_lane) -> v8i {
+    if constexpr (kKM) return frag_kmajor(tb, wn * 128 + jb * 16, (int)step_lane);
+    else return frag(tb, wn * 128 + jb * 16 + (lane & 15), lane);
+  };
 
   // Direct loads of one K step of tile t into stage `stage`.
   auto issue = [&](const Tile& t, int step, int stage) {
@@ -109,12 +122,24 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       const uint32_t off = (uint32_t)min(t.row0 + r, rows - 1) * (uint32_t)K + 16 * ((lane & 7) ^ swz(r));
       dma16(abase, off, base + (wave * A_LOADS + i) * 1024);
     }
+    if constexpr (kKM) {
+      // K rows kb*128 .. +127 of the expert's [K, N] weight, columns of the
+      // tile: a copy is 4 rows x 256 bytes; unit u of row r lands at u ^ kmsw(r).
+      const uint8_t* kbase = w + (size_t)t.e * N * K + (size_t)kb * BK * N + (size_t)t.nt * BN;
 #pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-      const int tr = (wave * B_LOADS + i) * 8 + (lane >> 3);
-      const uint32_t off = (uint32_t)weight_row(tr, t.nt, interleave, half_n) * (uint32_t)K +
-                           16 * ((lane & 7) ^ swz(tr));
-      dma16(bbase, off, base + A_BYTES + (wave * B_LOADS + i) * 1024);
+      for (int i = 0; i < B_LOADS; ++i) {
+        const int r = (wave * B_LOADS + i) * 4 + (lane >> 4);
+        const uint32_t off = (uint32_t)r * (uint32_t)N + 16 * ((lane & 15) ^ kmsw(r));
+        dma16(kbase, off, base + A_BYTES + (wave * B_LOADS + i) * 1024);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < B_LOADS; ++i) {
+        const int tr = (wave * B_LOADS + i) * 8 + (lane >> 3);
+        const uint32_t off = (uint32_t)weight_row(tr, t.nt, interleave, half_n) * (uint32_t)K +
+                             16 * ((lane & 7) ^ swz(tr));
+        dma16(bbase, off, base + A_BYTES + (wave * B_LOADS + i) * 1024);
+      }
     }
     if constexpr (kRow) return;  // no per-step scales
     const float* sbase = a_scale + (size_t)kb * rows;
@@ -224,14 +249,16 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       const uint8_t* ta = base;
       const uint8_t* tb = base + A_BYTES;
       if constexpr (kRow) {
-        v8i bcur = frag(tb, wn * 128 + (lane & 15), lane);
+        uint32_t klane = lane;
+        if constexpr (kKM) asm volatile("" : "+v"(klane));
+        v8i bcur = bfrag(tb, 0, klane);
         v8i af[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) af[i] = frag(ta, wm * 64 + i * 16 + (lane & 15), lane);
 #pragma unroll
         for (int jb = 0; jb < 8; ++jb) {
           v8i bnext = bcur;
-          if (jb < 7) bnext = frag(tb, wn * 128 + (jb + 1) * 16 + (lane & 15), lane);
+          if (jb < 7) bnext = bfrag(tb, jb + 1, klane);
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[i][jb] = mfma_acc(af[i], bcur, acc[i][jb]);
           bcur = bnext;
@@ -246,7 +273,9 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       // two waves share a SIMD, 256 registers each), read one block ahead.
       // Reads in use order (first B block, A blocks, then the scales), so
       // the first MFMA waits for two of them rather than for all.
-      v8i bcur = frag(tb, wn * 128 + (lane & 15), lane);
+      uint32_t klane = lane;
+      if constexpr (kKM) asm volatile("" : "+v"(klane));
+      v8i bcur = bfrag(tb, 0, klane);
       v8i af[4];
       float s4[4][4];
 #pragma unroll
@@ -267,7 +296,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
             for (int r = 0; r < 4; ++r) sc[i][r] = s4[i][r] * sb;
         }
         v8i bnext = bcur;
-        if (jb < 7) bnext = frag(tb, wn * 128 + (jb + 1) * 16 + (lane & 15), lane);
+        if (jb < 7) bnext = bfrag(tb, jb + 1, klane);
         v4f p[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) p[i] = mfma(af[i], bcur);
@@ -295,6 +324,43 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     uint32_t elane = lane;
     asm volatile("" : "+v"(elane));
     const uint32_t lane_col = (elane & 15) * 8;
+    if constexpr (kKM) {
+      // The lane holds column jb*16 + lane%16 of each block: the rows go
+      // through this wave's 8 KB of the stage the last step read (32 rows
+      // at a time, natural column order), and come back as 8 consecutive
+      // columns per lane for one 16-byte store per row, as below.
+      static_assert(!kAct && !kAdd && !kLora && !kRow, "K-major weights: plain form only");
+      lds_sync();  // every wave is done with the last step's fragments
+      uint16_t* st = (uint16_t*)(smem + (stage ^ 1) * STAGE_BYTES) + wave * (32 * 128);
+      const uint32_t l16 = elane & 15, lg = elane >> 4;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int jb = 0; jb < 8; ++jb)
+              st[(ii * 16 + 4 * lg + r) * 128 + jb * 16 + l16] =
+                  f32_to_bf16(acc[half * 2 + ii][jb][r]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t lrow = ii * 16 + 4 * lg + r;
+            const uint4 o = *(const uint4*)&st[lrow * 128 + lane_col];
+            const uint32_t orow = half * 32 + lrow;  // row within the wave's 64
+            if (wm * 64 + (int)orow < ct.nvalid)
+              store_stream(obase + orow * (uint32_t)N + lane_col, o);
+          }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    } else {
     // kRow: the lane's 8 output columns' weight descales.
     float wsc[8];
     if constexpr (kRow) {
@@ -406,6 +472,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
         }
       }
     }
+    }  // not kKM
     if (next_tile >= total) break;
     ++round;
     tile = next_tile;
@@ -476,6 +543,24 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
     addend != nullptr ? launch(grouped_gemm_v2_kernel<false, true, false>)
                       : launch(grouped_gemm_v2_kernel<false, false, false>);
   }
+  MI355X_LAUNCH_CHECK();
+  return 0;
+}
+
+// K-major weight (see kKM): w [E, K, N] e4m3 with its own block scales
+// [E, K/128, N/128]; returns 1 if the shape is not this kernel's (N % 256).
+int mi355x_gemm_v2_kmajor_launch(const uint8_t* a, const float* a_scale, int rows,
+                                 const uint8_t* w, const float* w_scale, int experts, int n, int k,
+                                 const int32_t* offsets, void* out, void* stream) {
+  if (n % BN != 0 || experts > kMaxExperts) return 1;
+  const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
+  const int grid = upper < cu_count() ? upper : cu_count();
+  const Order order = tile_order(n, k);
+  hipLaunchKernelGGL((grouped_gemm_v2_kernel<false, false, false, false, true>), dim3(grid),
+                     dim3(kThreads), 0, (hipStream_t)stream, a, a_scale, rows, w, w_scale, 1,
+                     experts, n, k, offsets, 0, (const uint16_t*)nullptr, (uint16_t*)out,
+                     (uint8_t*)nullptr, (float*)nullptr, 0.0f, (const uint16_t*)nullptr,
+                     (const uint16_t*)nullptr, 0, order.n_group, order.rotate);
   MI355X_LAUNCH_CHECK();
   return 0;
 }

@@ -554,6 +554,30 @@ def gemm(a, a_scale, w, w_scale, offsets, *, transposed_scale=False, interleave=
     return out
 
 
+def gemm_kmajor(a, a_scale, w, w_scale, offsets):
+    """Input-gradient GEMM on a weight as stored: ``a [A, K] @ w[e]`` for
+    e4m3 ``w [E, K, N]`` with its own scales ``[E, K/128, N/128]``, bf16
+    ``[A, N]`` (``mi355x_gemm_fp8_block_kmajor``); bitwise the same as
+    :func:`gemm` on the transposed copy with ``transposed_scale=True``."""
+    rows, k = a.shape
+    experts, wk, n = w.shape
+    if a.dtype != FP8 or w.dtype != FP8 or wk != k:
+        raise ValueError("gemm_kmajor takes e4m3 rows [A,K] and an e4m3 weight [E,K,N]")
+    _check(a_scale, (k // 128, rows), torch.float32, "row scales")
+    _check(w_scale, (experts, k // 128, n // 128), torch.float32, "weight scales")
+    _check(offsets, (experts + 1,), torch.int32, "offsets")
+    if not w.is_contiguous():
+        raise ValueError("gemm_kmajor: the weight must be contiguous")
+    device = _on_gpu(a, a_scale, w, w_scale, offsets)
+    out = torch.empty((rows, n), dtype=torch.bfloat16, device=device)
+    _timed(
+        "gemm_fp8_block", device, 2 * rows * n * k, rows * k + experts * n * k + 2 * rows * n,
+        "mi355x_gemm_fp8_block_kmajor", _ptr(a), _ptr(a_scale), rows, _ptr(w), _ptr(w_scale),
+        experts, n, k, _ptr(offsets), _ptr(out), _stream(device),
+    )
+    return out
+
+
 def rank_product(a, bt, offsets, *, splits=None):
     """``out[r] = a[r] @ bt[e]^T`` for the rows of each expert: bf16 ``[rows, R]``
     from bf16 ``a [rows, K]`` and ``bt [E, R, K]`` (``mi355x_rank_product``).

@@ -96,11 +96,11 @@ def _forward_gemm(aq, as_, weight, offsets, *, interleave=False):
 
 
 def _input_gradient_gemm(aq, as_, weight, offsets):
-    """``rows @ W`` through the weight's transposed copy."""
+    """``rows @ W`` through the weight's transposed copy (per-row FP8), or, for
+    block FP8, as :func:`fused.input_gradient_gemm` chooses."""
     if getattr(weight, "current", False):
         return kernels.gemm_rowwise(aq, as_, weight[1], weight[3], offsets)
-    return kernels.gemm(aq, as_, fused._transposed(weight, weight[0]), weight[1], offsets,
-                        transposed_scale=True)
+    return fused.input_gradient_gemm(aq, as_, weight, offsets)
 
 
 def _grad_dtypes(weight_grad_dtype, router_weight=None):
@@ -438,7 +438,7 @@ def _container_rule(cls, func, types, args, kwargs):
         if block is not None:
             args[index] = block[0]
             components.append(block[1])
-            transposed = (fused.transposed_data(value) if backward
+            transposed = (fused.available_transposed(value) if backward
                           else getattr(value, "_transposed", None))
             if transposed is not None:
                 components.append(transposed)

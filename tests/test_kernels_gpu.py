@@ -312,6 +312,32 @@ def test_grouped_gemm_matches_fp64(device, case):
     assert worst_cell_rel(out, want, offsets.tolist()) < 1e-2
 
 
+@pytest.mark.parametrize("counts,k,n", [
+    (COUNTS, 512, 256),                      # empty expert, partial row tiles
+    ([300, 0, 520, 45], 1536, 2048),         # C3's input gradient through W13 (K = 2I)
+    ([129, 64, 257], 2048, 768),             # C3's input gradient through W2 (N = I)
+    ([40, 700], 14336, 4096),                # Mixtral's K, the large-weight tile order
+])
+def test_grouped_gemm_kmajor_matches_transposed_copy(device, counts, k, n):
+    """The input-gradient GEMM on the weight as stored ([E, K, N], fragments
+    through ds_read_b64_tr_b8) is bitwise the GEMM on its transposed copy
+    (same products, same MFMA K grouping), including extreme block scales and
+    a zero block."""
+    g = torch.Generator().manual_seed(k + n + sum(counts))
+    offsets = _ragged(counts)
+    rows, experts = int(offsets[-1]), len(counts)
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16).to(device)
+    w = (torch.randn(experts, k, n, generator=g) * 0.02)
+    w[0, :128, :128] *= 2.0 ** 12
+    w[-1, 128:256, :128] = 0.0
+    xq, xs = K.quantize_rows(x)
+    wq, ws, wt = K.quantize_weight_blocks(w.to(device), transposed=True)
+    off = offsets.to(device)
+    want = K.gemm(xq, xs, wt, ws, off, transposed_scale=True)
+    got = K.gemm_kmajor(xq, xs, wq, ws, off)
+    assert torch.equal(got, want)
+
+
 def test_grouped_gemm_baseline_config2_sampled(device):
     """The BASELINE single-GEMM config (E=8, K=4096, N=2048, M_e ~ U{256..4096}
     step 128), checked per expert on sampled rows against fp64."""
