@@ -195,6 +195,7 @@ def backward_routed(
     grad_output, grad_aux, grad_probability_sum, h2, router_weight, w13, w2, logits,
     route_weights, route_ids, order, offsets, slots, h13, *, top_k, routing_mode, lengths,
     weight_grad_dtype, swiglu_limit=None, need_router=True, need_w13=True, need_w2=True,
+    need_residual=True,
 ):
     """VJPs ``(h2, residual, router_weight, w13, w2)`` with fp32 sums; the
     expert weights' gradients at ``weight_grad_dtype`` (bf16, the containers'
@@ -254,8 +255,8 @@ def backward_routed(
             grad_aux, grad_probability_sum, top_k=top_k, routing_mode=routing_mode,
             lengths=lengths, router_dtype=router_dtype, need_router=need_router,
         )
-    return (grad_h2.reshape(h2.shape).to(h2.dtype), grad_output.clone(), grad_router, grad_w13,
-            grad_w2)
+    grad_residual = grad_output.clone() if need_residual else grad_output.new_empty(0)
+    return (grad_h2.reshape(h2.shape).to(h2.dtype), grad_residual, grad_router, grad_w13, grad_w2)
 
 
 def routing_backward(grad_h2, x, router_weight, logits, route_weights, route_ids, dscore, slots,
@@ -419,7 +420,8 @@ def _backward_op(
     route_ids: torch.Tensor, order: torch.Tensor, offsets: torch.Tensor, slots: torch.Tensor,
     h13: torch.Tensor, top_k: int, routing_mode: str, lengths: list[int],
     weight_grad_dtype: torch.dtype | None, swiglu_limit: float | None, need_router: bool,
-    need_w13: bool, need_w2: bool, weight_components: list[torch.Tensor],
+    need_w13: bool, need_w2: bool, need_residual: bool,
+    weight_components: list[torch.Tensor],
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     w13, w2 = _split(w13_experts, w2_experts, weight_components)
     return backward_routed(
@@ -427,7 +429,7 @@ def _backward_op(
         route_weights, route_ids, order, offsets, slots, h13, top_k=top_k,
         routing_mode=routing_mode, lengths=lengths,
         weight_grad_dtype=weight_grad_dtype, swiglu_limit=swiglu_limit, need_router=need_router,
-        need_w13=need_w13, need_w2=need_w2,
+        need_w13=need_w13, need_w2=need_w2, need_residual=need_residual,
     )
 
 
@@ -435,12 +437,12 @@ def _backward_op(
 def _backward_fake(grad_output, grad_aux, grad_probability_sum, h2, router_weight, w13_experts,
                    w2_experts, logits, route_weights, route_ids, order, offsets, slots, h13,
                    top_k, routing_mode, lengths, weight_grad_dtype, swiglu_limit, need_router,
-                   need_w13, need_w2, weight_components):
+                   need_w13, need_w2, need_residual, weight_components):
     grad_dtype = torch.bfloat16 if weight_grad_dtype is None else weight_grad_dtype
     router_dtype = router_weight.dtype if weight_grad_dtype is None else weight_grad_dtype
     return (
         torch.empty_like(h2),
-        torch.empty_like(grad_output),
+        torch.empty_like(grad_output) if need_residual else grad_output.new_empty(0),
         torch.empty(router_weight.shape, dtype=router_dtype, device=h2.device)
         if need_router else skipped_gradient(router_weight, router_dtype),
         torch.empty(w13_experts.shape, dtype=grad_dtype, device=h2.device)
@@ -526,9 +528,13 @@ def _autograd_backward(ctx, grad_output, grad_aux, _g_counts, grad_probability_s
     grads = _backward_op(
         grad_output.contiguous(), grad_aux, grad_probability_sum, *saved[:11], ctx.top_k,
         ctx.routing_mode, ctx.lengths, ctx.weight_grad_dtype, ctx.swiglu_limit, bool(needs[2]),
-        bool(needs[3]), bool(needs[4]), components,
+        bool(needs[3]), bool(needs[4]), False, components,
     )
-    grad_h2, grad_residual, grad_router, grad_w13, grad_w2 = grads
+    grad_h2, _, grad_router, grad_w13, grad_w2 = grads
+    # d residual is the incoming cotangent itself; the operator returns an
+    # empty placeholder here rather than a copy (a custom operator's outputs
+    # may not alias its inputs).
+    grad_residual = grad_output if needs[1] else None
     return (grad_h2, grad_residual, grad_router if needs[2] else None,
             grad_w13 if needs[3] else None, grad_w2 if needs[4] else None, *([None] * 10),
             [None] * ctx.n_components)

@@ -40,11 +40,13 @@ def _inputs(device, tokens=256, hidden=512, experts=8, inter=1024, seed=0, std=0
 
 def _run(x, res, wr, w13, w2, dy, **kw):
     x = x.clone().requires_grad_(True)
+    res = res.clone().requires_grad_(True)
     wr = wr.clone().requires_grad_(True)
     w13c = BlockFP8Weight.quantize(w13).detach().requires_grad_(True)
     w2c = BlockFP8Weight.quantize(w2).detach().requires_grad_(True)
     out, aux, counts, psum = mlops_amd.moe(x, res, wr, w13c, w2c, **kw)
     torch.autograd.backward([out, aux], [dy, torch.ones_like(aux) * 0.1])
+    assert torch.equal(res.grad, dy)  # d residual is the output cotangent
     return dict(out=out.detach(), aux=aux.detach(), counts=counts, psum=psum.detach(),
                 gx=x.grad, gr=wr.grad, g13=w13c.grad, g2=w2c.grad, w13c=w13c, w2c=w2c)
 
@@ -190,8 +192,15 @@ def test_opcheck_forward_op(device):
     (out, aux, counts, psum, logits, weights, ids, order, offsets, slots, h13) = outs
     bargs = (dy, torch.zeros((), device=device), torch.zeros_like(psum), x, wr, w13q, w2q, logits,
              weights, ids, order, offsets, slots, h13, 2, "topk_then_softmax", [32], None, None,
-             True, True, True, [w13s, w2s])
+             True, True, True, True, [w13s, w2s])
     torch.library.opcheck(bwd, bargs, test_utils=("test_faketensor",))
+    # The autograd path asks for no residual copy: an empty placeholder.
+    quiet = bargs[:-2] + (False, bargs[-1])
+    torch.library.opcheck(bwd, quiet, test_utils=("test_faketensor",))
+    full, empty = bwd(*bargs), bwd(*quiet)
+    assert torch.equal(full[1], dy) and empty[1].numel() == 0
+    for u, v in zip(full[:1] + full[2:], empty[:1] + empty[2:]):
+        assert torch.equal(u, v)
 
 
 def test_qwen3_shape_properties(device):
