@@ -94,6 +94,17 @@ int mi355x_router_topk_bwd_split(const float* logits, const float* weights, cons
                                  const int32_t* seg_counts, float* grad_logits, void* pieces,
                                  void* stream);
 
+/* Router weight gradient from those pieces: grad_weight fp32 [E, H] =
+ * hi^T x + mid^T x with fp32 sums, x bf16 [T, H], on the bf16 MFMA over
+ * token ranges whose partials are summed in range order (deterministic).
+ * E a multiple of 8, H a multiple of 256; workspace of
+ * mi355x_router_weight_grad_workspace_size bytes. Replaces the two products
+ * of router_weight_gradient (kernels/router.py:91-110). */
+size_t mi355x_router_weight_grad_workspace_size(int tokens, int experts, int hidden);
+int mi355x_router_weight_grad(const void* pieces, const void* x, int tokens, int experts,
+                              int hidden, float* grad_weight, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 /* ----------------------------------------------------------- permute ---- */
 
 /* Stable counting sort of the flat expert ids [A] into expert order.

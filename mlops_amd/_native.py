@@ -36,6 +36,8 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _P, _P, _P, _P, _P],
     ),
+    "mi355x_router_weight_grad_workspace_size": (_S, [_I, _I, _I]),
+    "mi355x_router_weight_grad": (_I, [_P, _P, _I, _I, _I, _P, _P, _S, _P]),
     "mi355x_permute_plan_workspace_size": (_S, [_I, _I]),
     "mi355x_permute_plan": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _S, _P]),
     "mi355x_permute_plan_noalloc_max_assignments": (_S, [_I]),

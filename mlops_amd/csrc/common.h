@@ -233,8 +233,8 @@ __device__ inline void padded_block_prefix(const int32_t* __restrict__ offsets, 
 // (lane i <-> 7 - i) and the row mirror (i <-> 15 - i), each pairing two
 // partial results that cover disjoint lanes; every lane adds the same two
 // values, so all lanes of the group hold the same sum. Wider groups finish
-// with lane shuffles. A source lane that is not active returns the `old`
-// operand: the lane's own value for max, 0 for sums.
+// with lane shuffles. A source lane that is not active returns the lane's
+// own value for max and 0 for sums.
 template <int kCtrl>
 __device__ __forceinline__ float dpp_max_step(float v) {
   const int b = __float_as_int(v);
@@ -243,7 +243,7 @@ __device__ __forceinline__ float dpp_max_step(float v) {
 template <int kCtrl>
 __device__ __forceinline__ float dpp_sum_step(float v) {
   return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF,
-                                                        false));
+                                                        true));
 }
 template <int W>
 __device__ __forceinline__ float group_max(float v) {

@@ -236,6 +236,29 @@ def router_backward(
     return grad
 
 
+def router_weight_grad(pieces: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """fp32 ``[E, H]`` = ``hi^T x + mid^T x`` from the bf16 pieces ``[T, 2E]``
+    (``hi | mid``) and the bf16 hidden state ``x [T, H]``."""
+    if pieces.dtype != torch.bfloat16 or x.dtype != torch.bfloat16:
+        raise ValueError("router_weight_grad takes bf16 pieces and hidden state")
+    device = _on_gpu(pieces, x)
+    tokens, hidden = x.shape
+    experts = pieces.shape[1] // 2
+    if pieces.shape != (tokens, 2 * experts):
+        raise ValueError("pieces must be [T, 2E] beside x [T, H]")
+    pieces, x = pieces.contiguous(), x.contiguous()
+    out = torch.empty((experts, hidden), dtype=torch.float32, device=device)
+    size = _native.query("mi355x_router_weight_grad_workspace_size", tokens, experts, hidden)
+    ws = torch.empty(max(size, 4), dtype=torch.uint8, device=device)
+    flops = 4 * tokens * experts * hidden
+    # x and the pieces read once, the fp32 gradient written
+    nbytes = 2 * tokens * hidden + 4 * tokens * experts + 4 * experts * hidden
+    _timed("router_weight_grad", device, flops, nbytes, "mi355x_router_weight_grad",
+           _ptr(pieces), _ptr(x), tokens, experts, hidden, _ptr(out), _ptr(ws), size,
+           _stream(device))
+    return out
+
+
 # ----------------------------------------------------------------- permute
 def permute_plan(ids: torch.Tensor, experts: int):
     """``(counts int64 [E], offsets int32 [E+1], order int32 [A], slots int32 [T,k])``."""

@@ -33,7 +33,8 @@ def _zipf_ids(tokens, top_k, experts, s, seed):
 
 # ------------------------------------------------------------------ router
 @pytest.mark.parametrize("mode", ["topk_then_softmax", "softmax_then_topk", "sigmoid_noaux_tc"])
-@pytest.mark.parametrize("experts,top_k", [(128, 8), (8, 2), (300, 6), (256, 8), (512, 32), (64, 1)])
+@pytest.mark.parametrize("experts,top_k", [(128, 8), (8, 2), (300, 6), (256, 8), (512, 32), (64, 1),
+                                            (128, 16), (128, 17), (16, 16), (100, 3)])
 def test_router_topk_matches_oracle(device, mode, experts, top_k):
     g = torch.Generator().manual_seed(experts + top_k)
     logits = torch.randn(1000, experts, generator=g)
@@ -43,6 +44,25 @@ def test_router_topk_matches_oracle(device, mode, experts, top_k):
     ow, oids = O.route(logits, top_k, mode, routed_scaling=1.3)
     assert torch.equal(ids.cpu(), oids)
     assert max_rel(w.cpu(), ow) < 1e-5
+
+
+@pytest.mark.parametrize("mode", ["topk_then_softmax", "sigmoid_noaux_tc"])
+@pytest.mark.parametrize("experts,top_k", [(128, 8), (300, 6)])
+def test_router_topk_nan_and_signed_zero(device, mode, experts, top_k):
+    """torch.sort's order on the awkward values: NaN ahead of every number,
+    -0 equal to +0 (ties to the lower id), -inf last among numbers."""
+    g = torch.Generator().manual_seed(5)
+    logits = torch.randn(64, experts, generator=g)
+    logits[0, 7] = float("nan")
+    logits[1, [3, 9]] = float("nan")
+    logits[2] = float("-inf")
+    logits[2, 11] = 0.5
+    logits[3] = 0.0
+    logits[3, ::2] = -0.0
+    logits[4, : experts - 2] = float("-inf")
+    _, ids = K.router_topk(logits.to(device), top_k, mode)
+    _, oids = O.route(logits, top_k, mode)
+    assert torch.equal(ids.cpu(), oids)
 
 
 def test_router_topk_group_limited(device):
@@ -114,6 +134,36 @@ def test_router_stats_and_backward(device, mode, lengths, experts, top_k):
     hi = grad.cpu().to(torch.bfloat16)
     assert torch.equal(pieces[:, :experts], hi)
     assert torch.equal(pieces[:, experts:], (grad.cpu() - hi.float()).to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("tokens,experts,hidden", [
+    (16384, 128, 2048),   # C3's router
+    (1000, 32, 256),      # ragged last step
+    (37, 8, 512),         # one step, most expert rows masked
+    (700, 200, 768),      # E not a multiple of the 128-row tile
+    (513, 256, 256),      # two expert tiles
+    (0, 16, 256),         # no tokens: zeros
+])
+def test_router_weight_grad_matches_fp64(device, tokens, experts, hidden):
+    """dW = hi^T x + mid^T x (bf16 pieces, fp32 sums) against fp64 on the same
+    bf16 operands, and equal to the pieces' fp32 cotangent within the bf16
+    split's resolution."""
+    g = torch.Generator().manual_seed(tokens + experts)
+    grad = torch.randn(tokens, experts, generator=g) * 1e-3
+    hi = grad.to(torch.bfloat16)
+    mid = (grad - hi.float()).to(torch.bfloat16)
+    pieces = torch.cat([hi, mid], 1)
+    x = torch.randn(tokens, hidden, generator=g).to(torch.bfloat16)
+    got = K.router_weight_grad(pieces.to(device), x.to(device)).cpu()
+    want = hi.double().t() @ x.double() + mid.double().t() @ x.double()
+    assert got.dtype == torch.float32 and got.shape == (experts, hidden)
+    if tokens == 0:
+        assert torch.count_nonzero(got) == 0
+        return
+    assert (got.double() - want).abs().max() <= 1e-5 * want.abs().max()
+    # the split carries the fp32 cotangent to ~2^-16 relative
+    exact = grad.double().t() @ x.double()
+    assert (got.double() - exact).abs().max() <= 1e-4 * exact.abs().max()
 
 
 # ------------------------------------------------------------------ permute
