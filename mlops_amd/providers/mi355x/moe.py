@@ -265,7 +265,12 @@ def routing_backward(grad_h2, x, router_weight, logits, route_weights, route_ids
     """Score gradient ``dscore`` (per sorted row) and the aux / probability-sum
     cotangents through the router: returns the router weight's gradient (a
     placeholder when not needed) and adds the router's input gradient to
-    ``grad_h2`` in place."""
+    ``grad_h2`` in place. An empty ``grad_aux`` / ``grad_probability_sum``
+    stands for a zero cotangent."""
+    if grad_aux is not None and grad_aux.numel() == 0:
+        grad_aux = None
+    if grad_probability_sum is not None and grad_probability_sum.numel() == 0:
+        grad_probability_sum = None
     seg_offsets = seg_counts = None
     if routing_mode == "sigmoid_noaux_tc" and grad_aux is not None:
         _, _, seg_counts, seg_offsets = kernels.router_stats(
@@ -517,11 +522,12 @@ def _autograd_backward(ctx, grad_output, grad_aux, _g_counts, grad_probability_s
     saved = ctx.saved_tensors
     h2, router_weight = saved[:2]
     components = list(saved[11:])
+    # An absent cotangent travels as an empty tensor (no fill kernel); the
+    # router backward then treats it as zero.
     if grad_aux is None:
-        grad_aux = torch.zeros((), dtype=torch.float32, device=h2.device)
+        grad_aux = torch.empty(0, dtype=torch.float32, device=h2.device)
     if grad_probability_sum is None:
-        grad_probability_sum = torch.zeros(router_weight.shape[0], dtype=torch.float32,
-                                           device=h2.device)
+        grad_probability_sum = torch.empty(0, dtype=torch.float32, device=h2.device)
     if grad_output is None:
         grad_output = torch.zeros_like(h2)
     needs = ctx.needs_input_grad

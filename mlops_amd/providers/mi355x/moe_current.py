@@ -297,11 +297,12 @@ def _autograd_backward(ctx, grad_output, grad_aux, _g_counts, grad_probability_s
     saved = ctx.saved_tensors
     h2, router_weight = saved[:2]
     components = list(saved[11:])
+    # An absent cotangent travels as an empty tensor (no fill kernel); the
+    # router backward then treats it as zero.
     if grad_aux is None:
-        grad_aux = torch.zeros((), dtype=torch.float32, device=h2.device)
+        grad_aux = torch.empty(0, dtype=torch.float32, device=h2.device)
     if grad_probability_sum is None:
-        grad_probability_sum = torch.zeros(router_weight.shape[0], dtype=torch.float32,
-                                           device=h2.device)
+        grad_probability_sum = torch.empty(0, dtype=torch.float32, device=h2.device)
     if grad_output is None:
         grad_output = torch.zeros_like(h2)
     needs = ctx.needs_input_grad

@@ -69,12 +69,14 @@ def router_weight_gradient_from_pieces(pieces, hidden, dtype) -> torch.Tensor:
     """:func:`router_weight_gradient` from the cotangent already split into
     its bf16 ``[hi | mid]`` pieces ``[T, 2E]`` (the router backward kernel
     writes them): ``hi^T x + mid^T x`` with fp32 sums. On the MI355X kernel
-    (``mi355x_router_weight_grad``) when E is a multiple of 8 and H of 256;
-    other widths use the split-K product on hipBLASLt."""
+    (``mi355x_router_weight_grad``, 128-expert tiles) when E is a multiple of
+    8 from 64 up and H a multiple of 256; fewer experts would leave most of
+    its tile idle, and those and other widths use the split-K product on
+    hipBLASLt."""
     experts = pieces.shape[1] // 2
     hidden = hidden.reshape(-1, hidden.shape[-1])
     if (pieces.is_cuda and hidden.dtype == torch.bfloat16 and experts % 8 == 0
-            and hidden.shape[1] % 256 == 0):
+            and experts >= 64 and hidden.shape[1] % 256 == 0):
         from . import kernels
 
         return kernels.router_weight_grad(pieces, hidden).to(dtype)
