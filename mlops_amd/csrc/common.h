@@ -82,7 +82,7 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 // round-to-nearest-even, matching torch's cast for finite inputs in range.
 // Returns the two bytes in the low 16 bits (lo first).
 __device__ __forceinline__ uint32_t f32x2_to_e4m3(float lo, float hi) {
-  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(lo, hi, 0, false) & 0xffffu;
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(lo, hi, __float_as_int(lo), false) & 0xffffu;
 }
 
 // Four values divided by a power-of-two descale and encoded e4m3 by gfx950's
@@ -94,13 +94,18 @@ __device__ __forceinline__ uint32_t f32x2_to_e4m3(float lo, float hi) {
 typedef short v2i16_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t f32x4_to_e4m3_pow2(float a, float b, float c, float d,
                                                       float scale) {
-  v2i16_t w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32((v2i16_t){0, 0}, a, b, scale, false);
+  // The first conversion writes the low half and the second the high half,
+  // so the destination's prior contents never matter: it starts as a's bits
+  // (a register the first conversion can take over, where a zero would need
+  // a move).
+  v2i16_t w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(
+      __builtin_bit_cast(v2i16_t, a), a, b, scale, false);
   w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, c, d, scale, true);
   return __builtin_bit_cast(uint32_t, w);
 }
 
 __device__ __forceinline__ uint32_t f32x4_to_e4m3(float a, float b, float c, float d) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __float_as_int(a), false);  // see above
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return (uint32_t)w;
 }
@@ -266,6 +271,33 @@ __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
   for (int o = 16; o < W; o <<= 1) v += __shfl_xor(v, o, 64);
   return v;
+}
+
+// Maximum of non-negative, non-NaN floats (the block amax values of the
+// quantizers, each a running fmaxf from 0) over aligned groups of W lanes.
+// Such floats order like their bit patterns as unsigned integers, so each
+// DPP step fuses into one v_max_u32 (an fmaxf step needs a copy and a
+// canonicalizing max besides); a source lane that is not active reads as 0,
+// the identity. W = 64 combines the four rows' results as scalars.
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_umax_step(uint32_t v) {
+  return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, 0xF, 0xF, true));
+}
+template <int W>
+__device__ __forceinline__ float group_amax(float x) {
+  static_assert(W >= 2 && W <= 64 && (W & (W - 1)) == 0, "group width");
+  uint32_t v = __float_as_uint(x);
+  v = dpp_umax_step<0xB1>(v);
+  if constexpr (W >= 4) v = dpp_umax_step<0x4E>(v);
+  if constexpr (W >= 8) v = dpp_umax_step<0x141>(v);
+  if constexpr (W >= 16) v = dpp_umax_step<0x140>(v);
+  if constexpr (W == 32) v = max(v, (uint32_t)__shfl_xor((int)v, 16, 64));
+  if constexpr (W == 64) {
+    const uint32_t r0 = __builtin_amdgcn_readlane((int)v, 0), r1 = __builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t r2 = __builtin_amdgcn_readlane((int)v, 32), r3 = __builtin_amdgcn_readlane((int)v, 48);
+    v = max(max(r0, r1), max(r2, r3));
+  }
+  return __uint_as_float(v);
 }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }

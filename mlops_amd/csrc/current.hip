@@ -56,7 +56,7 @@ __global__ void __launch_bounds__(256) rows_current_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
   }
-  amax = wave_max(amax);
+  amax = group_amax<64>(amax);
   const float s = fmaxf(amax * kInv448, kMinScale);
   uint8_t* dst = q + (size_t)r * width;
   // Four chunks' loads before their stores: loads and stores complete in
@@ -92,7 +92,7 @@ __global__ void __launch_bounds__(256) permute_rows_current_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
   }
-  amax = wave_max(amax);
+  amax = group_amax<64>(amax);
   const float s = fmaxf(amax * kInv448, kMinScale);
   // The token's slots in registers (read before any store), then four
   // chunks' loads before their stores.
@@ -151,7 +151,7 @@ __global__ void __launch_bounds__(256) swiglu_rows_current_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(act[i]));
   }
-  amax = wave_max(amax);
+  amax = group_amax<64>(amax);
   const float s = fmaxf(amax * kInv448, kMinScale);
   uint8_t* dst = q + (size_t)r * width;
   // Four chunks' loads before their stores (loads and stores complete in

@@ -444,7 +444,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
                 act[ii][r][m] = silu_f(g) * u;
                 pmax = fmaxf(pmax, fabsf(act[ii][r][m]));
               }
-              pmax = group_max<16>(pmax);  // the 16 lanes of this row: 64 columns
+              pmax = group_amax<16>(pmax);  // the 16 lanes of this row: 64 columns
               if ((elane & 15) == 0) act_amax[wn][wm * 64 + lrow] = pmax;
             }
           }

@@ -186,7 +186,7 @@ __global__ void __launch_bounds__(256) permute_quantize_kernel(
       float amax = 0.0f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
-      amax = group_max<8>(amax);
+      amax = group_amax<8>(amax);
       const float s = fmaxf(amax * kInv448, kMinScale);
       const uint2 lo = quant8(v, s), hi = quant8(v + 8, s);
       const uint4 packed = make_uint4(lo.x, lo.y, hi.x, hi.y);

@@ -44,7 +44,7 @@ __global__ void __launch_bounds__(256) weight_blocks_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[p][i]));
   }
-  amax = wave_max(amax);
+  amax = group_amax<64>(amax);
   if (lane_id() == 0) red[threadIdx.x >> 6] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -137,7 +137,7 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __re
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-        amax = group_max<16>(amax);
+        amax = group_amax<16>(amax);
         const float s = fmaxf(amax * kInv448, kMinScale);
         const uint2 packed = quant8(v, s);
         if (col < width) {
@@ -178,8 +178,8 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __re
         ga = fmaxf(ga, fabsf(g[i]));
         ua = fmaxf(ua, fabsf(u[i]));
       }
-      ga = group_max<16>(ga);
-      ua = group_max<16>(ua);
+      ga = group_amax<16>(ga);
+      ua = group_amax<16>(ua);
       const float sg = fmaxf(ga * kInv448, kMinScale), su = fmaxf(ua * kInv448, kMinScale);
       const uint2 pg = quant8(g, sg), pu = quant8(u, su);
       if (j < half) {
@@ -260,7 +260,7 @@ __global__ void __launch_bounds__(256) swiglu_quantize_kernel(const uint16_t* __
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(act[i]));
-    amax = group_max<16>(amax);
+    amax = group_amax<16>(amax);
     const float sc = fmaxf(amax * kInv448, kMinScale);
     store_stream8(q + r * width + j, quant8(act, sc));
     if (lane16 == 0) scales[(size_t)grp * rows + r] = sc;
@@ -490,8 +490,8 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
             ga = fmaxf(ga, fabsf(gq[i]));
             ua = fmaxf(ua, fabsf(uq[i]));
           }
-          ga = group_max<16>(ga);
-          ua = group_max<16>(ua);
+          ga = group_amax<16>(ga);
+          ua = group_amax<16>(ua);
           const float sg = fmaxf(ga * kInv448, kMinScale), su = fmaxf(ua * kInv448, kMinScale);
           uint8_t* qrow = dhq + (size_t)row * 2 * width;
           *(uint2*)(qrow + j) = quant8(gq, sg);
@@ -639,8 +639,8 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
         ga = fmaxf(ga, fabsf(gq[i]));
         ua = fmaxf(ua, fabsf(uq[i]));
       }
-      ga = group_max<16>(ga);
-      ua = group_max<16>(ua);
+      ga = group_amax<16>(ga);
+      ua = group_amax<16>(ua);
       const float sg = fmaxf(ga * kInv448, kMinScale), su = fmaxf(ua * kInv448, kMinScale);
       *(uint2*)(dhq + (size_t)row * 2 * width + j) = quant8(gq, sg);
       *(uint2*)(dhq + (size_t)row * 2 * width + width + j) = quant8(uq, su);
