@@ -18,6 +18,7 @@ shape, timed on the host cores.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -387,6 +388,12 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # The ~270K Python objects alive by now (torch, the model inputs) move to
+    # the collector's permanent generation: a full collection would otherwise
+    # rescan them all, ~50 ms with the host thread (and so the GPU queue)
+    # stalled, once every few dozen steps. Nothing of a step is skipped.
+    gc.collect()
+    gc.freeze()
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -395,9 +402,8 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     # Per-kernel durations come from a second pass of the same K steps with a
-    # pair of HIP events around every launch, on the launch's stream. The
-    # events cost the step time itself (~20 us each: timestamped markers
-    # between dispatches), so they stay out of the pass that gives `value`.
+    # pair of HIP events around every launch, on the launch's stream, so that
+    # no marker sits inside the pass that gives `value`.
     timer = kernels.LaunchTimer()
     kernels.set_launch_timer(timer)
     torch.cuda.synchronize()
