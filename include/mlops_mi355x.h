@@ -294,6 +294,27 @@ int mi355x_gemm_fp8_block_kmajor(const uint8_t* a, const float* a_scale, int row
                                  const uint8_t* w, const float* w_scale, int experts, int n, int k,
                                  const int32_t* offsets, void* out, void* stream);
 
+/* mi355x_gemm_fp8_block / mi355x_gemm_fp8_block_kmajor whose GEMM row r
+ * (expert-sorted rows, offsets) is row a_rows[r] of a [a_total, K] e4m3 with
+ * 1x128 scales a_scale [K/128][a_total]: the activation (x forward, dy for
+ * r = dy @ W2) quantized once per token and read by each of its k routed
+ * rows, instead of a permuted copy of k rows per token. a_rows int32 [rows]
+ * (the token of each routed row). N a multiple of 256; no addend. Bitwise
+ * equal to the routed-row forms on mi355x_permute_quantize_fp8's copy.
+ * Replaces permute_quantize_rows followed by block_fp8_gemm /
+ * block_fp8_transposed_gemm (kernels/quack_moe/quantize_rows.py:35,
+ * block_fp8_gemm.py:1458 and :1424; the reference's GEMM takes no gather,
+ * block_fp8_gemm.py:392). */
+int mi355x_gemm_fp8_block_gathered(const uint8_t* a, const float* a_scale, int a_total,
+                                   const int32_t* a_rows, int rows, const uint8_t* w,
+                                   const float* w_scale, int experts, int n, int k,
+                                   const int32_t* offsets, int interleave, void* out,
+                                   void* stream);
+int mi355x_gemm_fp8_block_kmajor_gathered(const uint8_t* a, const float* a_scale, int a_total,
+                                          const int32_t* a_rows, int rows, const uint8_t* w,
+                                          const float* w_scale, int experts, int n, int k,
+                                          const int32_t* offsets, void* out, void* stream);
+
 /* mi355x_gemm_fp8_block with a rank-r term in place of the addend:
  *   out[r, n] = (block-FP8 product as above) + sum_j lora_z[r, j] * lora_b[e][n', j]
  * for rows r of expert e, where n' is the weight row feeding output column n

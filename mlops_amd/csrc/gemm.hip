@@ -402,10 +402,12 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
                           const float* w_scale, int w_scale_t, int experts, int n, int k,
                           const int32_t* offsets, int interleave, const void* addend, void* out,
                           uint8_t* act_q, float* act_scales, float limit, const void* lora_z,
-                          const void* lora_b, int lora_rank, void* stream);
+                          const void* lora_b, int lora_rank, void* stream,
+                          const int32_t* a_rows = nullptr, int a_total = 0);
 int mi355x_gemm_v2_kmajor_launch(const uint8_t* a, const float* a_scale, int rows,
                                  const uint8_t* w, const float* w_scale, int experts, int n, int k,
-                                 const int32_t* offsets, void* out, void* stream);
+                                 const int32_t* offsets, void* out, void* stream,
+                                 const int32_t* a_rows = nullptr, int a_total = 0);
 
 int mi355x_gemm_v2_rowwise_launch(const uint8_t* a, const float* a_scale, int rows,
                                   const uint8_t* w, const float* w_scale, int experts, int n,
@@ -456,6 +458,62 @@ extern "C" int mi355x_gemm_fp8_block_kmajor(const uint8_t* a, const float* a_sca
   if (rows == 0) return MI355X_OK;
   const int v2 = mi355x_gemm_v2_kmajor_launch(a, a_scale, rows, w, w_scale, experts, n, k, offsets,
                                               out, stream);
+  if (v2 < 0) return v2;
+  MI355X_REQUIRE(v2 == 0, "gemm_kmajor: shape outside the pipelined kernel");
+  return MI355X_OK;
+}
+
+// Gathered-A forms: GEMM row r (expert-sorted, offsets) reads row
+// a_rows[r] of a [a_total, K] and its 1x128 scales a_scale[K/128][a_total]
+// (the activation quantized once per token; a_rows = the token of each
+// routed row). Pipelined kernel only (N a multiple of 256).
+static int gathered_checks(int a_total, const int32_t* a_rows, int rows, int k) {
+  MI355X_REQUIRE(a_rows != nullptr && a_total > 0, "gemm gathered: a_rows and a_total required");
+  MI355X_REQUIRE((uint64_t)a_total * (uint64_t)k < (1ull << 32),
+                 "gemm gathered: gathered rows beyond 32-bit offsets");
+  MI355X_REQUIRE(rows >= 0, "gemm gathered: negative rows");
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_gemm_fp8_block_gathered(const uint8_t* a, const float* a_scale, int a_total,
+                                              const int32_t* a_rows, int rows, const uint8_t* w,
+                                              const float* w_scale, int experts, int n, int k,
+                                              const int32_t* offsets, int interleave, void* out,
+                                              void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= kMaxExperts, "gemm: experts must be in [1, %d]",
+                 kMaxExperts);
+  MI355X_REQUIRE(n > 0 && n % 256 == 0, "gemm gathered: N must be a multiple of 256, got %d", n);
+  MI355X_REQUIRE(k > 0 && k % BK == 0, "gemm: K must be a multiple of %d, got %d", BK, k);
+  MI355X_REQUIRE(!interleave || (n / 2) % 128 == 0,
+                 "gemm gathered: a gate/up weight needs halves that are multiples of 128");
+  const int c = gathered_checks(a_total, a_rows, rows, k);
+  if (c != MI355X_OK) return c;
+  if (rows == 0) return MI355X_OK;
+  const int v2 = mi355x_gemm_v2_launch(a, a_scale, rows, w, w_scale, 0, experts, n, k, offsets,
+                                       interleave, nullptr, out, nullptr, nullptr, 0.0f, nullptr,
+                                       nullptr, 0, stream, a_rows, a_total);
+  if (v2 < 0) return v2;
+  MI355X_REQUIRE(v2 == 0, "gemm gathered: shape outside the pipelined kernel");
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_gemm_fp8_block_kmajor_gathered(const uint8_t* a, const float* a_scale,
+                                                     int a_total, const int32_t* a_rows, int rows,
+                                                     const uint8_t* w, const float* w_scale,
+                                                     int experts, int n, int k,
+                                                     const int32_t* offsets, void* out,
+                                                     void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= kMaxExperts,
+                 "gemm_kmajor: experts must be in [1, %d]", kMaxExperts);
+  MI355X_REQUIRE(n > 0 && n % 256 == 0, "gemm_kmajor: N must be a multiple of 256, got %d", n);
+  MI355X_REQUIRE(k > 0 && k % BK == 0, "gemm_kmajor: K must be a multiple of %d, got %d", BK, k);
+  MI355X_REQUIRE((uint64_t)(k - 1) * (uint64_t)n + 256 < (1ull << 32),
+                 "gemm_kmajor: a weight slice beyond 32-bit offsets");
+  const int c = gathered_checks(a_total, a_rows, rows, k);
+  if (c != MI355X_OK) return c;
+  if (rows == 0) return MI355X_OK;
+  const int v2 = mi355x_gemm_v2_kmajor_launch(a, a_scale, rows, w, w_scale, experts, n, k, offsets,
+                                              out, stream, a_rows, a_total);
   if (v2 < 0) return v2;
   MI355X_REQUIRE(v2 == 0, "gemm_kmajor: shape outside the pipelined kernel");
   return MI355X_OK;

@@ -13,6 +13,7 @@ constexpr int kMaxExperts = 512;
 struct Tile {
   int e, row0, nvalid, nt;
   int rot;  // K-step rotation: the tile walks K steps rot, rot + 1, ... (mod nk)
+  int par;  // which of the two gathered-row tables holds this tile's A rows
 };
 
 __device__ __forceinline__ Tile describe(const int* prefix, const int32_t* __restrict__ offsets,
@@ -51,6 +52,7 @@ __device__ __forceinline__ Tile describe(const int* prefix, const int32_t* __res
   // grouped order runs unrotated: there the CUs sharing a panel read it
   // together.
   t.rot = rotate ? __builtin_amdgcn_readfirstlane(nk >= 8 ? tile % 3 : (tile * 7) % nk) : 0;
+  t.par = 0;
   return t;
 }
 
@@ -79,7 +81,8 @@ typedef short v4s __attribute__((ext_vector_type(4)));
 // 128 K rows of 256 bytes and the B fragments read with ds_read_b64_tr_b8;
 // the MFMA columns are then the tile's columns in order, so the epilogue
 // regroups each row's values through LDS into 8-column stores.
-template <bool kAct, bool kAdd, bool kLora, bool kRow = false, bool kKM = false>
+template <bool kAct, bool kAdd, bool kLora, bool kRow = false, bool kKM = false,
+          bool kGather = false>
 __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     const uint8_t* __restrict__ a, const float* __restrict__ a_scale, int rows,
     const uint8_t* __restrict__ w, const float* __restrict__ w_scale, int w_scale_t, int experts,
@@ -87,11 +90,16 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     const uint16_t* __restrict__ addend, uint16_t* __restrict__ out,
     uint8_t* __restrict__ act_q, float* __restrict__ act_scales, float limit,
     const uint16_t* __restrict__ lora_z, const uint16_t* __restrict__ lora_b, int lora_rank,
-    int n_group, int rotate) {
+    int n_group, int rotate, const int32_t* __restrict__ a_rows, int scale_pitch) {
   __shared__ __align__(1024) uint8_t smem[kStages * STAGE_BYTES];
   __shared__ float act_amax[2][BM];  // per-row amax of each wave column's 64 act columns
   __shared__ int prefix[kMaxExperts + 1];
   __shared__ int tmp[kThreads];
+  // Gathered A (a_rows non-null): GEMM row r reads a[a_rows[r]] and its
+  // scales a_scale[kb * scale_pitch + a_rows[r]]: the activation quantized
+  // once per token, each token row read by its k routed rows. A tile's 256
+  // source rows are copied into one of two tables one tile ahead.
+  __shared__ int gtok[2][BM];
   tile_prefix(offsets, experts, BM, prefix, tmp);
   const int n_tiles = N / BN;
   const int total = __builtin_amdgcn_readfirstlane(prefix[experts]) * n_tiles;
@@ -119,7 +127,10 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
       const int r = (wave * A_LOADS + i) * 8 + (lane >> 3);
-      const uint32_t off = (uint32_t)min(t.row0 + r, rows - 1) * (uint32_t)K + 16 * ((lane & 7) ^ swz(r));
+      int src;
+      if constexpr (kGather) src = gtok[t.par][r];
+      else src = min(t.row0 + r, rows - 1);
+      const uint32_t off = (uint32_t)src * (uint32_t)K + 16 * ((lane & 7) ^ swz(r));
       dma16(abase, off, base + (wave * A_LOADS + i) * 1024);
     }
     if constexpr (kKM) {
@@ -142,10 +153,12 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       }
     }
     if constexpr (kRow) return;  // no per-step scales
-    const float* sbase = a_scale + (size_t)kb * rows;
+    const float* sbase = a_scale + (size_t)kb * (kGather ? scale_pitch : rows);
     if (lane < 32) {
-      const uint32_t off = 4u * (uint32_t)min(t.row0 + wave * 32 + lane, rows - 1);
-      dma4(sbase, off, base + A_BYTES + B_BYTES + wave * 128);
+      int src;
+      if constexpr (kGather) src = gtok[t.par][wave * 32 + (lane & 31)];
+      else src = min(t.row0 + wave * 32 + lane, rows - 1);
+      dma4(sbase, 4u * (uint32_t)src, base + A_BYTES + B_BYTES + wave * 128);
     }
     // The wave's two weight block scales (its columns' low and high 128-column
     // blocks) into the stage as well: an ordinary load here would make the
@@ -179,6 +192,18 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
   int tile = tile_at(0);
   if (tile >= total) return;
   Tile ct = describe(prefix, offsets, experts, n_tiles, tile, nk, n_group, rotate);
+  // Gathered A: the tile's 256 source rows (row indices clamped to the last
+  // row, as the plain copies clamp) into table `par`, by the first four waves'
+  // direct loads; they land before the next wait_and_sync<0> returns.
+  auto load_rows = [&](const Tile& t, int par) {
+    if (kGather && wave < 4)
+      dma4(a_rows, 4u * (uint32_t)min(t.row0 + wave * 64 + lane, rows - 1),
+           (const uint8_t*)&gtok[par][wave * 64]);
+  };
+  if constexpr (kGather) {
+    load_rows(ct, 0);
+    wait_and_sync<0>();
+  }
   issue(ct, 0, 0);
   int stage = 0;
   for (;;) {
@@ -237,12 +262,21 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
 
     for (int kb = 0; kb < nk; ++kb) {
       wait_and_sync<0>();  // two stages: the only loads in flight are this step's
+      if (kGather && kb == 0 && next_tile < total) {
+        // The next tile's source rows, into the other table (its last reader,
+        // the tile before this one, finished before the barrier above). With
+        // a single K step they are needed right away.
+        load_rows(describe(prefix, offsets, experts, n_tiles, next_tile, nk, n_group, rotate),
+                  (round + 1) & 1);
+        if (nk == 1) wait_and_sync<0>();
+      }
       // Next step's operands (the next tile's first step at the last step:
       // its loads then run under this tile's epilogue).
       if (kb + 1 < nk) {
         issue(ct, kb + 1, stage ^ 1);
       } else if (next_tile < total) {
-        const Tile nt = describe(prefix, offsets, experts, n_tiles, next_tile, nk, n_group, rotate);
+        Tile nt = describe(prefix, offsets, experts, n_tiles, next_tile, nk, n_group, rotate);
+        if constexpr (kGather) nt.par = (round + 1) & 1;
         issue(nt, 0, stage ^ 1);
       }
       const uint8_t* base = smem + stage * STAGE_BYTES;
@@ -477,6 +511,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     ++round;
     tile = next_tile;
     ct = describe(prefix, offsets, experts, n_tiles, tile, nk, n_group, rotate);
+    if constexpr (kGather) ct.par = round & 1;
   }
 }
 
@@ -521,7 +556,8 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
                           const float* w_scale, int w_scale_t, int experts, int n, int k,
                           const int32_t* offsets, int interleave, const void* addend, void* out,
                           uint8_t* act_q, float* act_scales, float limit, const void* lora_z,
-                          const void* lora_b, int lora_rank, void* stream) {
+                          const void* lora_b, int lora_rank, void* stream,
+                          const int32_t* a_rows, int a_total) {
   if (n % BN != 0 || experts > kMaxExperts || (interleave && (n / 2) % 128 != 0)) return 1;
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   const int grid = upper < cu_count() ? upper : cu_count();
@@ -531,9 +567,12 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
                        rows, w, w_scale, w_scale_t, experts, n, k, offsets, interleave,
                        (const uint16_t*)addend, (uint16_t*)out, act_q, act_scales, limit,
                        (const uint16_t*)lora_z, (const uint16_t*)lora_b, lora_rank,
-                       order.n_group, order.rotate);
+                       order.n_group, order.rotate, a_rows, a_rows != nullptr ? a_total : rows);
   };
-  if (lora_z != nullptr) {
+  if (a_rows != nullptr) {
+    if (lora_z != nullptr || act_q != nullptr || addend != nullptr) return 1;
+    launch(grouped_gemm_v2_kernel<false, false, false, false, false, true>);
+  } else if (lora_z != nullptr) {
     if (act_q != nullptr || addend != nullptr) return 1;  // not a form of this kernel
     launch(grouped_gemm_v2_kernel<false, false, true>);
   } else if (act_q != nullptr) {
@@ -551,16 +590,21 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
 // [E, K/128, N/128]; returns 1 if the shape is not this kernel's (N % 256).
 int mi355x_gemm_v2_kmajor_launch(const uint8_t* a, const float* a_scale, int rows,
                                  const uint8_t* w, const float* w_scale, int experts, int n, int k,
-                                 const int32_t* offsets, void* out, void* stream) {
+                                 const int32_t* offsets, void* out, void* stream,
+                                 const int32_t* a_rows, int a_total) {
   if (n % BN != 0 || experts > kMaxExperts) return 1;
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   const int grid = upper < cu_count() ? upper : cu_count();
   const Order order = tile_order(n, k);
-  hipLaunchKernelGGL((grouped_gemm_v2_kernel<false, false, false, false, true>), dim3(grid),
-                     dim3(kThreads), 0, (hipStream_t)stream, a, a_scale, rows, w, w_scale, 1,
-                     experts, n, k, offsets, 0, (const uint16_t*)nullptr, (uint16_t*)out,
-                     (uint8_t*)nullptr, (float*)nullptr, 0.0f, (const uint16_t*)nullptr,
-                     (const uint16_t*)nullptr, 0, order.n_group, order.rotate);
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream, a, a_scale,
+                       rows, w, w_scale, 1, experts, n, k, offsets, 0, (const uint16_t*)nullptr,
+                       (uint16_t*)out, (uint8_t*)nullptr, (float*)nullptr, 0.0f,
+                       (const uint16_t*)nullptr, (const uint16_t*)nullptr, 0, order.n_group,
+                       order.rotate, a_rows, a_rows != nullptr ? a_total : rows);
+  };
+  if (a_rows != nullptr) launch(grouped_gemm_v2_kernel<false, false, false, false, true, true>);
+  else launch(grouped_gemm_v2_kernel<false, false, false, false, true>);
   MI355X_LAUNCH_CHECK();
   return 0;
 }
@@ -580,7 +624,7 @@ int mi355x_gemm_v2_rowwise_launch(const uint8_t* a, const float* a_scale, int ro
                        rows, w, w_scale, 0, experts, n, k, offsets, 0, (const uint16_t*)nullptr,
                        (uint16_t*)out, (uint8_t*)nullptr, (float*)nullptr, 0.0f,
                        (const uint16_t*)lora_z, (const uint16_t*)lora_b, lora_rank,
-                       order.n_group, order.rotate);
+                       order.n_group, order.rotate, (const int32_t*)nullptr, rows);
   };
   if (lora_z != nullptr) launch(grouped_gemm_v2_kernel<false, false, true, true>);
   else launch(grouped_gemm_v2_kernel<false, false, false, true>);

@@ -601,6 +601,44 @@ def gemm_kmajor(a, a_scale, w, w_scale, offsets):
     return out
 
 
+def gemm_gathered(a, a_scale, a_rows, w, w_scale, offsets, *, interleave=False, kmajor=False):
+    """:func:`gemm` (``kmajor=False``, ``w [E, N, K]`` with scales ``[E, N/128,
+    K/128]``) or :func:`gemm_kmajor` (``w [E, K, N]``) whose GEMM row r is row
+    ``a_rows[r]`` of ``a [T, K]``, scales ``a_scale [K/128, T]``: the
+    activation quantized once per token and read by each of its routed rows
+    (``mi355x_gemm_fp8_block_gathered`` / ``_kmajor_gathered``). Bitwise the
+    same as the routed-row forms on the permuted copy."""
+    tokens, k = a.shape
+    rows = a_rows.shape[0]
+    if kmajor:
+        experts, wk, n = w.shape
+        wscale = (experts, k // 128, n // 128)
+    else:
+        experts, n, wk = w.shape
+        wscale = (experts, n // 128, k // 128)
+    if a.dtype != FP8 or w.dtype != FP8 or wk != k:
+        raise ValueError("gemm_gathered takes e4m3 token rows [T,K] and an e4m3 weight")
+    _check(a_scale, (k // 128, tokens), torch.float32, "token row scales")
+    _check(a_rows, (rows,), torch.int32, "a_rows")
+    _check(w_scale, wscale, torch.float32, "weight scales")
+    _check(offsets, (experts + 1,), torch.int32, "offsets")
+    if not w.is_contiguous():
+        raise ValueError("gemm_gathered: the weight must be contiguous")
+    device = _on_gpu(a, a_scale, a_rows, w, w_scale, offsets)
+    out = torch.empty((rows, n), dtype=torch.bfloat16, device=device)
+    if kmajor:
+        _timed("gemm_fp8_block", device, 2 * rows * n * k, rows * k + experts * n * k + 2 * rows * n,
+               "mi355x_gemm_fp8_block_kmajor_gathered", _ptr(a), _ptr(a_scale), tokens,
+               _ptr(a_rows), rows, _ptr(w), _ptr(w_scale), experts, n, k, _ptr(offsets),
+               _ptr(out), _stream(device))
+    else:
+        _timed("gemm_fp8_block", device, 2 * rows * n * k, rows * k + experts * n * k + 2 * rows * n,
+               "mi355x_gemm_fp8_block_gathered", _ptr(a), _ptr(a_scale), tokens, _ptr(a_rows),
+               rows, _ptr(w), _ptr(w_scale), experts, n, k, _ptr(offsets), int(interleave),
+               _ptr(out), _stream(device))
+    return out
+
+
 def rank_product(a, bt, offsets, *, splits=None):
     """``out[r] = a[r] @ bt[e]^T`` for the rows of each expert: bf16 ``[rows, R]``
     from bf16 ``a [rows, K]`` and ``bt [E, R, K]`` (``mi355x_rank_product``).

@@ -12,13 +12,14 @@ Forward (sorted rows ``A = T * k``):
   logits = bf16 x @ bf16 Wr^T (fp32)          router GEMM
   weights, ids = router_topk(logits)          one wave per token
   counts, offsets, order, slots = plan(ids)   stable counting sort
-  xq = permute_quantize(x)                    read x once, write k e4m3 rows (1x128)
-  h  = gemm(xq, W13) interleaved gate/up      fp8 MFMA, bf16 out [A, 2I]
+  xq = quantize_rows(x)                       e4m3 token rows (1x128); k < 4: permuted
+  h  = gemm(xq[order / k], W13) gate/up       fp8 MFMA reading each routed row's token
+                                              row, bf16 out [A, 2I]
   aq = swiglu_quantize(h)                     e4m3 act (1x128)
   y  = gemm(aq, W2)                           [A, H]
   out = residual + sum_j w * y[slot]          token-parallel combine
 Backward:
-  r = gemm(quant(dy)[slots], W2^T)            input gradient through W2
+  r = gemm(quant(dy)[order / k], W2)         input gradient through W2 (K-major)
   dh, a', dscore = swiglu_bwd_quantize(r, h)  fused: quant(dh), dh^T, a'^T
   dW2 = wgrad(dy^T, a'^T), dW13 = wgrad(dh^T, x^T)   fp8 wgrad, 128-row blocks
   dx = gemm(quant(dh), W13^T); grad_x = sum_j dx[slot] + grad_logits @ Wr
@@ -169,11 +170,11 @@ def forward_routed(
             topk_group=int(topk_group), routed_scaling=float(routed_scaling), forced_ids=forced,
         )
         counts, offsets, order, slots = kernels.permute_plan(ids, experts)
-        xq, xs = kernels.permute_quantize(x, slots)
         # GEMM, then the SwiGLU pass: measured faster than the fused epilogue
         # of mi355x_gemm_fp8_block_swiglu, whose activation math runs while
         # every wave of the CU is in the epilogue (no MFMA work to hide it).
-        h13 = kernels.gemm(xq, xs, w13_data, w13_scale, offsets, interleave=True)
+        h13 = routed_rows_gemm(x, slots, order, int(top_k), (w13_data, w13_scale), offsets,
+                               interleave=True)
         aq, as_ = kernels.swiglu_quantize(h13, swiglu_limit)
         y = kernels.gemm(aq, as_, w2_data, w2_scale, offsets)
         output = kernels.combine(y, slots, weights, base)
@@ -216,8 +217,7 @@ def backward_routed(
         if dy.dtype != torch.bfloat16:
             dy = dy.to(torch.bfloat16)
         # Through the down projection: r = dy_routed @ W2, then SwiGLU backward.
-        dyq, dys = kernels.permute_quantize(dy, slots)
-        r = input_gradient_gemm(dyq, dys, w2, offsets)
+        r = routed_rows_gemm(dy, slots, order, int(top_k), w2, offsets, input_gradient=True)
         # SwiGLU backward fused with the quantizers of its outputs: dh row-
         # quantized for the input gradient, dh and a' transposed for the
         # weight gradients (each only when that gradient is wanted).
@@ -327,6 +327,36 @@ def _split(w13, w2, weight_components):
                 (w2, weight_components[1], weight_components[3]))
     raise ValueError("the block-FP8 operators take the two weights' scales (and optionally "
                      "their transposed data) as components")
+
+
+# From this many routed rows per token, the GEMMs read token rows quantized
+# once (mi355x_gemm_fp8_block_gathered) instead of a permuted copy of k rows
+# per token. Measured on MI355X at C3 (k = 8): the copy's 69 us against 18 us
+# for the token rows, the gathered GEMM ~3% slower on the up projection and
+# ~4% faster on r = dy @ W2; at k = 2 (Mixtral) the gathered GEMMs lose more
+# (4% of a 2 ms GEMM) than the copy costs.
+GATHER_MIN_TOP_K = 4
+
+
+def routed_rows_gemm(x, slots, order, top_k, weight, offsets, *, interleave=False,
+                     input_gradient=False):
+    """The GEMM on the routed rows of token rows ``x [T, K]`` (bf16): the
+    projection ``rows @ W[e]^T`` (``weight = (data [E, N, K], scale)``), or
+    with ``input_gradient`` the input gradient ``rows @ W[e]`` as
+    :func:`input_gradient_gemm` does it. Bitwise the same whichever way the
+    rows are read."""
+    data, scale = weight[0], weight[1]
+    n = data.shape[2] if input_gradient else data.shape[1]
+    kmajor = input_gradient and len(weight) == 2
+    if top_k >= GATHER_MIN_TOP_K and n % 256 == 0 and (kmajor or not input_gradient):
+        tq, ts = kernels.quantize_rows(x)
+        a_rows = torch.div(order, top_k, rounding_mode="floor")
+        return kernels.gemm_gathered(tq, ts, a_rows, data, scale, offsets, interleave=interleave,
+                                     kmajor=kmajor)
+    xq, xs = kernels.permute_quantize(x, slots)
+    if input_gradient:
+        return input_gradient_gemm(xq, xs, weight, offsets)
+    return kernels.gemm(xq, xs, data, scale, offsets, interleave=interleave)
 
 
 def input_gradient_gemm(aq, a_scale, weight, offsets):
@@ -699,6 +729,8 @@ IMPLEMENTATION = register_implementation(
 )
 
 __all__ = [
+    "GATHER_MIN_TOP_K",
+    "routed_rows_gemm",
     "IMPLEMENTATION",
     "apply",
     "backward",

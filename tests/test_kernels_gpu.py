@@ -362,6 +362,42 @@ def test_grouped_gemm_matches_fp64(device, case):
     assert worst_cell_rel(out, want, offsets.tolist()) < 1e-2
 
 
+@pytest.mark.parametrize("tokens,top_k,experts,k,n,form", [
+    (2000, 4, 16, 512, 512, "up"),           # gate/up interleave, partial row tiles
+    (1000, 3, 8, 128, 256, "plain"),         # one K step: the next tile's rows at once
+    (777, 2, 5, 1024, 768, "kmajor"),        # input gradient through a K-major weight
+    (16384, 8, 128, 2048, 1536, "up"),       # C3's up projection
+    (16384, 8, 128, 2048, 768, "kmajor"),    # C3's input gradient through W2
+])
+def test_grouped_gemm_gathered_matches_permuted_copy(device, tokens, top_k, experts, k, n, form):
+    """Token rows quantized once and read through the routed rows' tokens
+    (a_rows = order // top_k) give the same bytes as the routed-row GEMM on
+    the permuted copy; the per-token quantization equals the permuted one."""
+    g = torch.Generator().manual_seed(tokens + k + n)
+    logits = torch.randn(tokens, experts, generator=g)
+    logits[:, 1] -= 30.0  # expert 1 empty
+    x = torch.randn(tokens, k, generator=g).to(torch.bfloat16).to(device)
+    _, ids = K.router_topk(logits.to(device), top_k, "topk_then_softmax")
+    _, offsets, order, slots = K.permute_plan(ids, experts)
+    a_rows = (order // top_k).to(torch.int32)
+    xq, xs = K.permute_quantize(x, slots)
+    tq, ts = K.quantize_rows(x)
+    assert torch.equal(_bytes(tq[a_rows.long()]), _bytes(xq))
+    assert torch.equal(ts[:, a_rows.long()].cpu(), xs.cpu())
+    w = (torch.randn(experts, n, k, generator=g) * 0.02).to(torch.bfloat16).to(device)
+    if form == "kmajor":
+        wk = w.transpose(1, 2).contiguous()              # [E, K, N] as stored
+        wq, ws = K.quantize_weight_blocks(wk)
+        want = K.gemm_kmajor(xq, xs, wq, ws, offsets)
+        got = K.gemm_gathered(tq, ts, a_rows, wq, ws, offsets, kmajor=True)
+    else:
+        wq, ws = K.quantize_weight_blocks(w)
+        inter = form == "up"
+        want = K.gemm(xq, xs, wq, ws, offsets, interleave=inter)
+        got = K.gemm_gathered(tq, ts, a_rows, wq, ws, offsets, interleave=inter)
+    assert torch.equal(got.cpu(), want.cpu())
+
+
 @pytest.mark.parametrize("counts,k,n", [
     (COUNTS, 512, 256),                      # empty expert, partial row tiles
     ([300, 0, 520, 45], 1536, 2048),         # C3's input gradient through W13 (K = 2I)
