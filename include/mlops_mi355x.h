@@ -296,7 +296,8 @@ int mi355x_gemm_fp8_block_kmajor(const uint8_t* a, const float* a_scale, int row
 
 /* mi355x_gemm_fp8_block / mi355x_gemm_fp8_block_kmajor whose GEMM row r
  * (expert-sorted rows, offsets) is row a_rows[r] of a [a_total, K] e4m3 with
- * 1x128 scales a_scale [K/128][a_total]: the activation (x forward, dy for
+ * 1x128 scales a_scale [a_total][K/128] (token-major, as
+ * mi355x_quantize_token_rows_fp8 writes them): the activation (x forward, dy for
  * r = dy @ W2) quantized once per token and read by each of its k routed
  * rows, instead of a permuted copy of k rows per token. a_rows int32 [rows]
  * (the token of each routed row). N a multiple of 256; no addend. Bitwise
@@ -305,6 +306,11 @@ int mi355x_gemm_fp8_block_kmajor(const uint8_t* a, const float* a_scale, int row
  * block_fp8_transposed_gemm (kernels/quack_moe/quantize_rows.py:35,
  * block_fp8_gemm.py:1458 and :1424; the reference's GEMM takes no gather,
  * block_fp8_gemm.py:392). */
+/* Token rows quantized for the gathered GEMMs: x bf16 [rows, width] ->
+ * e4m3 q [rows, width] with 1x128 scales [rows][width/128] (row-major: a
+ * row's scales together), the same values as mi355x_quantize_rows_fp8. */
+int mi355x_quantize_token_rows_fp8(const void* x, int rows, int width, uint8_t* q, float* scales,
+                                   void* stream);
 int mi355x_gemm_fp8_block_gathered(const uint8_t* a, const float* a_scale, int a_total,
                                    const int32_t* a_rows, int rows, const uint8_t* w,
                                    const float* w_scale, int experts, int n, int k,

@@ -95,10 +95,10 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
   __shared__ float act_amax[2][BM];  // per-row amax of each wave column's 64 act columns
   __shared__ int prefix[kMaxExperts + 1];
   __shared__ int tmp[kThreads];
-  // Gathered A (a_rows non-null): GEMM row r reads a[a_rows[r]] and its
-  // scales a_scale[kb * scale_pitch + a_rows[r]]: the activation quantized
-  // once per token, each token row read by its k routed rows. A tile's 256
-  // source rows are copied into one of two tables one tile ahead.
+  // Gathered A (kGather): GEMM row r reads a[a_rows[r]] and its scales
+  // a_scale[a_rows[r] * (K/128) + kb] (token-major): the activation
+  // quantized once per token, each token row read by its k routed rows. A
+  // tile's 256 source rows are copied into one of two tables one tile ahead.
   __shared__ int gtok[2][BM];
   tile_prefix(offsets, experts, BM, prefix, tmp);
   const int n_tiles = N / BN;
@@ -153,12 +153,14 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       }
     }
     if constexpr (kRow) return;  // no per-step scales
-    const float* sbase = a_scale + (size_t)kb * (kGather ? scale_pitch : rows);
     if (lane < 32) {
-      int src;
-      if constexpr (kGather) src = gtok[t.par][wave * 32 + (lane & 31)];
-      else src = min(t.row0 + wave * 32 + lane, rows - 1);
-      dma4(sbase, 4u * (uint32_t)src, base + A_BYTES + B_BYTES + wave * 128);
+      // Gathered: token-major scales [tokens][K/128], a token's K steps on
+      // one line; else K-block-major [K/128][rows].
+      const float* sbase = kGather ? a_scale + kb : a_scale + (size_t)kb * rows;
+      uint32_t off;
+      if constexpr (kGather) off = 4u * (uint32_t)gtok[t.par][wave * 32 + (lane & 31)] * (uint32_t)kbw;
+      else off = 4u * (uint32_t)min(t.row0 + wave * 32 + lane, rows - 1);
+      dma4(sbase, off, base + A_BYTES + B_BYTES + wave * 128);
     }
     // The wave's two weight block scales (its columns' low and high 128-column
     // blocks) into the stage as well: an ordinary load here would make the

@@ -108,10 +108,13 @@ __global__ void __launch_bounds__(256) transpose_fp8_kernel(const uint8_t* __res
 // ---------------------------------------------------------------------------
 // Rows already in routed order -> e4m3 with 1x128 scales [width/128][rows].
 // gate_up: the source row is [g0,u0,g1,u1,...]; store gates then ups.
+// row_scales: scales [rows][width/128] instead (a row's scales together: the
+// gathered GEMM's per-step scale reads of a token then share one line).
 __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __restrict__ x,
                                                             int rows, int width, int64_t pitch,
                                                             int gate_up, uint8_t* __restrict__ q,
-                                                            float* __restrict__ scales) {
+                                                            float* __restrict__ scales,
+                                                            int row_scales = 0) {
   const int wave = threadIdx.x >> 6, lane = lane_id();
   const int r = blockIdx.x * 4 + wave;
   if (r >= rows) return;
@@ -142,7 +145,11 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __re
         const uint2 packed = quant8(v, s);
         if (col < width) {
           *(uint2*)(q + (size_t)r * width + col) = packed;
-          if ((lane & 15) == 0) scales[(size_t)(col >> 7) * rows + r] = s;
+          if ((lane & 15) == 0) {
+            const size_t si = row_scales ? (size_t)r * (width >> 7) + (col >> 7)
+                                         : (size_t)(col >> 7) * rows + r;
+            scales[si] = s;
+          }
         }
       }
     }
@@ -748,6 +755,16 @@ extern "C" int mi355x_quantize_rows_fp8(const void* x, int rows, int width, int6
   if (rows == 0) return MI355X_OK;
   hipLaunchKernelGGL(quantize_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)x, rows, width, pitch, gate_up, q, scales);
+  MI355X_LAUNCH_CHECK();
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_quantize_token_rows_fp8(const void* x, int rows, int width, uint8_t* q,
+                                              float* scales, void* stream) {
+  MI355X_REQUIRE(width > 0 && width % 128 == 0, "quantize_token_rows: width must be a multiple of 128");
+  if (rows == 0) return MI355X_OK;
+  hipLaunchKernelGGL(quantize_rows_kernel, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, rows, width, (int64_t)width, 0, q, scales, 1);
   MI355X_LAUNCH_CHECK();
   return MI355X_OK;
 }

@@ -601,10 +601,27 @@ def gemm_kmajor(a, a_scale, w, w_scale, offsets):
     return out
 
 
+def quantize_token_rows(x: torch.Tensor):
+    """Token rows ``bf16 [T, W]`` -> ``(e4m3 [T, W], scales [T, W/128])`` for
+    :func:`gemm_gathered`: :func:`quantize_rows`' values, scales row-major."""
+    if x.dtype != torch.bfloat16 or x.ndim != 2:
+        raise ValueError("quantize_token_rows takes bf16 [rows, width]")
+    x = x.contiguous()
+    rows, width = x.shape
+    device = _on_gpu(x)
+    q = torch.empty((rows, width), dtype=FP8, device=device)
+    scales = torch.empty((rows, width // 128), dtype=torch.float32, device=device)
+    nbytes = 2 * rows * width + rows * width + 4 * rows * (width // 128)
+    _timed("quantize_rows_fp8", device, 0, nbytes, "mi355x_quantize_token_rows_fp8", _ptr(x), rows,
+           width, _ptr(q), _ptr(scales), _stream(device))
+    return q, scales
+
+
 def gemm_gathered(a, a_scale, a_rows, w, w_scale, offsets, *, interleave=False, kmajor=False):
     """:func:`gemm` (``kmajor=False``, ``w [E, N, K]`` with scales ``[E, N/128,
     K/128]``) or :func:`gemm_kmajor` (``w [E, K, N]``) whose GEMM row r is row
-    ``a_rows[r]`` of ``a [T, K]``, scales ``a_scale [K/128, T]``: the
+    ``a_rows[r]`` of ``a [T, K]``, token-major scales ``a_scale [T, K/128]``
+    (:func:`quantize_token_rows`): the
     activation quantized once per token and read by each of its routed rows
     (``mi355x_gemm_fp8_block_gathered`` / ``_kmajor_gathered``). Bitwise the
     same as the routed-row forms on the permuted copy."""
@@ -618,7 +635,7 @@ def gemm_gathered(a, a_scale, a_rows, w, w_scale, offsets, *, interleave=False, 
         wscale = (experts, n // 128, k // 128)
     if a.dtype != FP8 or w.dtype != FP8 or wk != k:
         raise ValueError("gemm_gathered takes e4m3 token rows [T,K] and an e4m3 weight")
-    _check(a_scale, (k // 128, tokens), torch.float32, "token row scales")
+    _check(a_scale, (tokens, k // 128), torch.float32, "token row scales")
     _check(a_rows, (rows,), torch.int32, "a_rows")
     _check(w_scale, wscale, torch.float32, "weight scales")
     _check(offsets, (experts + 1,), torch.int32, "offsets")

@@ -349,7 +349,7 @@ def routed_rows_gemm(x, slots, order, top_k, weight, offsets, *, interleave=Fals
     n = data.shape[2] if input_gradient else data.shape[1]
     kmajor = input_gradient and len(weight) == 2
     if top_k >= GATHER_MIN_TOP_K and n % 256 == 0 and (kmajor or not input_gradient):
-        tq, ts = kernels.quantize_rows(x)
+        tq, ts = kernels.quantize_token_rows(x)
         a_rows = torch.div(order, top_k, rounding_mode="floor")
         return kernels.gemm_gathered(tq, ts, a_rows, data, scale, offsets, interleave=interleave,
                                      kmajor=kmajor)

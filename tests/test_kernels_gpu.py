@@ -381,9 +381,9 @@ def test_grouped_gemm_gathered_matches_permuted_copy(device, tokens, top_k, expe
     _, offsets, order, slots = K.permute_plan(ids, experts)
     a_rows = (order // top_k).to(torch.int32)
     xq, xs = K.permute_quantize(x, slots)
-    tq, ts = K.quantize_rows(x)
+    tq, ts = K.quantize_token_rows(x)
     assert torch.equal(_bytes(tq[a_rows.long()]), _bytes(xq))
-    assert torch.equal(ts[:, a_rows.long()].cpu(), xs.cpu())
+    assert torch.equal(ts[a_rows.long()].t().cpu(), xs.cpu())
     w = (torch.randn(experts, n, k, generator=g) * 0.02).to(torch.bfloat16).to(device)
     if form == "kmajor":
         wk = w.transpose(1, 2).contiguous()              # [E, K, N] as stored
