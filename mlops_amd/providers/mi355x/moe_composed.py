@@ -133,10 +133,14 @@ def prepare_forward(h2, router_weight, w13, *, top_k, routing_mode, router_bias=
             topk_group=int(topk_group), routed_scaling=float(routed_scaling), forced_ids=forced,
         )
         counts, offsets, order, slots = kernels.permute_plan(ids, experts)
-        xq, xs = _rows(x, slots, w13)
         # Block-FP8 w13 is stored gate rows then up rows and the GEMM
         # interleaves its output; an fp8_current w13 is stored interleaved.
-        h13 = _forward_gemm(xq, xs, w13, offsets, interleave=True)
+        if getattr(w13, "current", False):
+            xq, xs = _rows(x, slots, w13)
+            h13 = _forward_gemm(xq, xs, w13, offsets, interleave=True)
+        else:
+            h13 = fused.routed_rows_gemm(x, slots, order, int(top_k), w13, offsets,
+                                         interleave=True)
         aux, probability_sum, _, _ = kernels.router_stats(logits, ids, int(top_k), routing_mode,
                                                           lengths)
     return aux, counts, probability_sum, logits, weights, ids, order, offsets, slots, h13
@@ -170,8 +174,12 @@ def finish_backward(grad_output, h13, w2, route_weights, order, offsets, slots, 
         dy = grad_output.reshape(-1, width).contiguous()
         if dy.dtype != torch.bfloat16:
             dy = dy.to(torch.bfloat16)
-        dyq, dys = _rows(dy, slots, w2)
-        r = _input_gradient_gemm(dyq, dys, w2, offsets)
+        if getattr(w2, "current", False):
+            dyq, dys = _rows(dy, slots, w2)
+            r = _input_gradient_gemm(dyq, dys, w2, offsets)
+        else:
+            r = fused.routed_rows_gemm(dy, slots, order, int(top_k), w2, offsets,
+                                       input_gradient=True)
         grad_h13, a_prime, dscore = kernels.routed_swiglu_backward(
             r, h13, route_weights.reshape(-1), order, swiglu_limit, dh_out=grad_h13_out)
         grad_route_weights = dscore[slots.reshape(-1).long()].view(route_weights.shape)
