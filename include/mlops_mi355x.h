@@ -348,6 +348,14 @@ int mi355x_gemm_fp8_block_lora(const uint8_t* a, const float* a_scale, int rows,
  * providers/sonicmoe/fp8.py:226-247 _project_down, :330-357
  * input_gradient_rows, the products of :205-224 up_projection and :271-309
  * down_backward_activations). */
+/* mi355x_gemm_fp8_rowwise whose row r is row a_rows[r] of per-token e4m3
+ * a [a_total, K] with descales a_scale [a_total] (the fp8_current activation
+ * quantized once per token; see mi355x_gemm_fp8_block_gathered). Bitwise
+ * equal to the routed-row form on mi355x_permute_quantize_current_fp8's copy. */
+int mi355x_gemm_fp8_rowwise_gathered(const uint8_t* a, const float* a_scale, int a_total,
+                                     const int32_t* a_rows, int rows, const uint8_t* w,
+                                     const float* w_scale, int experts, int n, int k,
+                                     const int32_t* offsets, void* out, void* stream);
 int mi355x_gemm_fp8_rowwise(const uint8_t* a, const float* a_scale, int rows, const uint8_t* w,
                             const float* w_scale, int experts, int n, int k,
                             const int32_t* offsets, void* out, void* stream);

@@ -412,7 +412,8 @@ int mi355x_gemm_v2_kmajor_launch(const uint8_t* a, const float* a_scale, int row
 int mi355x_gemm_v2_rowwise_launch(const uint8_t* a, const float* a_scale, int rows,
                                   const uint8_t* w, const float* w_scale, int experts, int n,
                                   int k, const int32_t* offsets, const void* lora_z,
-                                  const void* lora_b, int lora_rank, void* out, void* stream);
+                                  const void* lora_b, int lora_rank, void* out, void* stream,
+                                  const int32_t* a_rows = nullptr, int a_total = 0);
 
 int mi355x_wgrad_v2_launch(const uint8_t* p, const float* p_scale, int m_features,
                            const uint8_t* q, const float* q_scale, int n_features, int padded,
@@ -516,6 +517,25 @@ extern "C" int mi355x_gemm_fp8_block_kmajor_gathered(const uint8_t* a, const flo
                                               out, stream, a_rows, a_total);
   if (v2 < 0) return v2;
   MI355X_REQUIRE(v2 == 0, "gemm_kmajor: shape outside the pipelined kernel");
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_gemm_fp8_rowwise_gathered(const uint8_t* a, const float* a_scale,
+                                                int a_total, const int32_t* a_rows, int rows,
+                                                const uint8_t* w, const float* w_scale,
+                                                int experts, int n, int k,
+                                                const int32_t* offsets, void* out, void* stream) {
+  MI355X_REQUIRE(experts > 0 && experts <= kMaxExperts, "gemm_rowwise: experts must be in [1, %d]",
+                 kMaxExperts);
+  MI355X_REQUIRE(n > 0 && n % 256 == 0, "gemm_rowwise: N must be a multiple of 256, got %d", n);
+  MI355X_REQUIRE(k > 0 && k % BK == 0, "gemm_rowwise: K must be a multiple of %d, got %d", BK, k);
+  const int c = gathered_checks(a_total, a_rows, rows, k);
+  if (c != MI355X_OK) return c;
+  if (rows == 0) return MI355X_OK;
+  const int v2 = mi355x_gemm_v2_rowwise_launch(a, a_scale, rows, w, w_scale, experts, n, k, offsets,
+                                               nullptr, nullptr, 0, out, stream, a_rows, a_total);
+  if (v2 < 0) return v2;
+  MI355X_REQUIRE(v2 == 0, "gemm_rowwise gathered: shape outside the pipelined kernel");
   return MI355X_OK;
 }
 

@@ -451,7 +451,9 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
           if (wm * 64 + lrow < ct.nvalid) {
             const uint32_t off = (uint32_t)lrow * (uint32_t)N + lane_col;
             if constexpr (kRow) {
-              const float xs = a_scale[ct.row0 + wm * 64 + lrow];
+              float xs;
+              if constexpr (kGather) xs = a_scale[gtok[ct.par][wm * 64 + lrow]];
+              else xs = a_scale[ct.row0 + wm * 64 + lrow];
 #pragma unroll
               for (int m = 0; m < 8; ++m) v[m] = (v[m] * xs) * wsc[m];
             }
@@ -616,7 +618,8 @@ int mi355x_gemm_v2_kmajor_launch(const uint8_t* a, const float* a_scale, int row
 int mi355x_gemm_v2_rowwise_launch(const uint8_t* a, const float* a_scale, int rows,
                                   const uint8_t* w, const float* w_scale, int experts, int n,
                                   int k, const int32_t* offsets, const void* lora_z,
-                                  const void* lora_b, int lora_rank, void* out, void* stream) {
+                                  const void* lora_b, int lora_rank, void* out, void* stream,
+                                  const int32_t* a_rows, int a_total) {
   if (n % BN != 0 || experts > kMaxExperts) return 1;
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   const int grid = upper < cu_count() ? upper : cu_count();
@@ -626,9 +629,12 @@ int mi355x_gemm_v2_rowwise_launch(const uint8_t* a, const float* a_scale, int ro
                        rows, w, w_scale, 0, experts, n, k, offsets, 0, (const uint16_t*)nullptr,
                        (uint16_t*)out, (uint8_t*)nullptr, (float*)nullptr, 0.0f,
                        (const uint16_t*)lora_z, (const uint16_t*)lora_b, lora_rank,
-                       order.n_group, order.rotate, (const int32_t*)nullptr, rows);
+                       order.n_group, order.rotate, a_rows, a_rows != nullptr ? a_total : rows);
   };
-  if (lora_z != nullptr) launch(grouped_gemm_v2_kernel<false, false, true, true>);
+  if (a_rows != nullptr) {
+    if (lora_z != nullptr) return 1;  // not a form of this kernel
+    launch(grouped_gemm_v2_kernel<false, false, false, true, false, true>);
+  } else if (lora_z != nullptr) launch(grouped_gemm_v2_kernel<false, false, true, true>);
   else launch(grouped_gemm_v2_kernel<false, false, false, true>);
   MI355X_LAUNCH_CHECK();
   return 0;

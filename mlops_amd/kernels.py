@@ -886,6 +886,30 @@ def gemm_rowwise(a, a_scale, w, w_scale, offsets, *, lora=None):
     return out
 
 
+def gemm_rowwise_gathered(a, a_scale, a_rows, w, w_scale, offsets):
+    """:func:`gemm_rowwise` whose row r is row ``a_rows[r]`` of per-token
+    ``a [T, K]`` with descales ``a_scale [T]`` (:func:`quantize_rows_current`
+    on the token rows; ``mi355x_gemm_fp8_rowwise_gathered``). Bitwise the
+    same as on the permuted copy."""
+    tokens, k = a.shape
+    rows = a_rows.shape[0]
+    experts, n, wk = w.shape
+    if a.dtype != FP8 or w.dtype != FP8 or wk != k:
+        raise ValueError("gemm_rowwise_gathered takes e4m3 token rows [T,K] and weights [E,N,K]")
+    _check(a_scale, (tokens,), torch.float32, "token row scales")
+    _check(a_rows, (rows,), torch.int32, "a_rows")
+    _check(w_scale, (experts, n), torch.float32, "weight row scales")
+    _check(offsets, (experts + 1,), torch.int32, "offsets")
+    device = _on_gpu(a, a_scale, a_rows, w, w_scale, offsets)
+    out = torch.empty((rows, n), dtype=torch.bfloat16, device=device)
+    _timed(
+        "gemm_fp8_rowwise", device, 2 * rows * n * k, rows * k + experts * n * k + 2 * rows * n,
+        "mi355x_gemm_fp8_rowwise_gathered", _ptr(a), _ptr(a_scale), tokens, _ptr(a_rows), rows,
+        _ptr(w), _ptr(w_scale), experts, n, k, _ptr(offsets), _ptr(out), _stream(device),
+    )
+    return out
+
+
 def _gemm_rowwise_lora(a, a_scale, w, w_scale, offsets, z, b):
     rows, k = a.shape
     experts, n, wk = w.shape

@@ -6,8 +6,10 @@ Expert weights are `RowFP8Weight` containers (the reference's
 ``QuackFP8Weight``), or bf16/fp32 masters quantized per call. Every operand
 of the expert GEMMs carries one descale per row:
 
-* forward: each token's row quantized once and written to its routed slots
-  (``mi355x_permute_quantize_current_fp8``); the up GEMM against the
+* forward: each token's row quantized once (from top_k 4 read by the GEMM
+  through the routed rows' tokens, ``mi355x_gemm_fp8_rowwise_gathered``;
+  below, written to its routed slots, ``mi355x_permute_quantize_current_fp8``);
+  the up GEMM against the
   gate/up-adjacent rows of ``w13`` writes ``h13`` interleaved; SwiGLU and
   its per-row quantization in one pass; the down GEMM; combine;
 * backward: the gathered cotangent quantized per row, then ``r = dy @ W2``
@@ -108,8 +110,7 @@ def forward_routed(h2, residual, router_weight, w13, w2, *, top_k, routing_mode,
             topk_group=int(topk_group), routed_scaling=float(routed_scaling), forced_ids=forced,
         )
         counts, offsets, order, slots = kernels.permute_plan(ids, experts)
-        xq, xs = kernels.permute_quantize_current(x, slots)
-        h13 = kernels.gemm_rowwise(xq, xs, w13[0], w13[2], offsets)
+        h13 = _routed_rows_gemm(x, slots, order, int(top_k), w13[0], w13[2], offsets)
         aq, as_ = kernels.swiglu_quantize_rows_current(h13, swiglu_limit)
         y = kernels.gemm_rowwise(aq, as_, w2[0], w2[2], offsets)
         output = kernels.combine(y, slots, weights, base)
@@ -117,6 +118,19 @@ def forward_routed(h2, residual, router_weight, w13, w2, *, top_k, routing_mode,
                                                           lengths)
     return (output.reshape(h2.shape), aux, counts, probability_sum, logits, weights, ids, order,
             offsets, slots, h13)
+
+
+def _routed_rows_gemm(x, slots, order, top_k, data, scale, offsets):
+    """The row-scaled GEMM on the routed rows of token rows ``x``: from
+    ``GATHER_MIN_TOP_K`` routed rows per token, on the token rows quantized
+    once (``mi355x_gemm_fp8_rowwise_gathered``), else on the permuted copy.
+    Bitwise the same either way."""
+    if top_k >= fused.GATHER_MIN_TOP_K and data.shape[1] % 256 == 0:
+        tq, ts = kernels.quantize_rows_current(x)
+        a_rows = torch.div(order, top_k, rounding_mode="floor")
+        return kernels.gemm_rowwise_gathered(tq, ts, a_rows, data, scale, offsets)
+    xq, xs = kernels.permute_quantize_current(x, slots)
+    return kernels.gemm_rowwise(xq, xs, data, scale, offsets)
 
 
 def backward_routed(grad_output, grad_aux, grad_probability_sum, h2, router_weight, w13, w2,
@@ -139,8 +153,7 @@ def backward_routed(grad_output, grad_aux, grad_probability_sum, h2, router_weig
         dy = grad_output.reshape(rows, width).contiguous()
         if dy.dtype != torch.bfloat16:
             dy = dy.to(torch.bfloat16)
-        dyq, dys = kernels.permute_quantize_current(dy, slots)
-        r = kernels.gemm_rowwise(dyq, dys, w2[1], w2[3], offsets)
+        r = _routed_rows_gemm(dy, slots, order, int(top_k), w2[1], w2[3], offsets)
         if need_w2 or need_w13:
             # One pass for bf16 dh and the transposed dh and a' of the weight
             # gradients (equal to the SwiGLU backward then quantize_transpose).

@@ -398,6 +398,32 @@ def test_grouped_gemm_gathered_matches_permuted_copy(device, tokens, top_k, expe
     assert torch.equal(got.cpu(), want.cpu())
 
 
+@pytest.mark.parametrize("tokens,top_k,experts,k,n", [
+    (1500, 4, 16, 512, 512),
+    (16384, 8, 128, 2048, 1536),             # C3's up projection at fp8_current
+])
+def test_rowwise_gemm_gathered_matches_permuted_copy(device, tokens, top_k, experts, k, n):
+    """The row-scaled GEMM on token rows read through the routed rows equals
+    the one on the permuted copy bit for bit (per-row descales in the epilogue
+    taken from the tokens)."""
+    g = torch.Generator().manual_seed(tokens + n)
+    logits = torch.randn(tokens, experts, generator=g)
+    logits[:, 2] -= 30.0
+    x = torch.randn(tokens, k, generator=g).to(torch.bfloat16).to(device)
+    _, ids = K.router_topk(logits.to(device), top_k, "topk_then_softmax")
+    _, offsets, order, slots = K.permute_plan(ids, experts)
+    a_rows = (order // top_k).to(torch.int32)
+    xq, xs = K.permute_quantize_current(x, slots)
+    tq, ts = K.quantize_rows_current(x)
+    assert torch.equal(_bytes(tq[a_rows.long()]), _bytes(xq))
+    assert torch.equal(ts[a_rows.long()].cpu(), xs.cpu())
+    w = (torch.randn(experts, n, k, generator=g) * 0.02).to(torch.bfloat16).to(device)
+    wq, _, wsc, _ = K.quantize_weights_current(w)
+    want = K.gemm_rowwise(xq, xs, wq, wsc, offsets)
+    got = K.gemm_rowwise_gathered(tq, ts, a_rows, wq, wsc, offsets)
+    assert torch.equal(got.cpu(), want.cpu())
+
+
 @pytest.mark.parametrize("counts,k,n", [
     (COUNTS, 512, 256),                      # empty expert, partial row tiles
     ([300, 0, 520, 45], 1536, 2048),         # C3's input gradient through W13 (K = 2I)
