@@ -308,9 +308,8 @@ class _ExpertLoRA(torch.autograd.Function):
                 grad_aux, grad_probability_sum, top_k=top_k, routing_mode=mode,
                 lengths=opts["lengths"], router_dtype=router_dtype, need_router=bool(need[2]),
             )
-        grad_residual = None
-        if need[1] and grad_output is not None:
-            grad_residual = grad_output.clone()
+        # d residual is the output cotangent itself (no copy).
+        grad_residual = grad_output if need[1] else None
         return (grad_hidden.reshape(hidden.shape).to(hidden.dtype) if need[0] else None,
                 grad_residual, grad_router if need[2] else None, grad_w13, grad_w2,
                 *grads, None)

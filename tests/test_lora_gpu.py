@@ -46,7 +46,7 @@ def _leaf(t):
 
 def _run_gpu(x, res, wr, w13, w2, a13, b13, a2, b2, dy, *, train_base, mode, limit=None,
              current=False):
-    x, wr = _leaf(x), _leaf(wr)
+    x, wr, res = _leaf(x), _leaf(wr), _leaf(res)
     factors = [_leaf(t) for t in (a13, b13, a2, b2)]
     if train_base:
         w13, w2 = _leaf(w13), _leaf(w2)
@@ -60,7 +60,10 @@ def _run_gpu(x, res, wr, w13, w2, a13, b13, a2, b2, dy, *, train_base, mode, lim
         x, res, wr, w13, w2, *factors, top_k=TOP_K, routing_mode=mode, scale=SCALE,
         swiglu_limit=limit, compute_precision=precision)
     trainable = [x, wr, *factors] + ([w13, w2] if train_base else [])
-    grads = torch.autograd.grad((out.float() * dy.float()).sum() + 0.3 * aux, trainable)
+    *grads, grad_res = torch.autograd.grad((out.float() * dy.float()).sum() + 0.3 * aux,
+                                           trainable + [res])
+    # The residual passes straight through: its gradient is the output cotangent.
+    assert torch.equal(grad_res, dy.to(grad_res.dtype))
     return out.detach(), aux.detach(), counts, psum.detach(), grads
 
 
