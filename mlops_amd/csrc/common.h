@@ -133,12 +133,16 @@ __device__ __forceinline__ float quant_div(float x, float scale) {
 // q0 = RN(x inv), the residual e = x - scale q0 is exact (FMA) and
 // RN(q0 + e inv) = RN(x / scale) (Markstein) for quotients that neither
 // overflow nor underflow, which covers every quotient that reaches a nonzero
-// e4m3 value. Then the same clip to +-448.
+// e4m3 value.
+// No clip to +-448: every caller's scale is max(amax * RN(1/448), 1e-12) or
+// max(amax / 448, 1e-12) over a group holding x, so |x / scale| <=
+// 448 (1 + 2^-22) < 464, which round-to-nearest e4m3 takes to 448 (the clip
+// of the division form above would not change it), and a NaN or infinite x
+// stays NaN, as the reference's clamp-then-cast leaves it.
 __device__ __forceinline__ float quant_div_inv(float x, float scale, float inv) {
   const float q0 = x * inv;
   const float e = fmaf(-scale, q0, x);
-  const float q = fmaf(e, inv, q0);
-  return fminf(fmaxf(q, -kE4M3Max), kE4M3Max);
+  return fmaf(e, inv, q0);
 }
 
 // SwiGLU clamp (limit <= 0: none): gate from above, up on both sides.

@@ -235,22 +235,22 @@ __global__ void __launch_bounds__(256) swiglu_quantize_kernel(const uint16_t* __
       if (++grp == groups) { grp = 0; ++r; }
     }
   }
+  // Unit g covers h elements [256 g, 256 g + 256) and act / q elements
+  // [128 g, 128 g + 128): a row holds `groups` units back to back in both.
+  const uint16_t* src = h + (size_t)g0 * 256 + lane16 * 16;
+  const size_t dst0 = (size_t)g0 * 128 + lane16 * 8;
   uint4 ha[kSwUnits], hb[kSwUnits];
 #pragma unroll
   for (int u = 0; u < kSwUnits; ++u) {
     ha[u] = hb[u] = make_uint4(0, 0, 0, 0);
     if (g0 + u < units) {
-      const uint16_t* src = h + (size_t)urow[u] * 2 * width + 2 * (ugrp[u] * 128 + lane16 * 8);
-      ha[u] = load_stream(src);
-      hb[u] = load_stream(src + 8);
+      ha[u] = load_stream(src + u * 256);
+      hb[u] = load_stream(src + u * 256 + 8);
     }
   }
 #pragma unroll
   for (int u = 0; u < kSwUnits; ++u) {
     if (g0 + u >= units) break;  // uniform over the 16-lane group
-    const size_t r = urow[u];
-    const uint32_t grp = ugrp[u];
-    const int j = (int)grp * 128 + lane16 * 8;
     float a[8], b[8], act[8];
     unpack_bf16x8(ha[u], a);
     unpack_bf16x8(hb[u], b);
@@ -269,15 +269,15 @@ __global__ void __launch_bounds__(256) swiglu_quantize_kernel(const uint16_t* __
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(act[i]));
     amax = group_amax<16>(amax);
     const float sc = fmaxf(amax * kInv448, kMinScale);
-    store_stream8(q + r * width + j, quant8(act, sc));
-    if (lane16 == 0) scales[(size_t)grp * rows + r] = sc;
+    store_stream8(q + dst0 + u * 128, quant8(act, sc));
+    if (lane16 == 0) scales[(size_t)ugrp[u] * rows + urow[u]] = sc;
     if (act_out != nullptr) {
       uint4 o;
       o.x = pack_bf16x2(act[0], act[1]);
       o.y = pack_bf16x2(act[2], act[3]);
       o.z = pack_bf16x2(act[4], act[5]);
       o.w = pack_bf16x2(act[6], act[7]);
-      store_stream(act_out + r * width + j, o);
+      store_stream(act_out + dst0 + u * 128, o);
     }
   }
 }
