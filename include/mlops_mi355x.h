@@ -300,7 +300,9 @@ int mi355x_gemm_fp8_block_kmajor(const uint8_t* a, const float* a_scale, int row
  * mi355x_quantize_token_rows_fp8 writes them): the activation (x forward, dy for
  * r = dy @ W2) quantized once per token and read by each of its k routed
  * rows, instead of a permuted copy of k rows per token. a_rows int32 [rows]
- * (the token of each routed row). N a multiple of 256; no addend. Bitwise
+ * (the token of each routed row), every entry in [0, a_total): the kernel
+ * reads the rows they name unchecked, as it reads offsets. N a multiple of
+ * 256; no addend. Bitwise
  * equal to the routed-row forms on mi355x_permute_quantize_fp8's copy.
  * Replaces permute_quantize_rows followed by block_fp8_gemm /
  * block_fp8_transposed_gemm (kernels/quack_moe/quantize_rows.py:35,
