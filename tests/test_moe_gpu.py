@@ -421,3 +421,42 @@ def test_protocol_container_equals_block_fp8_weight(device):
     ours = run(lambda d, s: BlockFP8Weight(d, s, dtype=torch.bfloat16))
     for a, b in zip(theirs, ours, strict=True):
         assert a is not None and torch.equal(a, b)
+
+
+@pytest.mark.parametrize("precision", ["fp8_block", "fp8_current"])
+def test_gathered_token_rows_equal_permuted_copy_in_the_layer(device, monkeypatch, precision):
+    """From top_k 4 the up projection and r = dy @ W2 read the token rows
+    quantized once (gathered GEMMs); below, a permuted copy. Forcing either
+    path on the same top-4 layer gives bitwise the same outputs and
+    gradients (bf16 masters quantized per call)."""
+    from mlops_amd.providers.mi355x import moe as fused
+
+    x, res, wr, w13, w2, dy = _inputs(device, tokens=384, hidden=512, experts=8, inter=256,
+                                      seed=7)
+
+    calls = []
+    for name in ("gemm_gathered", "gemm_rowwise_gathered"):
+        original = getattr(K, name)
+
+        def counted(*args, _original=original, **kwargs):
+            calls.append(1)
+            return _original(*args, **kwargs)
+
+        monkeypatch.setattr(K, name, counted)
+
+    def run(threshold):
+        monkeypatch.setattr(fused, "GATHER_MIN_TOP_K", threshold)
+        leaves = [t.clone().requires_grad_(True) for t in (x, wr, w13, w2)]
+        out, aux, counts, psum = mlops_amd.moe(leaves[0], res, leaves[1], leaves[2], leaves[3],
+                                               top_k=4, routing_mode="softmax_then_topk",
+                                               compute_precision=precision)
+        grads = torch.autograd.grad([out, aux], leaves, [dy, torch.ones_like(aux) * 0.1])
+        return [out, aux, counts, psum, *grads]
+
+    gathered = run(4)
+    assert len(calls) == 2  # the up projection and r = dy @ W2
+    permuted = run(10**9)
+    assert len(calls) == 2
+    names = ["out", "aux", "counts", "psum", "x", "router", "w13", "w2"]
+    for name, a, b in zip(names, gathered, permuted, strict=True):
+        assert torch.equal(a, b), name
