@@ -11,6 +11,7 @@ Layouts: routed rows ``A = tokens * top_k`` are in expert-sorted order;
 
 from __future__ import annotations
 
+import ctypes
 from typing import Sequence
 
 import torch
@@ -24,6 +25,47 @@ MAX_EXPERTS = 512
 MAX_TOP_K = 32
 
 
+class _HipEvents:
+    """HIP events created with ``hipEventDisableSystemFence``, through the HIP
+    runtime this process already loaded (torch's). A default event's record
+    ends with a system-scope fence, a cache writeback that a timed interval
+    would count; these events only take timestamps."""
+
+    DISABLE_SYSTEM_FENCE = 0x20000000
+
+    def __init__(self):
+        paths = [line.split()[-1] for line in open("/proc/self/maps") if "libamdhip64" in line]
+        if not paths:
+            raise RuntimeError("the HIP runtime is not loaded in this process")
+        lib = ctypes.CDLL(paths[0])
+        lib.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                            ctypes.c_void_p]
+        lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.lib = lib
+
+    def _check(self, status, what):
+        if status != 0:
+            raise RuntimeError(f"{what} failed with HIP error {status}")
+
+    def record(self, stream) -> ctypes.c_void_p:
+        event = ctypes.c_void_p()
+        self._check(self.lib.hipEventCreateWithFlags(ctypes.byref(event), self.DISABLE_SYSTEM_FENCE),
+                    "hipEventCreateWithFlags")
+        self._check(self.lib.hipEventRecord(event, stream), "hipEventRecord")
+        return event
+
+    def elapsed_ms(self, start, end) -> float:
+        ms = ctypes.c_float()
+        self._check(self.lib.hipEventElapsedTime(ctypes.byref(ms), start, end),
+                    "hipEventElapsedTime")
+        return ms.value
+
+    def destroy(self, event) -> None:
+        self.lib.hipEventDestroy(event)
+
+
 class LaunchTimer:
     """Records a pair of device events around each timed kernel launch, on the
     stream the kernel is enqueued on, with the launch's algorithmic work.
@@ -31,26 +73,27 @@ class LaunchTimer:
 
     def __init__(self):
         self.records = []  # (name, start, end, flops, bytes)
+        self.events = _HipEvents()
 
     def start(self, device):
-        event = torch.cuda.Event(enable_timing=True)
-        event.record(torch.cuda.current_stream(device))
-        return event
+        return self.events.record(_stream(device))
 
     def stop(self, name, device, start, flops=0, nbytes=0):
-        event = torch.cuda.Event(enable_timing=True)
-        event.record(torch.cuda.current_stream(device))
-        self.records.append((name, start, event, flops, nbytes))
+        self.records.append((name, start, self.events.record(_stream(device)), flops, nbytes))
 
     def summary(self):
-        """``{name: dict(launches, ms_total, ms_avg, flops, bytes)}``."""
+        """``{name: dict(launches, ms_total, ms_avg, flops, bytes)}``; the
+        events are released."""
         out = {}
         for name, start, end, flops, nbytes in self.records:
             entry = out.setdefault(name, dict(launches=0, ms_total=0.0, flops=0, bytes=0))
             entry["launches"] += 1
-            entry["ms_total"] += start.elapsed_time(end)
+            entry["ms_total"] += self.events.elapsed_ms(start, end)
             entry["flops"] += flops
             entry["bytes"] += nbytes
+            self.events.destroy(start)
+            self.events.destroy(end)
+        self.records = []
         for entry in out.values():
             entry["ms_avg"] = entry["ms_total"] / entry["launches"]
         return out
