@@ -18,6 +18,13 @@ template <>
 __device__ __forceinline__ void load8<uint16_t>(const uint16_t* p, float* v) {
   load_bf16x8(p, v);
 }
+// Weights: read once per pass, through non-temporal loads.
+template <typename T>
+__device__ __forceinline__ void load8_once(const T* p, float* v) { load8(p, v); }
+template <>
+__device__ __forceinline__ void load8_once<uint16_t>(const uint16_t* p, float* v) {
+  unpack_bf16x8(load_stream(p), v);
+}
 template <>
 __device__ __forceinline__ void load8<float>(const float* p, float* v) {
   const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
@@ -222,7 +229,7 @@ __device__ __forceinline__ void load_tile(const T* __restrict__ we, int out, int
   for (int i = 0; i < R; ++i) {
     const int p = p0 + rg * R + i;
     if (p < out && col < in) {
-      load8(we + (size_t)logical_row(p, out, interleave) * in + col, v[i]);
+      load8_once(we + (size_t)logical_row(p, out, interleave) * in + col, v[i]);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[i][j] = 0.0f;
