@@ -465,7 +465,8 @@ extern "C" int mi355x_gemm_fp8_block_kmajor(const uint8_t* a, const float* a_sca
 }
 
 // Gathered-A forms: GEMM row r (expert-sorted, offsets) reads row
-// a_rows[r] of a [a_total, K] and its 1x128 scales a_scale[K/128][a_total]
+// a_rows[r] of a [a_total, K] and its 1x128 scales a_scale[a_total][K/128]
+// (token-major, as mi355x_quantize_token_rows_fp8 writes them)
 // (the activation quantized once per token; a_rows = the token of each
 // routed row). Pipelined kernel only (N a multiple of 256).
 static int gathered_checks(int a_total, const int32_t* a_rows, int rows, int k) {

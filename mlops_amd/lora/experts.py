@@ -187,6 +187,9 @@ class _ExpertLoRA(torch.autograd.Function):
         ctx.opts = opts
         ctx.w13, ctx.w2 = w13, w2
         ctx.factor_dtypes = (a13.dtype, b13.dtype, a2.dtype, b2.dtype)
+        # The bf16 activation (A * I * 2 bytes) is kept only for dA2.
+        if not ctx.needs_input_grad[7]:
+            act = act.new_empty(0)
         ctx.save_for_backward(hidden, router_weight, logits, weights, ids, order, offsets, slots,
                               h13, act, z13, z2p, rows_token, rows_expert, a13b, b13b, a2b, b2b)
         ctx.mark_non_differentiable(counts)

@@ -319,12 +319,16 @@ def _split(w13, w2, weight_components):
     """``((w13, scale[, data_t]), (w2, scale[, data_t]))``: the two scales,
     optionally followed by the two transposed e4m3 copies the per-call
     quantizer writes in the same pass (containers built elsewhere have none;
-    the input-gradient GEMMs then transpose on the fly)."""
+    the input-gradient GEMMs then read the data as stored or transpose on the
+    fly). An empty tensor stands for the copy of a weight that has none."""
     if len(weight_components) == 2:
         return (w13, weight_components[0]), (w2, weight_components[1])
     if len(weight_components) == 4:
-        return ((w13, weight_components[0], weight_components[2]),
-                (w2, weight_components[1], weight_components[3]))
+        parts = []
+        for data, scale, data_t in ((w13, weight_components[0], weight_components[2]),
+                                    (w2, weight_components[1], weight_components[3])):
+            parts.append((data, scale) if data_t.numel() == 0 else (data, scale, data_t))
+        return tuple(parts)
     raise ValueError("the block-FP8 operators take the two weights' scales (and optionally "
                      "their transposed data) as components")
 
@@ -517,8 +521,9 @@ def _container_rule(cls, func, types, args, kwargs):
             # already has, or the data as stored (none is made here).
             transposed.append(available_transposed(value) if backward
                               else getattr(value, "_transposed", None))
-    if len(transposed) == 2 and all(t is not None for t in transposed):
-        components.extend(transposed)
+    if len(transposed) == 2 and any(t is not None for t in transposed):
+        components.extend(t if t is not None else args[0].new_empty(0, dtype=torch.uint8)
+                          for t in transposed)
     args[-1] = components
     return func(*args)
 
@@ -585,12 +590,13 @@ class _QuantizePerCall(torch.autograd.Function):
     semantics, straight-through gradient). The input-gradient GEMMs read the
     e4m3 data as stored (K-major), so no transposed copy is written: that
     saves a quarter of the quantizer's bytes for ~4-10% on those two GEMMs.
-    A weight whose N is not a multiple of 256 (outside the K-major kernel)
-    still gets the copy from the same pass."""
+    A weight whose last axis (the N of that K-major GEMM) is not a multiple
+    of 256 (outside the K-major kernel) still gets the copy from the same
+    pass."""
 
     @staticmethod
     def forward(ctx, weight):
-        if weight.shape[1] % 256 == 0:
+        if weight.shape[2] % 256 == 0:
             data, scale = kernels.quantize_weight_blocks(weight.detach())
             return BlockFP8Weight(data, scale, dtype=weight.dtype)
         data, scale, data_t = kernels.quantize_weight_blocks(weight.detach(), transposed=True)

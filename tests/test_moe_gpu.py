@@ -317,6 +317,43 @@ def test_per_call_transposed_weights_match_containers_bitwise(device, monkeypatc
         assert torch.equal(u.float(), v.float())
 
 
+def test_per_call_transposed_copy_follows_the_kmajor_width(device, monkeypatch):
+    """The per-call quantizer writes the transposed copy exactly for a weight
+    whose last axis (the N of its K-major input-gradient GEMM) is not a
+    multiple of 256: w2 [E, H, I] with I = 384 gets it, w13 [E, 2I, H] with
+    H = 256 does not; the backward then transposes nothing itself, and the
+    results equal those of pre-built containers bit for bit."""
+    from mlops_amd import kernels as K
+
+    flags, calls = [], []
+    quantize, transpose = K.quantize_weight_blocks, K.transpose_fp8
+    monkeypatch.setattr(K, "quantize_weight_blocks",
+                        lambda w, transposed=False: flags.append((w.shape[2], transposed))
+                        or quantize(w, transposed=transposed))
+    monkeypatch.setattr(K, "transpose_fp8", lambda data: calls.append(1) or transpose(data))
+    x, res, wr, w13, w2, dy = _inputs(device, tokens=256, hidden=256, experts=4, inter=384,
+                                      seed=11)
+    results = []
+    for per_call in (True, False):
+        xg = x.clone().requires_grad_(True)
+        if per_call:
+            a, b = w13.clone().requires_grad_(True), w2.clone().requires_grad_(True)
+        else:
+            a = BlockFP8Weight.quantize(w13).detach().requires_grad_(True)
+            b = BlockFP8Weight.quantize(w2).detach().requires_grad_(True)
+        flags.clear()
+        calls.clear()
+        out, *_ = mlops_amd.moe(xg, res, wr, a, b, top_k=2, routing_mode="topk_then_softmax",
+                                compute_precision="fp8_block")
+        out.backward(dy)
+        if per_call:
+            assert sorted(flags) == [(256, False), (384, True)]
+            assert len(calls) == 0
+        results.append((out, xg.grad, a.grad, b.grad))
+    for u, v in zip(*results):
+        assert torch.equal(u.float(), v.float())
+
+
 @pytest.mark.parametrize("shape", [
     # BASELINE config 4 (DeepSeek-V3 shard: H=7168, I=2048, 32 local experts,
     # k=8, Zipf(1.2)-skewed routing, weights N(0, 0.006)) at 512 tokens.
