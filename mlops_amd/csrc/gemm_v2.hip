@@ -153,25 +153,27 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       }
     }
     if constexpr (kRow) return;  // no per-step scales
-    if (lane < 32) {
+    // The step's scales travel in the stage with its operands (an ordinary
+    // load here would make the compiler wait on it, and in-order completion
+    // would make that wait cover this step's operand copies too), in as few
+    // copies as their layout allows: the 256 row scales by waves 0-3, 64
+    // rows each, and the two weight block scales of each wave column (its
+    // low and high 128 columns) by waves 4-5.
+    if (wave < 4) {
       // Gathered: token-major scales [tokens][K/128], a token's K steps on
       // one line; else K-block-major [K/128][rows].
       const float* sbase = kGather ? a_scale + kb : a_scale + (size_t)kb * rows;
       uint32_t off;
-      if constexpr (kGather) off = 4u * (uint32_t)gtok[t.par][wave * 32 + (lane & 31)] * (uint32_t)kbw;
-      else off = 4u * (uint32_t)min(t.row0 + wave * 32 + lane, rows - 1);
-      dma4(sbase, off, base + A_BYTES + B_BYTES + wave * 128);
-    }
-    // The wave's two weight block scales (its columns' low and high 128-column
-    // blocks) into the stage as well: an ordinary load here would make the
-    // compiler wait on it, and in-order completion would make that wait
-    // cover this step's operand copies too.
-    if (lane < 2) {
-      const int nb = lane == 0 ? (interleave ? t.nt : 2 * t.nt + wn)
-                               : (interleave ? half_n / 128 + t.nt : 2 * t.nt + wn);
+      if constexpr (kGather) off = 4u * (uint32_t)gtok[t.par][wave * 64 + lane] * (uint32_t)kbw;
+      else off = 4u * (uint32_t)min(t.row0 + wave * 64 + lane, rows - 1);
+      dma4(sbase, off, base + A_BYTES + B_BYTES + wave * 256);
+    } else if (wave < 6 && lane < 2) {
+      const int c = wave - 4;  // wave column
+      const int nb = lane == 0 ? (interleave ? t.nt : 2 * t.nt + c)
+                               : (interleave ? half_n / 128 + t.nt : 2 * t.nt + c);
       const uint32_t idx = w_scale_t ? (uint32_t)((t.e * kbw + kb) * nbw + nb)
                                      : (uint32_t)((t.e * nbw + nb) * kbw + kb);
-      dma4(w_scale, 4u * idx, base + A_BYTES + B_BYTES + SA_BYTES + wave * 8);
+      dma4(w_scale, 4u * idx, base + A_BYTES + B_BYTES + SA_BYTES + c * 8);
     }
   };
 
@@ -303,7 +305,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
         continue;
       }
       const float* sa = (const float*)(base + A_BYTES + B_BYTES);
-      const float2 sbw = *(const float2*)(base + A_BYTES + B_BYTES + SA_BYTES + wave * 8);
+      const float2 sbw = *(const float2*)(base + A_BYTES + B_BYTES + SA_BYTES + wn * 8);
       const float sb_lo = sbw.x, sb_hi = sbw.y;
       // One B block at a time against the four A blocks (register budget:
       // two waves share a SIMD, 256 registers each), read one block ahead.
