@@ -354,6 +354,54 @@ def test_per_call_transposed_copy_follows_the_kmajor_width(device, monkeypatch):
         assert torch.equal(u.float(), v.float())
 
 
+def test_forced_zipf_top1_at_c4_width_matches_fp8_oracle(device):
+    """The C4 benchmark's own workload form -- top-1 slots whose experts are
+    forced from an i.i.d. Zipf(1.2) draw through the routing override, at
+    the DeepSeek-V3 shard widths (H=7168, I=2048, 32 experts, weights
+    N(0, 0.006)) -- on 384 slots, against the block-FP8 oracle. The oracle
+    routes through logits raised by 100 at the forced experts (top-1 under
+    topk_then_softmax: the route weight is 1 and carries no logit gradient
+    either way). Several experts receive no slot."""
+    import numpy as np
+
+    from mlops_amd import router
+    from mlops_amd.routing import routing_override
+
+    tokens, hidden, inter, experts = 384, 7168, 2048, 32
+    x, res, wr, w13, w2, dy = _inputs(device, tokens, hidden, experts, inter, seed=31, std=0.006)
+    p = np.arange(1, experts + 1, dtype=np.float64) ** -1.2
+    draw = np.random.default_rng(7).choice(experts, size=(tokens, 1), p=p / p.sum())
+    ids = torch.from_numpy(draw.astype(np.int32)).to(device)
+    xg = x.clone().requires_grad_(True)
+    w13c = BlockFP8Weight.quantize(w13).detach().requires_grad_(True)
+    w2c = BlockFP8Weight.quantize(w2).detach().requires_grad_(True)
+    with routing_override([ids]):
+        out, _aux, counts, _psum = mlops_amd.moe(xg, res, wr, w13c, w2c, top_k=1,
+                                                 routing_mode="topk_then_softmax")
+    out.backward(dy)
+    want_counts = torch.bincount(ids.long().cpu().reshape(-1), minlength=experts)
+    assert torch.equal(counts.cpu().long(), want_counts)
+    assert int((want_counts == 0).sum()) > 0
+    cpu = lambda t: t.detach().cpu()
+    w13q, w13s = w13c.components()
+    w2q, w2s = w2c.components()
+    logits = router.router_logits(x, wr).cpu()
+    logits[torch.arange(tokens), ids.long().cpu()[:, 0]] += 100.0
+    fwd = O.fp8_moe_forward(cpu(x), cpu(res), cpu(wr), cpu(w13q), cpu(w13s), cpu(w2q), cpu(w2s),
+                            top_k=1, routing_mode="topk_then_softmax", logits=logits)
+    assert torch.equal(fwd["counts"], want_counts)
+    assert frob_rel(cpu(out).float(), fwd["out"].float()) < 1e-2
+    bwd = O.fp8_moe_backward(fwd, cpu(x), cpu(dy), cpu(wr), cpu(w13q), cpu(w13s), cpu(w2q),
+                             cpu(w2s), top_k=1, routing_mode="topk_then_softmax")
+    assert frob_rel(cpu(xg.grad).float(), bwd["grad_x"].float()) < 1e-2
+    for e in range(experts):
+        if int(want_counts[e]) == 0:
+            assert float(w13c.grad[e].abs().max()) == 0.0
+            continue
+        assert frob_rel(cpu(w13c.grad[e]).float(), bwd["dw13"][e]) < 1e-2, e
+        assert frob_rel(cpu(w2c.grad[e]).float(), bwd["dw2"][e]) < 1e-2, e
+
+
 @pytest.mark.parametrize("shape", [
     # BASELINE config 4 (DeepSeek-V3 shard: H=7168, I=2048, 32 local experts,
     # k=8, Zipf(1.2)-skewed routing, weights N(0, 0.006)) at 512 tokens.
