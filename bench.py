@@ -321,12 +321,34 @@ def cpu_baseline(cfg_name, sample_tokens=128, budget_s=20.0, max_iters=10, warmu
     }
 
 
+# Sources whose code decides the grouped GEMMs' memory traffic: the traffic
+# figures in profiles/traffic.json hold the digest of these files as they were
+# when the counters were read, and are reported only while it still matches.
+TRAFFIC_SOURCES = ("mlops_amd/csrc/gemm_v2.hip", "mlops_amd/csrc/gemm_pipe.h",
+                   "mlops_amd/csrc/gemm_wgrad.hip", "mlops_amd/csrc/quantize.hip",
+                   "mlops_amd/csrc/permute.hip")
+
+
+def source_digest():
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in TRAFFIC_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def load_traffic(kernel):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary,
+    or None when the summary is missing or was taken on other sources."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         data = json.load(f)
+    if data.get("_sources") != source_digest():
+        return None
     return data.get(kernel)
 
 
