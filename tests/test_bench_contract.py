@@ -15,11 +15,13 @@ def test_traffic_summary_is_reported_for_its_own_sources(tmp_path, monkeypatch):
     """A summary whose digest names the current sources is reported as is."""
     bench = _bench()
     data = json.loads((ROOT / "profiles" / "traffic.json").read_text())
-    data["_sources"] = bench["source_digest"]()
+    digest = bench["source_digest"]()
+    data["_sources"] = digest
     (tmp_path / "profiles").mkdir()
     (tmp_path / "profiles" / "traffic.json").write_text(json.dumps(data))
     load = bench["load_traffic"]
     monkeypatch.setitem(load.__globals__, "ROOT", str(tmp_path))
+    monkeypatch.setitem(load.__globals__, "source_digest", lambda: digest)
     assert load("gemm_fp8_block") == data["gemm_fp8_block"]
 
 
