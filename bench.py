@@ -321,12 +321,11 @@ def cpu_baseline(cfg_name, sample_tokens=128, budget_s=20.0, max_iters=10, warmu
     }
 
 
-# Sources whose code decides the grouped GEMMs' memory traffic: the traffic
+# Sources whose code decides the GEMMs' memory traffic: the traffic
 # figures in profiles/traffic.json hold the digest of these files as they were
 # when the counters were read, and are reported only while it still matches.
 TRAFFIC_SOURCES = ("mlops_amd/csrc/gemm_v2.hip", "mlops_amd/csrc/gemm_pipe.h",
-                   "mlops_amd/csrc/gemm_wgrad.hip", "mlops_amd/csrc/quantize.hip",
-                   "mlops_amd/csrc/permute.hip")
+                   "mlops_amd/csrc/gemm_wgrad.hip")
 
 
 def source_digest():
