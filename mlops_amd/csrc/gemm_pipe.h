@@ -58,16 +58,6 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t off, const uint
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" MI355X_DMA_POLICY
                :: "s"(lds_addr(lds)), "v"(off), "s"(base) : "memory", "m0");
 }
-// The same with the LDS destination as a byte address (wave-uniform), for
-// kernels that form their stage addresses from the LDS base once.
-__device__ __forceinline__ void dma16a(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" MI355X_DMA_POLICY
-               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(off), "s"(base) : "memory", "m0");
-}
-__device__ __forceinline__ void dma4a(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
-               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(off), "s"(base) : "memory", "m0");
-}
 __device__ __forceinline__ void dma4(const void* base, uint32_t off, const uint8_t* lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
                :: "s"(lds_addr(lds)), "v"(off), "s"(base) : "memory", "m0");

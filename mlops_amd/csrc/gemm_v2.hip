@@ -118,24 +118,20 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
   };
 
   // Direct loads of one K step of tile t into stage `stage`.
-  // LDS byte address of the stages, formed once (the stage addresses below
-  // are integer offsets from it).
-  const uint32_t smem_lds = lds_addr(smem);
   auto issue = [&](const Tile& t, int step, int stage) {
     const int kb = __builtin_amdgcn_readfirstlane(step + t.rot < nk ? step + t.rot : step + t.rot - nk);
-    const uint32_t base = smem_lds + (uint32_t)(stage * STAGE_BYTES);
+    uint8_t* base = smem + stage * STAGE_BYTES;
     const size_t koff = (size_t)kb * BK;
     const uint8_t* abase = a + koff;
     const uint8_t* bbase = w + (size_t)t.e * N * K + koff;
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
-      if ((wave * A_LOADS + i) * 8 >= t.nvalid) continue;  // rows past the group's end
       const int r = (wave * A_LOADS + i) * 8 + (lane >> 3);
       int src;
       if constexpr (kGather) src = gtok[t.par][r];
       else src = min(t.row0 + r, rows - 1);
       const uint32_t off = (uint32_t)src * (uint32_t)K + 16 * ((lane & 7) ^ swz(r));
-      dma16a(abase, off, base + (wave * A_LOADS + i) * 1024);
+      dma16(abase, off, base + (wave * A_LOADS + i) * 1024);
     }
     if constexpr (kKM) {
       // K rows kb*128 .. +127 of the expert's [K, N] weight, columns of the
@@ -145,7 +141,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       for (int i = 0; i < B_LOADS; ++i) {
         const int r = (wave * B_LOADS + i) * 4 + (lane >> 4);
         const uint32_t off = (uint32_t)r * (uint32_t)N + 16 * ((lane & 15) ^ kmsw(r));
-        dma16a(kbase, off, base + A_BYTES + (wave * B_LOADS + i) * 1024);
+        dma16(kbase, off, base + A_BYTES + (wave * B_LOADS + i) * 1024);
       }
     } else {
 #pragma unroll
@@ -153,7 +149,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
         const int tr = (wave * B_LOADS + i) * 8 + (lane >> 3);
         const uint32_t off = (uint32_t)weight_row(tr, t.nt, interleave, half_n) * (uint32_t)K +
                              16 * ((lane & 7) ^ swz(tr));
-        dma16a(bbase, off, base + A_BYTES + (wave * B_LOADS + i) * 1024);
+        dma16(bbase, off, base + A_BYTES + (wave * B_LOADS + i) * 1024);
       }
     }
     if constexpr (kRow) return;  // no per-step scales
@@ -164,24 +160,20 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     // rows each, and the two weight block scales of each wave column (its
     // low and high 128 columns) by waves 4-5.
     if (wave < 4) {
-      // (A wave whose 64 rows all lie past the group's end copies nothing,
-      // and must not fall through to the weight-scale branch below.)
-      if (wave * 64 < t.nvalid) {
       // Gathered: token-major scales [tokens][K/128], a token's K steps on
       // one line; else K-block-major [K/128][rows].
       const float* sbase = kGather ? a_scale + kb : a_scale + (size_t)kb * rows;
       uint32_t off;
       if constexpr (kGather) off = 4u * (uint32_t)gtok[t.par][wave * 64 + lane] * (uint32_t)kbw;
       else off = 4u * (uint32_t)min(t.row0 + wave * 64 + lane, rows - 1);
-      dma4a(sbase, off, base + A_BYTES + B_BYTES + wave * 256);
-      }
+      dma4(sbase, off, base + A_BYTES + B_BYTES + wave * 256);
     } else if (wave < 6 && lane < 2) {
       const int c = wave - 4;  // wave column
       const int nb = lane == 0 ? (interleave ? t.nt : 2 * t.nt + c)
                                : (interleave ? half_n / 128 + t.nt : 2 * t.nt + c);
       const uint32_t idx = w_scale_t ? (uint32_t)((t.e * kbw + kb) * nbw + nb)
                                      : (uint32_t)((t.e * nbw + nb) * kbw + kb);
-      dma4a(w_scale, 4u * idx, base + A_BYTES + B_BYTES + SA_BYTES + c * 8);
+      dma4(w_scale, 4u * idx, base + A_BYTES + B_BYTES + SA_BYTES + c * 8);
     }
   };
 
@@ -290,10 +282,6 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
         Tile nt = describe(prefix, offsets, experts, n_tiles, next_tile, nk, n_group, rotate);
         if constexpr (kGather) nt.par = (round + 1) & 1;
         issue(nt, 0, stage ^ 1);
-      }
-      if (wm * 64 >= ct.nvalid) {  // this wave's rows are all past the group's end
-        stage ^= 1;
-        continue;
       }
       const uint8_t* base = smem + stage * STAGE_BYTES;
       const uint8_t* ta = base;
