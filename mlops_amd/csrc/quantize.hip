@@ -144,7 +144,7 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __re
         const float s = fmaxf(amax * kInv448, kMinScale);
         const uint2 packed = quant8(v, s);
         if (col < width) {
-          *(uint2*)(q + (size_t)r * width + col) = packed;
+          store_stream8(q + (size_t)r * width + col, packed);
           if ((lane & 15) == 0) {
             const size_t si = row_scales ? (size_t)r * (width >> 7) + (col >> 7)
                                          : (size_t)(col >> 7) * rows + r;
@@ -190,8 +190,8 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __re
       const float sg = fmaxf(ga * kInv448, kMinScale), su = fmaxf(ua * kInv448, kMinScale);
       const uint2 pg = quant8(g, sg), pu = quant8(u, su);
       if (j < half) {
-        *(uint2*)(q + (size_t)r * width + j) = pg;
-        *(uint2*)(q + (size_t)r * width + half + j) = pu;
+        store_stream8(q + (size_t)r * width + j, pg);
+        store_stream8(q + (size_t)r * width + half + j, pu);
         if ((lane & 15) == 0) {
           scales[(size_t)(j >> 7) * rows + r] = sg;
           scales[(size_t)((half + j) >> 7) * rows + r] = su;
@@ -358,8 +358,8 @@ __device__ __forceinline__ void transpose_tile_pow2(bool active, uint16_t* tile,
   for (int pass = 0; pass < 4; ++pass) {
     const int lc = pass * 32 + (t >> 3), part = t & 7;
     const int feat = tile_feature(lc, feat0, c0, gate_half);
-    *(uint4*)(qt + (size_t)feat * padded + (size_t)pb * 128 + part * 16) =
-        *(const uint4*)&staged[lc * kQtLine + part * 16];
+    store_stream(qt + (size_t)feat * padded + (size_t)pb * 128 + part * 16,
+                 *(const uint4*)&staged[lc * kQtLine + part * 16]);
   }
 }
 
@@ -501,8 +501,8 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
           ua = group_amax<16>(ua);
           const float sg = fmaxf(ga * kInv448, kMinScale), su = fmaxf(ua * kInv448, kMinScale);
           uint8_t* qrow = dhq + (size_t)row * 2 * width;
-          *(uint2*)(qrow + j) = quant8(gq, sg);
-          *(uint2*)(qrow + width + j) = quant8(uq, su);
+          store_stream8(qrow + j, quant8(gq, sg));
+          store_stream8(qrow + width + j, quant8(uq, su));
           if ((lane & 15) == 0) {
             dhs[(size_t)(j >> 7) * rows + row] = sg;
             dhs[(size_t)(width / 128 + (j >> 7)) * rows + row] = su;
@@ -533,28 +533,23 @@ __global__ void __launch_bounds__(256) routed_swiglu_bwd_kernel(
 //     power-of-two scales, as quantize_transpose_kernel does.
 constexpr int kSbThreads = 512;
 
-template <bool kClamp>
-__global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
+template <bool kClamp, bool kFull>
+__device__ __forceinline__ void swiglu_bwd_block(
     const uint16_t* __restrict__ rmat, const uint16_t* __restrict__ h,
     const float* __restrict__ weights, const int32_t* __restrict__ order,
     const int32_t* __restrict__ row_blocks, int rows, int width, int padded, float limit,
     uint8_t* __restrict__ dhq, float* __restrict__ dhs, uint8_t* __restrict__ dht,
     float* __restrict__ dhts, uint8_t* __restrict__ apt, float* __restrict__ apts,
-    float* __restrict__ dsp, uint16_t* __restrict__ dh) {
-  // dgate and dup tiles (a' is staged through tile 0 afterwards): ~74 KB,
-  // two blocks per CU.
-  __shared__ __align__(16) uint16_t tiles[2][128 * kQtPitch];
-  __shared__ __align__(16) float pmax[2][8][128];
-  const int pb = blockIdx.x, cb = blockIdx.y, tid = threadIdx.x;
-  const int r0 = row_blocks[2 * pb], nvalid = row_blocks[2 * pb + 1];
-  if (nvalid <= 0) return;  // past the last expert's rows
+    float* __restrict__ dsp, uint16_t* __restrict__ dh,
+    uint16_t (*tiles)[128 * kQtPitch], int cb, int r0, int nvalid, uint4* apk) {
+  const int tid = threadIdx.x;
 
   // Phases 1-3: 16 lanes per row (8 j each), 32 rows per pass, 4 passes;
   // every pass's loads are issued before any compute (memory parallelism).
   const int lane16 = tid & 15, rsub = tid >> 4;
   const int jl = lane16 * 8, j = cb * 128 + jl;
   const int nblk = width / 128;
-  uint4 hv0[4], hv1[4], rv4[4], apk[4];
+  uint4 hv0[4], hv1[4], rv4[4];
   float score[4];
   // The rows' order entries first: each score is a load that depends on
   // one, and loads complete in order, so an order load issued after a
@@ -564,13 +559,13 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int rr = pass * 32 + rsub;
-    orow[pass] = rr < nvalid ? order[r0 + rr] : 0;
+    orow[pass] = (kFull || rr < nvalid) ? order[r0 + rr] : 0;
   }
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int rr = pass * 32 + rsub;
     hv0[pass] = hv1[pass] = rv4[pass] = make_uint4(0, 0, 0, 0);
-    if (rr < nvalid) {
+    if (kFull || rr < nvalid) {
       const int row = r0 + rr;
       const uint16_t* hp = h + (size_t)row * 2 * width + 2 * j;
       hv0[pass] = *(const uint4*)hp;
@@ -580,11 +575,11 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
   }
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass)
-    score[pass] = pass * 32 + rsub < nvalid ? weights[orow[pass]] : 0.0f;
+    score[pass] = (kFull || pass * 32 + rsub < nvalid) ? weights[orow[pass]] : 0.0f;
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int rr = pass * 32 + rsub;
-    const bool valid = rr < nvalid;  // uniform over the 16-lane group
+    const bool valid = (kFull || rr < nvalid);  // uniform over the 16-lane group
     uint4 og = make_uint4(0, 0, 0, 0), ou = og, oa = og;
     if (valid) {
       const int row = r0 + rr;
@@ -649,8 +644,10 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
       ga = group_amax<16>(ga);
       ua = group_amax<16>(ua);
       const float sg = fmaxf(ga * kInv448, kMinScale), su = fmaxf(ua * kInv448, kMinScale);
-      *(uint2*)(dhq + (size_t)row * 2 * width + j) = quant8(gq, sg);
-      *(uint2*)(dhq + (size_t)row * 2 * width + width + j) = quant8(uq, su);
+      // Streaming stores: the outputs are far larger than L2 and are read
+      // back only by later launches.
+      store_stream8(dhq + (size_t)row * 2 * width + j, quant8(gq, sg));
+      store_stream8(dhq + (size_t)row * 2 * width + width + j, quant8(uq, su));
       if (lane16 == 0) {
         dhs[(size_t)cb * rows + row] = sg;
         dhs[(size_t)(nblk + cb) * rows + row] = su;
@@ -661,9 +658,42 @@ __global__ void __launch_bounds__(kSbThreads) swiglu_bwd_quantize_kernel(
     *(uint4*)&tiles[1][rr * kQtPitch + jl] = ou;
     apk[pass] = oa;
   }
+}
+
+
+template <bool kClamp>
+__global__ void __launch_bounds__(kSbThreads) __attribute__((amdgpu_waves_per_eu(4)))
+swiglu_bwd_quantize_kernel(
+    const uint16_t* __restrict__ rmat, const uint16_t* __restrict__ h,
+    const float* __restrict__ weights, const int32_t* __restrict__ order,
+    const int32_t* __restrict__ row_blocks, int rows, int width, int padded, float limit,
+    uint8_t* __restrict__ dhq, float* __restrict__ dhs, uint8_t* __restrict__ dht,
+    float* __restrict__ dhts, uint8_t* __restrict__ apt, float* __restrict__ apts,
+    float* __restrict__ dsp, uint16_t* __restrict__ dh) {
+  // dgate and dup tiles (a' is staged through tile 0 afterwards): ~74 KB,
+  // two blocks per CU.
+  __shared__ __align__(16) uint16_t tiles[2][128 * kQtPitch];
+  __shared__ __align__(16) float pmax[2][8][128];
+  const int pb = blockIdx.x, cb = blockIdx.y;
+  const int r0 = row_blocks[2 * pb], nvalid = row_blocks[2 * pb + 1];
+  if (nvalid <= 0) return;  // past the last expert's rows
+  // A whole block of rows (all but each expert's last block) takes a body
+  // with no per-row validity tests: no zeroed registers for absent rows and
+  // no masked branches around their loads, arithmetic and stores.
+  uint4 apk[4];  // this thread's packed bf16 a' (4 rows x 8 columns)
+  if (nvalid >= 128)
+    swiglu_bwd_block<kClamp, true>(rmat, h, weights, order, row_blocks, rows, width, padded,
+                                   limit, dhq, dhs, dht, dhts, apt, apts, dsp, dh, tiles, cb,
+                                   r0, nvalid, apk);
+  else
+    swiglu_bwd_block<kClamp, false>(rmat, h, weights, order, row_blocks, rows, width, padded,
+                                    limit, dhq, dhs, dht, dhts, apt, apts, dsp, dh, tiles, cb,
+                                    r0, nvalid, apk);
+  // Phase 4 (both bodies): transposed outputs; threads 0-255 and 256-511
+  // each take a tile.
+  const int tid = threadIdx.x, rsub = tid >> 4, jl = (tid & 15) * 8;
   if (dht == nullptr && apt == nullptr) return;
   __syncthreads();
-  // Phase 4: transposed outputs; threads 0-255 and 256-511 each take a tile.
   const int half = tid >> 8, t = tid & 255;
   if (dht != nullptr)
     transpose_tile_pow2(true, tiles[half], pmax[half], t, dht, dhts, half * width + cb * 128,
