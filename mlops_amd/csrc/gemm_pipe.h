@@ -51,11 +51,8 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
 }
 // Source address = wave-uniform 64-bit base (SGPRs) + per-lane 32-bit byte
 // offset (one VGPR), the saddr form of the global load.
-#ifndef MI355X_DMA_POLICY
-#define MI355X_DMA_POLICY ""
-#endif
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, const uint8_t* lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" MI355X_DMA_POLICY
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :: "s"(lds_addr(lds)), "v"(off), "s"(base) : "memory", "m0");
 }
 __device__ __forceinline__ void dma4(const void* base, uint32_t off, const uint8_t* lds) {
