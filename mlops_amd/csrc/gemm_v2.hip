@@ -81,6 +81,9 @@ typedef short v4s __attribute__((ext_vector_type(4)));
 // 128 K rows of 256 bytes and the B fragments read with ds_read_b64_tr_b8;
 // the MFMA columns are then the tile's columns in order, so the epilogue
 // regroups each row's values through LDS into 8-column stores.
+// MFMA block of a K step at which waves 4-7 issue the next step's copies.
+constexpr int kLateIssueBlock = 1;
+
 template <bool kAct, bool kAdd, bool kLora, bool kRow = false, bool kKM = false,
           bool kGather = false>
 __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
@@ -275,8 +278,16 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
         if (nk == 1) wait_and_sync<0>();
       }
       // Next step's operands (the next tile's first step at the last step:
-      // its loads then run under this tile's epilogue).
-      if (kb + 1 < nk) {
+      // its loads then run under this tile's epilogue). A wave is held at
+      // each direct load until the address unit takes it, and waves w and
+      // w + 4 share a SIMD: waves 4-7 issue theirs after their first MFMA
+      // block instead, so that while one wave of a SIMD is held the other
+      // has MFMAs to issue. (A later issue point needs registers the step
+      // does not have: the compiler spills.)
+      const bool late = wave >= 4 && kb + 1 < nk;
+      if (late) {
+        // issued in the K step below, at MFMA block kLateIssueBlock
+      } else if (kb + 1 < nk) {
         issue(ct, kb + 1, stage ^ 1);
       } else if (next_tile < total) {
         Tile nt = describe(prefix, offsets, experts, n_tiles, next_tile, nk, n_group, rotate);
@@ -295,6 +306,11 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
         for (int i = 0; i < 4; ++i) af[i] = frag(ta, wm * 64 + i * 16 + (lane & 15), lane);
 #pragma unroll
         for (int jb = 0; jb < 8; ++jb) {
+          if (late && jb == kLateIssueBlock) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue(ct, kb + 1, stage ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
+          }
           v8i bnext = bcur;
           if (jb < 7) bnext = bfrag(tb, jb + 1, klane);
 #pragma unroll
@@ -326,6 +342,11 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       float sc[4][4];
 #pragma unroll
       for (int jb = 0; jb < 8; ++jb) {
+        if (late && jb == kLateIssueBlock) {
+          __builtin_amdgcn_sched_barrier(0);
+          issue(ct, kb + 1, stage ^ 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
         if (jb == 0 || jb == 4) {
           const float sb = jb < 4 ? sb_lo : sb_hi;
 #pragma unroll
