@@ -299,9 +299,11 @@ int mi355x_gemm_fp8_block_kmajor(const uint8_t* a, const float* a_scale, int row
  * 1x128 scales a_scale [a_total][K/128] (token-major, as
  * mi355x_quantize_token_rows_fp8 writes them): the activation (x forward, dy for
  * r = dy @ W2) quantized once per token and read by each of its k routed
- * rows, instead of a permuted copy of k rows per token. a_rows int32 [rows]
- * (the token of each routed row), every entry in [0, a_total): the kernel
- * reads the rows they name unchecked, as it reads offsets. N a multiple of
+ * rows, instead of a permuted copy of k rows per token. Routed row r reads
+ * token a_rows[r] / a_rows_div: a_rows int32 [rows] is the plan's sorted
+ * slot order with a_rows_div = top_k (no token-id pass), or token ids with
+ * a_rows_div = 1; every token in [0, a_total), a_total * a_rows_div < 2^31:
+ * the kernel reads the rows they name unchecked, as it reads offsets. N a multiple of
  * 256; no addend. Bitwise
  * equal to the routed-row forms on mi355x_permute_quantize_fp8's copy.
  * Replaces permute_quantize_rows followed by block_fp8_gemm /
@@ -314,12 +316,12 @@ int mi355x_gemm_fp8_block_kmajor(const uint8_t* a, const float* a_scale, int row
 int mi355x_quantize_token_rows_fp8(const void* x, int rows, int width, uint8_t* q, float* scales,
                                    void* stream);
 int mi355x_gemm_fp8_block_gathered(const uint8_t* a, const float* a_scale, int a_total,
-                                   const int32_t* a_rows, int rows, const uint8_t* w,
+                                   const int32_t* a_rows, int a_rows_div, int rows, const uint8_t* w,
                                    const float* w_scale, int experts, int n, int k,
                                    const int32_t* offsets, int interleave, void* out,
                                    void* stream);
 int mi355x_gemm_fp8_block_kmajor_gathered(const uint8_t* a, const float* a_scale, int a_total,
-                                          const int32_t* a_rows, int rows, const uint8_t* w,
+                                          const int32_t* a_rows, int a_rows_div, int rows, const uint8_t* w,
                                           const float* w_scale, int experts, int n, int k,
                                           const int32_t* offsets, void* out, void* stream);
 
@@ -355,7 +357,7 @@ int mi355x_gemm_fp8_block_lora(const uint8_t* a, const float* a_scale, int rows,
  * quantized once per token; see mi355x_gemm_fp8_block_gathered). Bitwise
  * equal to the routed-row form on mi355x_permute_quantize_current_fp8's copy. */
 int mi355x_gemm_fp8_rowwise_gathered(const uint8_t* a, const float* a_scale, int a_total,
-                                     const int32_t* a_rows, int rows, const uint8_t* w,
+                                     const int32_t* a_rows, int a_rows_div, int rows, const uint8_t* w,
                                      const float* w_scale, int experts, int n, int k,
                                      const int32_t* offsets, void* out, void* stream);
 int mi355x_gemm_fp8_rowwise(const uint8_t* a, const float* a_scale, int rows, const uint8_t* w,

@@ -86,11 +86,9 @@ SIGNATURES = {
     ),
     "mi355x_gemm_fp8_block_kmajor": (_I, [_P, _P, _I, _P, _P, _I, _I, _I, _P, _P, _P]),
     "mi355x_quantize_token_rows_fp8": (_I, [_P, _I, _I, _P, _P, _P]),
-    "mi355x_gemm_fp8_block_gathered": (_I, [_P, _P, _I, _P, _I, _P, _P, _I, _I, _I, _P, _I, _P,
-                                            _P]),
-    "mi355x_gemm_fp8_block_kmajor_gathered": (_I, [_P, _P, _I, _P, _I, _P, _P, _I, _I, _I, _P, _P,
-                                                   _P]),
-    "mi355x_gemm_fp8_rowwise_gathered": (_I, [_P, _P, _I, _P, _I, _P, _P, _I, _I, _I, _P, _P, _P]),
+    "mi355x_gemm_fp8_block_gathered": (_I, [_P, _P, _I, _P, _I, _I, _P, _P, _I, _I, _I, _P, _I, _P, _P]),
+    "mi355x_gemm_fp8_block_kmajor_gathered": (_I, [_P, _P, _I, _P, _I, _I, _P, _P, _I, _I, _I, _P, _P, _P]),
+    "mi355x_gemm_fp8_rowwise_gathered": (_I, [_P, _P, _I, _P, _I, _I, _P, _P, _I, _I, _I, _P, _P, _P]),
     "mi355x_gemm_fp8_rowwise": (_I, [_P, _P, _I, _P, _P, _I, _I, _I, _P, _P, _P]),
     "mi355x_quantize_rows_current_fp8": (_I, [_P, _I, _I, _I64, _P, _I, _P, _P, _P]),
     "mi355x_permute_quantize_current_fp8": (_I, [_P, _I, _I, _I, _P, _P, _P, _P]),

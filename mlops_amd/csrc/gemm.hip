@@ -403,17 +403,17 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
                           const int32_t* offsets, int interleave, const void* addend, void* out,
                           uint8_t* act_q, float* act_scales, float limit, const void* lora_z,
                           const void* lora_b, int lora_rank, void* stream,
-                          const int32_t* a_rows = nullptr, int a_total = 0);
+                          const int32_t* a_rows = nullptr, int a_total = 0, int a_rows_div = 1);
 int mi355x_gemm_v2_kmajor_launch(const uint8_t* a, const float* a_scale, int rows,
                                  const uint8_t* w, const float* w_scale, int experts, int n, int k,
                                  const int32_t* offsets, void* out, void* stream,
-                                 const int32_t* a_rows = nullptr, int a_total = 0);
+                                 const int32_t* a_rows = nullptr, int a_total = 0, int a_rows_div = 1);
 
 int mi355x_gemm_v2_rowwise_launch(const uint8_t* a, const float* a_scale, int rows,
                                   const uint8_t* w, const float* w_scale, int experts, int n,
                                   int k, const int32_t* offsets, const void* lora_z,
                                   const void* lora_b, int lora_rank, void* out, void* stream,
-                                  const int32_t* a_rows = nullptr, int a_total = 0);
+                                  const int32_t* a_rows = nullptr, int a_total = 0, int a_rows_div = 1);
 
 int mi355x_wgrad_v2_launch(const uint8_t* p, const float* p_scale, int m_features,
                            const uint8_t* q, const float* q_scale, int n_features, int padded,
@@ -469,8 +469,10 @@ extern "C" int mi355x_gemm_fp8_block_kmajor(const uint8_t* a, const float* a_sca
 // (token-major, as mi355x_quantize_token_rows_fp8 writes them)
 // (the activation quantized once per token; a_rows = the token of each
 // routed row). Pipelined kernel only (N a multiple of 256).
-static int gathered_checks(int a_total, const int32_t* a_rows, int rows, int k) {
+static int gathered_checks(int a_total, const int32_t* a_rows, int a_rows_div, int rows, int k) {
   MI355X_REQUIRE(a_rows != nullptr && a_total > 0, "gemm gathered: a_rows and a_total required");
+  MI355X_REQUIRE(a_rows_div >= 1 && (uint64_t)a_total * (uint64_t)a_rows_div < (1ull << 31),
+                 "gemm gathered: a_rows_div must be >= 1 with a_total * a_rows_div < 2^31");
   MI355X_REQUIRE((uint64_t)a_total * (uint64_t)k < (1ull << 32),
                  "gemm gathered: gathered rows beyond 32-bit offsets");
   MI355X_REQUIRE(rows >= 0, "gemm gathered: negative rows");
@@ -478,7 +480,7 @@ static int gathered_checks(int a_total, const int32_t* a_rows, int rows, int k) 
 }
 
 extern "C" int mi355x_gemm_fp8_block_gathered(const uint8_t* a, const float* a_scale, int a_total,
-                                              const int32_t* a_rows, int rows, const uint8_t* w,
+                                              const int32_t* a_rows, int a_rows_div, int rows, const uint8_t* w,
                                               const float* w_scale, int experts, int n, int k,
                                               const int32_t* offsets, int interleave, void* out,
                                               void* stream) {
@@ -488,19 +490,19 @@ extern "C" int mi355x_gemm_fp8_block_gathered(const uint8_t* a, const float* a_s
   MI355X_REQUIRE(k > 0 && k % BK == 0, "gemm: K must be a multiple of %d, got %d", BK, k);
   MI355X_REQUIRE(!interleave || (n / 2) % 128 == 0,
                  "gemm gathered: a gate/up weight needs halves that are multiples of 128");
-  const int c = gathered_checks(a_total, a_rows, rows, k);
+  const int c = gathered_checks(a_total, a_rows, a_rows_div, rows, k);
   if (c != MI355X_OK) return c;
   if (rows == 0) return MI355X_OK;
   const int v2 = mi355x_gemm_v2_launch(a, a_scale, rows, w, w_scale, 0, experts, n, k, offsets,
                                        interleave, nullptr, out, nullptr, nullptr, 0.0f, nullptr,
-                                       nullptr, 0, stream, a_rows, a_total);
+                                       nullptr, 0, stream, a_rows, a_total, a_rows_div);
   if (v2 < 0) return v2;
   MI355X_REQUIRE(v2 == 0, "gemm gathered: shape outside the pipelined kernel");
   return MI355X_OK;
 }
 
 extern "C" int mi355x_gemm_fp8_block_kmajor_gathered(const uint8_t* a, const float* a_scale,
-                                                     int a_total, const int32_t* a_rows, int rows,
+                                                     int a_total, const int32_t* a_rows, int a_rows_div, int rows,
                                                      const uint8_t* w, const float* w_scale,
                                                      int experts, int n, int k,
                                                      const int32_t* offsets, void* out,
@@ -511,18 +513,18 @@ extern "C" int mi355x_gemm_fp8_block_kmajor_gathered(const uint8_t* a, const flo
   MI355X_REQUIRE(k > 0 && k % BK == 0, "gemm_kmajor: K must be a multiple of %d, got %d", BK, k);
   MI355X_REQUIRE((uint64_t)(k - 1) * (uint64_t)n + 256 < (1ull << 32),
                  "gemm_kmajor: a weight slice beyond 32-bit offsets");
-  const int c = gathered_checks(a_total, a_rows, rows, k);
+  const int c = gathered_checks(a_total, a_rows, a_rows_div, rows, k);
   if (c != MI355X_OK) return c;
   if (rows == 0) return MI355X_OK;
   const int v2 = mi355x_gemm_v2_kmajor_launch(a, a_scale, rows, w, w_scale, experts, n, k, offsets,
-                                              out, stream, a_rows, a_total);
+                                              out, stream, a_rows, a_total, a_rows_div);
   if (v2 < 0) return v2;
   MI355X_REQUIRE(v2 == 0, "gemm_kmajor: shape outside the pipelined kernel");
   return MI355X_OK;
 }
 
 extern "C" int mi355x_gemm_fp8_rowwise_gathered(const uint8_t* a, const float* a_scale,
-                                                int a_total, const int32_t* a_rows, int rows,
+                                                int a_total, const int32_t* a_rows, int a_rows_div, int rows,
                                                 const uint8_t* w, const float* w_scale,
                                                 int experts, int n, int k,
                                                 const int32_t* offsets, void* out, void* stream) {
@@ -530,11 +532,11 @@ extern "C" int mi355x_gemm_fp8_rowwise_gathered(const uint8_t* a, const float* a
                  kMaxExperts);
   MI355X_REQUIRE(n > 0 && n % 256 == 0, "gemm_rowwise: N must be a multiple of 256, got %d", n);
   MI355X_REQUIRE(k > 0 && k % BK == 0, "gemm_rowwise: K must be a multiple of %d, got %d", BK, k);
-  const int c = gathered_checks(a_total, a_rows, rows, k);
+  const int c = gathered_checks(a_total, a_rows, a_rows_div, rows, k);
   if (c != MI355X_OK) return c;
   if (rows == 0) return MI355X_OK;
   const int v2 = mi355x_gemm_v2_rowwise_launch(a, a_scale, rows, w, w_scale, experts, n, k, offsets,
-                                               nullptr, nullptr, 0, out, stream, a_rows, a_total);
+                                               nullptr, nullptr, 0, out, stream, a_rows, a_total, a_rows_div);
   if (v2 < 0) return v2;
   MI355X_REQUIRE(v2 == 0, "gemm_rowwise gathered: shape outside the pipelined kernel");
   return MI355X_OK;

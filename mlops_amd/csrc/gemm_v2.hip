@@ -81,6 +81,16 @@ typedef short v4s __attribute__((ext_vector_type(4)));
 // 128 K rows of 256 bytes and the B fragments read with ds_read_b64_tr_b8;
 // the MFMA columns are then the tile's columns in order, so the epilogue
 // regroups each row's values through LDS into 8-column stores.
+// x / d for the divisor d encoded by row_div_magic (s == 0: d = 1): the
+// round-down multiply-high method for unsigned division by an invariant
+// integer (Granlund and Montgomery, PLDI 1994), with a 33-bit multiplier
+// 2^32 + m, exact for every 32-bit x.
+__device__ __forceinline__ uint32_t div_rows(uint32_t x, uint32_t m, int s) {
+  const uint32_t t = __umulhi(x, m);
+  const uint32_t q = (t + ((x - t) >> 1)) >> (s > 0 ? s - 1 : 0);
+  return s == 0 ? x : q;  // a select: no branch around the LDS reads it feeds
+}
+
 // MFMA block of a K step at which waves 4-7 issue the next step's copies.
 constexpr int kLateIssueBlock = 1;
 
@@ -93,13 +103,17 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     const uint16_t* __restrict__ addend, uint16_t* __restrict__ out,
     uint8_t* __restrict__ act_q, float* __restrict__ act_scales, float limit,
     const uint16_t* __restrict__ lora_z, const uint16_t* __restrict__ lora_b, int lora_rank,
-    int n_group, int rotate, const int32_t* __restrict__ a_rows, int scale_pitch) {
+    int n_group, int rotate, const int32_t* __restrict__ a_rows, int scale_pitch,
+    uint32_t div_m, int div_s) {
   __shared__ __align__(1024) uint8_t smem[kStages * STAGE_BYTES];
   __shared__ float act_amax[2][BM];  // per-row amax of each wave column's 64 act columns
   __shared__ int prefix[kMaxExperts + 1];
   __shared__ int tmp[kThreads];
-  // Gathered A (kGather): GEMM row r reads a[a_rows[r]] and its scales
-  // a_scale[a_rows[r] * (K/128) + kb] (token-major): the activation
+  // Gathered A (kGather): GEMM row r reads a[tok] and its scales
+  // a_scale[tok * (K/128) + kb] (token-major), tok = a_rows[r] / d with the
+  // divisor d given as (div_m, div_s) (row_div_magic): d = top_k turns the
+  // plan's sorted slot order into token rows, d = 1 takes token ids. The
+  // activation
   // quantized once per token, each token row read by its k routed rows. A
   // tile's 256 source rows are copied into one of two tables one tile ahead.
   __shared__ int gtok[2][BM];
@@ -131,7 +145,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     for (int i = 0; i < A_LOADS; ++i) {
       const int r = (wave * A_LOADS + i) * 8 + (lane >> 3);
       int src;
-      if constexpr (kGather) src = gtok[t.par][r];
+      if constexpr (kGather) src = (int)div_rows((uint32_t)gtok[t.par][r], div_m, div_s);
       else src = min(t.row0 + r, rows - 1);
       const uint32_t off = (uint32_t)src * (uint32_t)K + 16 * ((lane & 7) ^ swz(r));
       dma16(abase, off, base + (wave * A_LOADS + i) * 1024);
@@ -167,7 +181,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
       // one line; else K-block-major [K/128][rows].
       const float* sbase = kGather ? a_scale + kb : a_scale + (size_t)kb * rows;
       uint32_t off;
-      if constexpr (kGather) off = 4u * (uint32_t)gtok[t.par][wave * 64 + lane] * (uint32_t)kbw;
+      if constexpr (kGather) off = 4u * div_rows((uint32_t)gtok[t.par][wave * 64 + lane], div_m, div_s) * (uint32_t)kbw;
       else off = 4u * (uint32_t)min(t.row0 + wave * 64 + lane, rows - 1);
       dma4(sbase, off, base + A_BYTES + B_BYTES + wave * 256);
     } else if (wave < 6 && lane < 2) {
@@ -475,7 +489,7 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
             const uint32_t off = (uint32_t)lrow * (uint32_t)N + lane_col;
             if constexpr (kRow) {
               float xs;
-              if constexpr (kGather) xs = a_scale[gtok[ct.par][wm * 64 + lrow]];
+              if constexpr (kGather) xs = a_scale[div_rows((uint32_t)gtok[ct.par][wm * 64 + lrow], div_m, div_s)];
               else xs = a_scale[ct.row0 + wm * 64 + lrow];
 #pragma unroll
               for (int m = 0; m < 8; ++m) v[m] = (v[m] * xs) * wsc[m];
@@ -577,6 +591,20 @@ Order tile_order(int n, int k) {
 }
 }  // namespace
 
+// (m, s) for div_rows: s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1
+// for d >= 2; (0, 0) for d = 1.
+struct RowDiv {
+  uint32_t m;
+  int s;
+};
+RowDiv row_div_magic(int d) {
+  if (d <= 1) return {0u, 0};
+  int s = 0;
+  while ((1 << s) < d) ++s;
+  const uint64_t m = (((uint64_t)1 << 32) * (uint64_t)((1 << s) - d)) / (uint64_t)d + 1;
+  return {(uint32_t)m, s};
+}
+
 // Launches the pipelined kernel; returns 1 if the shape is not its form
 // (N % 256 != 0), in which case the caller uses the general kernel.
 int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, const uint8_t* w,
@@ -584,8 +612,9 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
                           const int32_t* offsets, int interleave, const void* addend, void* out,
                           uint8_t* act_q, float* act_scales, float limit, const void* lora_z,
                           const void* lora_b, int lora_rank, void* stream,
-                          const int32_t* a_rows, int a_total) {
+                          const int32_t* a_rows, int a_total, int a_rows_div) {
   if (n % BN != 0 || experts > kMaxExperts || (interleave && (n / 2) % 128 != 0)) return 1;
+  const RowDiv div = row_div_magic(a_rows_div);
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   const int grid = upper < cu_count() ? upper : cu_count();
   const Order order = tile_order(n, k);
@@ -594,7 +623,7 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
                        rows, w, w_scale, w_scale_t, experts, n, k, offsets, interleave,
                        (const uint16_t*)addend, (uint16_t*)out, act_q, act_scales, limit,
                        (const uint16_t*)lora_z, (const uint16_t*)lora_b, lora_rank,
-                       order.n_group, order.rotate, a_rows, a_rows != nullptr ? a_total : rows);
+                       order.n_group, order.rotate, a_rows, a_rows != nullptr ? a_total : rows, div.m, div.s);
   };
   if (a_rows != nullptr) {
     if (lora_z != nullptr || act_q != nullptr || addend != nullptr) return 1;
@@ -618,8 +647,9 @@ int mi355x_gemm_v2_launch(const uint8_t* a, const float* a_scale, int rows, cons
 int mi355x_gemm_v2_kmajor_launch(const uint8_t* a, const float* a_scale, int rows,
                                  const uint8_t* w, const float* w_scale, int experts, int n, int k,
                                  const int32_t* offsets, void* out, void* stream,
-                                 const int32_t* a_rows, int a_total) {
+                                 const int32_t* a_rows, int a_total, int a_rows_div) {
   if (n % BN != 0 || experts > kMaxExperts) return 1;
+  const RowDiv div = row_div_magic(a_rows_div);
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   const int grid = upper < cu_count() ? upper : cu_count();
   const Order order = tile_order(n, k);
@@ -628,7 +658,7 @@ int mi355x_gemm_v2_kmajor_launch(const uint8_t* a, const float* a_scale, int row
                        rows, w, w_scale, 1, experts, n, k, offsets, 0, (const uint16_t*)nullptr,
                        (uint16_t*)out, (uint8_t*)nullptr, (float*)nullptr, 0.0f,
                        (const uint16_t*)nullptr, (const uint16_t*)nullptr, 0, order.n_group,
-                       order.rotate, a_rows, a_rows != nullptr ? a_total : rows);
+                       order.rotate, a_rows, a_rows != nullptr ? a_total : rows, div.m, div.s);
   };
   if (a_rows != nullptr) launch(grouped_gemm_v2_kernel<false, false, false, false, true, true>);
   else launch(grouped_gemm_v2_kernel<false, false, false, false, true>);
@@ -642,8 +672,9 @@ int mi355x_gemm_v2_rowwise_launch(const uint8_t* a, const float* a_scale, int ro
                                   const uint8_t* w, const float* w_scale, int experts, int n,
                                   int k, const int32_t* offsets, const void* lora_z,
                                   const void* lora_b, int lora_rank, void* out, void* stream,
-                                  const int32_t* a_rows, int a_total) {
+                                  const int32_t* a_rows, int a_total, int a_rows_div) {
   if (n % BN != 0 || experts > kMaxExperts) return 1;
+  const RowDiv div = row_div_magic(a_rows_div);
   const int upper = ((rows + BM - 1) / BM + experts) * (n / BN);
   const int grid = upper < cu_count() ? upper : cu_count();
   const Order order = tile_order(n, k);
@@ -652,7 +683,7 @@ int mi355x_gemm_v2_rowwise_launch(const uint8_t* a, const float* a_scale, int ro
                        rows, w, w_scale, 0, experts, n, k, offsets, 0, (const uint16_t*)nullptr,
                        (uint16_t*)out, (uint8_t*)nullptr, (float*)nullptr, 0.0f,
                        (const uint16_t*)lora_z, (const uint16_t*)lora_b, lora_rank,
-                       order.n_group, order.rotate, a_rows, a_rows != nullptr ? a_total : rows);
+                       order.n_group, order.rotate, a_rows, a_rows != nullptr ? a_total : rows, div.m, div.s);
   };
   if (a_rows != nullptr) {
     if (lora_z != nullptr) return 1;  // not a form of this kernel

@@ -660,10 +660,12 @@ def quantize_token_rows(x: torch.Tensor):
     return q, scales
 
 
-def gemm_gathered(a, a_scale, a_rows, w, w_scale, offsets, *, interleave=False, kmajor=False):
+def gemm_gathered(a, a_scale, a_rows, w, w_scale, offsets, *, interleave=False, kmajor=False,
+                  rows_div=1):
     """:func:`gemm` (``kmajor=False``, ``w [E, N, K]`` with scales ``[E, N/128,
     K/128]``) or :func:`gemm_kmajor` (``w [E, K, N]``) whose GEMM row r is row
-    ``a_rows[r]`` of ``a [T, K]``, token-major scales ``a_scale [T, K/128]``
+    ``a_rows[r] // rows_div`` of ``a [T, K]`` (``rows_div = top_k`` reads the
+    plan's sorted slot order directly), token-major scales ``a_scale [T, K/128]``
     (:func:`quantize_token_rows`): the
     activation quantized once per token and read by each of its routed rows
     (``mi355x_gemm_fp8_block_gathered`` / ``_kmajor_gathered``). Bitwise the
@@ -689,12 +691,12 @@ def gemm_gathered(a, a_scale, a_rows, w, w_scale, offsets, *, interleave=False, 
     if kmajor:
         _timed("gemm_fp8_block", device, 2 * rows * n * k, rows * k + experts * n * k + 2 * rows * n,
                "mi355x_gemm_fp8_block_kmajor_gathered", _ptr(a), _ptr(a_scale), tokens,
-               _ptr(a_rows), rows, _ptr(w), _ptr(w_scale), experts, n, k, _ptr(offsets),
+               _ptr(a_rows), int(rows_div), rows, _ptr(w), _ptr(w_scale), experts, n, k, _ptr(offsets),
                _ptr(out), _stream(device))
     else:
         _timed("gemm_fp8_block", device, 2 * rows * n * k, rows * k + experts * n * k + 2 * rows * n,
                "mi355x_gemm_fp8_block_gathered", _ptr(a), _ptr(a_scale), tokens, _ptr(a_rows),
-               rows, _ptr(w), _ptr(w_scale), experts, n, k, _ptr(offsets), int(interleave),
+               int(rows_div), rows, _ptr(w), _ptr(w_scale), experts, n, k, _ptr(offsets), int(interleave),
                _ptr(out), _stream(device))
     return out
 
@@ -929,8 +931,8 @@ def gemm_rowwise(a, a_scale, w, w_scale, offsets, *, lora=None):
     return out
 
 
-def gemm_rowwise_gathered(a, a_scale, a_rows, w, w_scale, offsets):
-    """:func:`gemm_rowwise` whose row r is row ``a_rows[r]`` of per-token
+def gemm_rowwise_gathered(a, a_scale, a_rows, w, w_scale, offsets, *, rows_div=1):
+    """:func:`gemm_rowwise` whose row r is row ``a_rows[r] // rows_div`` of per-token
     ``a [T, K]`` with descales ``a_scale [T]`` (:func:`quantize_rows_current`
     on the token rows; ``mi355x_gemm_fp8_rowwise_gathered``). Bitwise the
     same as on the permuted copy."""
@@ -947,7 +949,8 @@ def gemm_rowwise_gathered(a, a_scale, a_rows, w, w_scale, offsets):
     out = torch.empty((rows, n), dtype=torch.bfloat16, device=device)
     _timed(
         "gemm_fp8_rowwise", device, 2 * rows * n * k, rows * k + experts * n * k + 2 * rows * n,
-        "mi355x_gemm_fp8_rowwise_gathered", _ptr(a), _ptr(a_scale), tokens, _ptr(a_rows), rows,
+        "mi355x_gemm_fp8_rowwise_gathered", _ptr(a), _ptr(a_scale), tokens, _ptr(a_rows),
+        int(rows_div), rows,
         _ptr(w), _ptr(w_scale), experts, n, k, _ptr(offsets), _ptr(out), _stream(device),
     )
     return out

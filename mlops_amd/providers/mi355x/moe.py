@@ -354,9 +354,9 @@ def routed_rows_gemm(x, slots, order, top_k, weight, offsets, *, interleave=Fals
     kmajor = input_gradient and len(weight) == 2
     if top_k >= GATHER_MIN_TOP_K and n % 256 == 0 and (kmajor or not input_gradient):
         tq, ts = kernels.quantize_token_rows(x)
-        a_rows = torch.div(order, top_k, rounding_mode="floor")
-        return kernels.gemm_gathered(tq, ts, a_rows, data, scale, offsets, interleave=interleave,
-                                     kmajor=kmajor)
+        # Routed row r reads token order[r] // top_k, divided in the kernel.
+        return kernels.gemm_gathered(tq, ts, order, data, scale, offsets, interleave=interleave,
+                                     kmajor=kmajor, rows_div=top_k)
     xq, xs = kernels.permute_quantize(x, slots)
     if input_gradient:
         return input_gradient_gemm(xq, xs, weight, offsets)

@@ -127,8 +127,9 @@ def _routed_rows_gemm(x, slots, order, top_k, data, scale, offsets):
     Bitwise the same either way."""
     if top_k >= fused.GATHER_MIN_TOP_K and data.shape[1] % 256 == 0:
         tq, ts = kernels.quantize_rows_current(x)
-        a_rows = torch.div(order, top_k, rounding_mode="floor")
-        return kernels.gemm_rowwise_gathered(tq, ts, a_rows, data, scale, offsets)
+        # Routed row r reads token order[r] // top_k, divided in the kernel.
+        return kernels.gemm_rowwise_gathered(tq, ts, order, data, scale, offsets,
+                                             rows_div=top_k)
     xq, xs = kernels.permute_quantize_current(x, slots)
     return kernels.gemm_rowwise(xq, xs, data, scale, offsets)
 

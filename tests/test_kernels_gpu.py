@@ -390,12 +390,17 @@ def test_grouped_gemm_gathered_matches_permuted_copy(device, tokens, top_k, expe
         wq, ws = K.quantize_weight_blocks(wk)
         want = K.gemm_kmajor(xq, xs, wq, ws, offsets)
         got = K.gemm_gathered(tq, ts, a_rows, wq, ws, offsets, kmajor=True)
+        # The plan's slot order itself, divided by top_k in the kernel.
+        got_slots = K.gemm_gathered(tq, ts, order, wq, ws, offsets, kmajor=True, rows_div=top_k)
     else:
         wq, ws = K.quantize_weight_blocks(w)
         inter = form == "up"
         want = K.gemm(xq, xs, wq, ws, offsets, interleave=inter)
         got = K.gemm_gathered(tq, ts, a_rows, wq, ws, offsets, interleave=inter)
+        got_slots = K.gemm_gathered(tq, ts, order, wq, ws, offsets, interleave=inter,
+                                    rows_div=top_k)
     assert torch.equal(got.cpu(), want.cpu())
+    assert torch.equal(got_slots.cpu(), want.cpu())
 
 
 @pytest.mark.parametrize("form", ["up", "kmajor"])
@@ -459,6 +464,8 @@ def test_rowwise_gemm_gathered_matches_permuted_copy(device, tokens, top_k, expe
     want = K.gemm_rowwise(xq, xs, wq, wsc, offsets)
     got = K.gemm_rowwise_gathered(tq, ts, a_rows, wq, wsc, offsets)
     assert torch.equal(got.cpu(), want.cpu())
+    got_slots = K.gemm_rowwise_gathered(tq, ts, order, wq, wsc, offsets, rows_div=top_k)
+    assert torch.equal(got_slots.cpu(), want.cpu())
 
 
 @pytest.mark.parametrize("counts,k,n", [
