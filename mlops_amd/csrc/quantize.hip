@@ -661,6 +661,8 @@ __device__ __forceinline__ void swiglu_bwd_block(
 }
 
 
+// Four waves per SIMD (at most 128 registers): the two bodies below would
+// otherwise be allocated 144, and the LDS already limits a CU to two blocks.
 template <bool kClamp>
 __global__ void __launch_bounds__(kSbThreads) __attribute__((amdgpu_waves_per_eu(4)))
 swiglu_bwd_quantize_kernel(
