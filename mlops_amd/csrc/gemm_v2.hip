@@ -135,7 +135,18 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
   };
 
   // Direct loads of one K step of tile t into stage `stage`.
+  const int issue_lane = lane;
   auto issue = [&](const Tile& t, int step, int stage) {
+    // The fused-SwiGLU form has no registers to keep the per-lane copy
+    // offsets across the K loop: the compiler spilled them, and each scratch
+    // reload waited on vmcnt, i.e. on the copies in flight. There the lane id
+    // passes through an empty asm so the offsets are recomputed at each issue.
+    int lane = issue_lane;
+    if constexpr (kAct) {
+      uint32_t l = (uint32_t)lane;
+      asm volatile("" : "+v"(l));
+      lane = (int)l;
+    }
     const int kb = __builtin_amdgcn_readfirstlane(step + t.rot < nk ? step + t.rot : step + t.rot - nk);
     uint8_t* base = smem + stage * STAGE_BYTES;
     const size_t koff = (size_t)kb * BK;
@@ -448,29 +459,32 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
     // in this wave; the 128-column group spans both wave columns (wn), whose
     // row maxima meet in LDS.
     constexpr bool act_out = kAct;  // act_q != nullptr
-    // Two halves of the wave's rows (i = 0-1, then 2-3), each: store h and
-    // keep the activations, exchange row maxima, quantize and store act.
+    // Row groups of the wave (kParts of them), each: store h and keep the
+    // activations, exchange row maxima, quantize and store act. With the
+    // activations one 16-row block at a time (four exchanges) the epilogue
+    // fits the registers; two blocks at a time spilled inside the K loop.
+    constexpr int kParts = act_out ? 4 : 2, kPer = 4 / kParts;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      float act[2][4][4];
+    for (int half = 0; half < kParts; ++half) {
+      float act[kPer][4][4];
       // The addend's 8 rows of this half, loaded before its first store:
       // loads and stores share one completion counter, so a load issued
       // after a store would wait for that store too.
-      uint4 cadd[2][4];
+      uint4 cadd[kPer][4];
       if (kAdd) {
 #pragma unroll
-        for (int ii = 0; ii < 2; ++ii)
+        for (int ii = 0; ii < kPer; ++ii)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int lrow = (half * 2 + ii) * 16 + 4 * (elane >> 4) + r;
+            const int lrow = (half * kPer + ii) * 16 + 4 * (elane >> 4) + r;
             cadd[ii][r] = make_uint4(0, 0, 0, 0);
             if (wm * 64 + lrow < ct.nvalid)
               cadd[ii][r] = *(const uint4*)(cbase + (uint32_t)lrow * (uint32_t)N + lane_col);
           }
       }
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii) {
-        const int i = half * 2 + ii;
+      for (int ii = 0; ii < kPer; ++ii) {
+        const int i = half * kPer + ii;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int lrow = i * 16 + 4 * (elane >> 4) + r;  // row within the wave's 64
@@ -529,10 +543,10 @@ __global__ void __launch_bounds__(kThreads, 2) grouped_gemm_v2_kernel(
         lds_sync();
         const int half_w = N / 2;
 #pragma unroll
-        for (int ii = 0; ii < 2; ++ii) {
+        for (int ii = 0; ii < kPer; ++ii) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int trow = wm * 64 + (half * 2 + ii) * 16 + 4 * (elane >> 4) + r;
+            const int trow = wm * 64 + (half * kPer + ii) * 16 + 4 * (elane >> 4) + r;
             if (trow < ct.nvalid) {
               const float amax = fmaxf(act_amax[0][trow], act_amax[1][trow]);
               const float sc = fmaxf(amax * kInv448, kMinScale);
