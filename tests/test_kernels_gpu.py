@@ -368,6 +368,7 @@ def test_grouped_gemm_matches_fp64(device, case):
     (777, 2, 5, 1024, 768, "kmajor"),        # input gradient through a K-major weight
     (16384, 8, 128, 2048, 1536, "up"),       # C3's up projection
     (16384, 8, 128, 2048, 768, "kmajor"),    # C3's input gradient through W2
+    (600, 16, 64, 256, 512, "up"),           # top-16: slot order / 16 in the kernel
 ])
 def test_grouped_gemm_gathered_matches_permuted_copy(device, tokens, top_k, experts, k, n, form):
     """Token rows quantized once and read through the routed rows' tokens
